@@ -1,0 +1,236 @@
+// extern "C" shim over the genuine reference engine's CPU path, compiled
+// from /root/reference by oracle/ref.mk into oracle/_ref/libgai_ref.so.
+// TEST INFRASTRUCTURE ONLY: tests/golden/make_golden.py loads it in this
+// container to write golden fixtures. It never travels to the GPU box in a
+// form anything loads there (the fixtures do), and the product never links it.
+//
+// The Generator's per-token host path is private in the reference; the shim
+// reaches it by opening the class (test code only), so the greedy loop below
+// is the reference's own prefill + decode_step + greedy argmax
+// (inference/generator.cpp:917-1098 with the greedy branch of
+// inference/sampler.cpp:129-141).
+#include "core/ops.h"
+#include "core/ops_cpu.h"
+#include "core/rng.h"
+#include "core/dtype.h"
+#include "quantization/quantize.h"
+#include "model/model.h"
+#define private public
+#include "inference/generator.h"
+#undef private
+
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace gai;
+
+extern "C" {
+
+void ref_f32_to_f16(const float* s, u16* d, i64 n) { for (i64 i = 0; i < n; ++i) d[i] = fp32_to_fp16(s[i]); }
+void ref_f16_to_f32(const u16* s, float* d, i64 n) { for (i64 i = 0; i < n; ++i) d[i] = fp16_to_fp32(s[i]); }
+void ref_f32_to_bf16(const float* s, u16* d, i64 n) { for (i64 i = 0; i < n; ++i) d[i] = fp32_to_bf16(s[i]); }
+
+void ref_rng_normal(u64 seed, float mean, float sd, float* out, i64 n) {
+    Rng r(seed);
+    for (i64 i = 0; i < n; ++i) out[i] = r.normal(mean, sd);
+}
+void ref_rng_uniform(u64 seed, float lo, float hi, float* out, i64 n) {
+    Rng r(seed);
+    for (i64 i = 0; i < n; ++i) out[i] = r.uniform(lo, hi);
+}
+void ref_rng_below(u64 seed, u64 bound, i32* out, i64 n) {
+    Rng r(seed);
+    for (i64 i = 0; i < n; ++i) out[i] = (i32)r.below(bound);
+}
+
+int ref_quantize(int kind, const float* src, void* dst, i64 n) {
+    try {
+        if (kind == 0) quant::quantize_q4_0(src, dst, n);
+        else if (kind == 1) quant::quantize_q4_1(src, dst, n);
+        else if (kind == 2) quant::quantize_q8_0(src, dst, n);
+        else return -1;
+    } catch (...) { return -2; }
+    return 0;
+}
+int ref_dequantize(int kind, const void* src, float* dst, i64 n) {
+    try {
+        if (kind == 0) quant::dequantize_q4_0(src, dst, n);
+        else if (kind == 1) quant::dequantize_q4_1(src, dst, n);
+        else if (kind == 2) quant::dequantize_q8_0(src, dst, n);
+        else return -1;
+    } catch (...) { return -2; }
+    return 0;
+}
+int ref_quant_materialize(int kind, const void* packed, u16* out, i64 n) {
+    try {
+        const u16* p = ops::quant_materialize(Device::CPU, packed, kind, n, 0);
+        std::memcpy(out, p, (size_t)n * 2);
+    } catch (...) { return -2; }
+    return 0;
+}
+int ref_linear_forward_q4(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    try { ops::linear_forward_q4(Device::CPU, x, w, y, M, K, N, kind); } catch (...) { return -2; }
+    return 0;
+}
+void ref_linear_forward_fp16(const float* x, const u16* w, float* y, int M, int K, int N) {
+    ops::linear_forward_fp16(Device::CPU, x, w, y, M, K, N);
+}
+void ref_linear_forward_f32(const float* x, const float* w, float* y, int M, int K, int N) {
+    ops::linear_forward(Device::CPU, x, w, y, M, K, N);
+}
+void ref_rmsnorm_forward(const float* x, const float* w, float* out, float* rrms, i64 rows, int dim, float eps) {
+    ops::rmsnorm_forward(Device::CPU, x, w, out, rrms, rows, dim, eps);
+}
+void ref_swiglu_forward(const float* g, const float* u, float* out, i64 n) {
+    ops::swiglu_forward(Device::CPU, g, u, out, n);
+}
+void ref_softmax_row(float* x, int n) { cpu::softmax_row(x, n); }
+i32 ref_argmax_token(const float* l, int V) { return ops::argmax_token(Device::CPU, l, V); }
+void ref_embedding_forward_half(const i32* ids, const u16* table, float* out, i64 ntok, int dim, int vocab) {
+    ops::embedding_forward_half(Device::CPU, ids, table, out, ntok, dim, vocab);
+}
+void ref_attention_forward_ex(const float* q, const float* k, const float* v, float* out, int B, int T, int H,
+                              int KV, int hd, float scale, int window) {
+    ops::attention_forward_ex(Device::CPU, q, k, v, out, nullptr, B, T, H, KV, hd, scale, window, nullptr);
+}
+int ref_attention_decode_ring_fp16(const float* q, const u16* kc, const u16* vc, float* out, int H, int KV, int hd,
+                                   int ring_start, int pinned, int cur_len, int cache_max, float scale,
+                                   int window) {
+    std::vector<float> scratch((size_t)H * (size_t)(cur_len > 0 ? cur_len : 1));
+    try {
+        ops::attention_decode_ring_fp16(Device::CPU, q, kc, vc, out, H, KV, hd, ring_start, pinned, cur_len,
+                                        cache_max, scale, scratch.data(), window);
+    } catch (...) { return -2; }
+    return 0;
+}
+int ref_mamba2_forward_half(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
+                            const float* dt_bias, const float* a_log, const float* D, const float* norm_w,
+                            const void* w_out, float* state, float* out, int B, int T, int d, int d_inner,
+                            int conv_dim, int n_heads, int d_head, int d_state, int k, float eps, int qkind) {
+    try {
+        ops::mamba2_forward_half(Device::CPU, x, (const u16*)w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w,
+                                 (const u16*)w_out, state, out, B, T, d, d_inner, conv_dim, n_heads, d_head,
+                                 d_state, k, eps, qkind);
+    } catch (...) { return -2; }
+    return 0;
+}
+int ref_moe_forward_bias_half(const float* x, const float* rw, const float* bias, const void* g, const void* u,
+                              const void* dn, const void* sg, const void* su, const void* sd, float* out,
+                              float* probs, i32* idx, float* w, i64 N, int d, int E, int ne, int K, int SH,
+                              int qkind) {
+    std::vector<float> s_gate((size_t)N * K * E), s_up(s_gate.size()), s_act(s_gate.size());
+    try {
+        ops::moe_forward_bias_half(Device::CPU, x, rw, bias, (const u16*)g, (const u16*)u, (const u16*)dn,
+                                   (const u16*)sg, (const u16*)su, (const u16*)sd, out, probs, idx, w,
+                                   s_gate.data(), s_up.data(), s_act.data(), N, d, E, ne, K, SH, qkind);
+    } catch (...) { return -2; }
+    return 0;
+}
+
+// Tiny Granite-hybrid greedy run through the reference Model + Generator.
+// cfg / fcfg use the same layout as orc_granite_generate (oracle/oracle.h).
+// Parameters are set by name from caller buffers holding the storage bytes
+// (Q-kind blocks for matrices, fp16 for tok_embeddings, fp32 for vectors).
+int ref_granite_generate(const i32* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
+                         const i32* prompt, int P, int n_new, int max_ctx, i32* out_ids, float* out_margins) {
+    try {
+        ModelConfig c;
+        c.arch = ModelConfig::ArchGranite;
+        c.vocab_size = cfg[0];
+        c.hidden_size = cfg[1];
+        c.num_layers = cfg[2];
+        c.num_heads = cfg[3];
+        c.num_kv_heads = cfg[4];
+        c.head_dim_override = cfg[5];
+        c.moe_expert_dim = cfg[6];
+        c.num_experts = cfg[7];
+        c.moe_top_k = cfg[8];
+        c.shared_expert_intermediate_size = cfg[9];
+        c.use_moe = true;
+        c.moe_shared = true;
+        c.mamba_expand = cfg[10] / cfg[1];
+        c.mamba_n_heads = cfg[11];
+        c.mamba_d_head = cfg[12];
+        c.mamba_d_state = cfg[13];
+        c.mamba_n_groups = 1;
+        c.mamba_d_conv = cfg[14];
+        c.layer_types.assign(cfg + 16, cfg + 16 + cfg[2]);
+        c.position_embedding = 1;  // NoPE
+        c.rms_eps = fcfg[0];
+        c.attention_multiplier = fcfg[1];
+        c.intermediate_size = cfg[6];
+        c.max_seq_len = max_ctx;
+        c.tie_embeddings = true;
+        const int qkind = cfg[15];
+        Model m(c, Device::CPU, false, qkind);
+        std::map<std::string, const void*> pm;
+        for (int i = 0; i < nparams; ++i) pm[names[i]] = ptrs[i];
+        for (Parameter* p : m.parameters()) {
+            auto it = pm.find(p->name);
+            if (it == pm.end()) return -3;
+            std::memcpy(p->w.data_ptr(), it->second, p->w.nbytes());
+        }
+        ops::set_fused_q4(true);
+        Tokenizer tok;
+        Generator g(m, tok, max_ctx);
+        std::vector<i32> pr(prompt, prompt + P);
+        g.prefill(pr);
+        const int V = c.vocab_size;
+        for (int step = 0; step < n_new; ++step) {
+            const float* lg = g.logits_host_.data();
+            const i32 next = ops::argmax_token(Device::CPU, lg, V);
+            float best = -std::numeric_limits<float>::infinity(), second = best;
+            for (int i = 0; i < V; ++i) {
+                if (!std::isfinite(lg[i])) continue;
+                if (lg[i] > best) { second = best; best = lg[i]; }
+                else if (lg[i] > second) second = lg[i];
+            }
+            out_ids[step] = next;
+            out_margins[step] = best - second;
+            if (step == n_new - 1) break;
+            g.push_history(next);
+            g.decode_step(next, (int)g.absolute_pos_);
+            ++g.absolute_pos_;
+        }
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_granite_generate: %s\n", e.what());
+        return -2;
+    }
+    return 0;
+}
+
+// The parameter table the reference Model allocates for a config: names,
+// element counts and storage dtypes (core/dtype.h:9-21 numbering), so the
+// fixture writer fills exactly the tensors the reference expects.
+int ref_granite_param_table(const i32* cfg, const float* fcfg, int max_ctx, char* names_out, int names_cap,
+                            i64* numel_out, i32* dtype_out, int cap) {
+    ModelConfig c;
+    c.arch = ModelConfig::ArchGranite;
+    c.vocab_size = cfg[0]; c.hidden_size = cfg[1]; c.num_layers = cfg[2]; c.num_heads = cfg[3];
+    c.num_kv_heads = cfg[4]; c.head_dim_override = cfg[5]; c.moe_expert_dim = cfg[6]; c.num_experts = cfg[7];
+    c.moe_top_k = cfg[8]; c.shared_expert_intermediate_size = cfg[9]; c.use_moe = true; c.moe_shared = true;
+    c.mamba_expand = cfg[10] / cfg[1]; c.mamba_n_heads = cfg[11]; c.mamba_d_head = cfg[12];
+    c.mamba_d_state = cfg[13]; c.mamba_n_groups = 1; c.mamba_d_conv = cfg[14];
+    c.layer_types.assign(cfg + 16, cfg + 16 + cfg[2]); c.position_embedding = 1; c.rms_eps = fcfg[0];
+    c.attention_multiplier = fcfg[1]; c.intermediate_size = cfg[6]; c.max_seq_len = max_ctx;
+    c.tie_embeddings = true;
+    Model m(c, Device::CPU, false, cfg[15]);
+    int i = 0, off = 0;
+    for (Parameter* p : m.parameters()) {
+        if (i >= cap) return -1;
+        const int l = (int)p->name.size() + 1;
+        if (off + l > names_cap) return -1;
+        std::memcpy(names_out + off, p->name.c_str(), (size_t)l);
+        off += l;
+        numel_out[i] = p->w.numel();
+        dtype_out[i] = (i32)p->w.dtype();
+        ++i;
+    }
+    return i;
+}
+
+}  // extern "C"
