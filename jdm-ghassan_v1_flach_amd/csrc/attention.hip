@@ -1,0 +1,515 @@
+// GQA attention over the KV cache.
+//
+// Decode (one query token per sequence), split-K "flash decoding":
+// a block owns one kv head and a contiguous run of logical positions, reads
+// each K and V row ONCE for all `group` query heads of that kv head (the
+// reference re-reads them per q head, cuda/attention.cu:621-810), keeps the
+// scores of its run in LDS, and writes (max, sum, unnormalised o) partials
+// that a small combine kernel merges. Lanes are laid out as positions x
+// 16-byte channel groups, so one wave load instruction reads whole K/V rows
+// contiguously. The same kernel serves the reference's fp16 ring cache
+// (core/attn_cpu.cpp:151-254: pinned prefix + rolling ring) and the paged
+// bf16 ragged-batch extension (page table per sequence).
+//
+// Prefill (attention_forward_ex, core/attn_cpu.cpp:29-94): causal flash
+// attention on the matrix cores. A block is one q head x 128 queries, each
+// wave 32 queries; per 64-key tile S^T = K Q^T (v_mfma_f32_32x32x16_bf16),
+// online softmax in registers, O += P V with P taken straight from the S^T
+// accumulator layout (no LDS round trip) and V staged transposed in LDS.
+#include "gh_common.h"
+
+namespace gh {
+
+// ============================================================== decode
+struct DecodeArgs {
+    const float* q;           // [S][H][hd]
+    const uint16_t* k;        // ring: [cache_max][KV][hd]  paged: [pages][page_size][KV][hd]
+    const uint16_t* v;
+    float* o_part;            // [S][KV][splits][G][hd]
+    float* ml_part;           // [S][KV][splits][G][2]
+    int H, KV, G, splits, chunk;
+    float scale;
+    // ring
+    int ring_start, pinned, cur_len, cache_max, j0;
+    // paged
+    const int32_t* page_table;
+    const int32_t* seq_lens;
+    int max_pages, page_size;
+};
+
+template <bool BF16>
+__device__ __forceinline__ void widen8(const uint4 r, float* f) {
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (BF16) {
+            f[2 * i] = bf16_to_f32((uint16_t)(u[i] & 0xFFFF));
+            f[2 * i + 1] = bf16_to_f32((uint16_t)(u[i] >> 16));
+        } else {
+            f[2 * i] = f16_to_f32((uint16_t)(u[i] & 0xFFFF));
+            f[2 * i + 1] = f16_to_f32((uint16_t)(u[i] >> 16));
+        }
+    }
+}
+
+constexpr int DEC_CHUNK_MAX = 512, DEC_GMAX = 8;
+
+template <int HD, bool PAGED>
+__global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
+    constexpr int LPP = HD / 8;     // lanes per position (16 B each)
+    constexpr int PPS = 64 / LPP;   // positions per wave step
+    __shared__ float sc[DEC_GMAX][DEC_CHUNK_MAX];
+    __shared__ float sm[DEC_GMAX], sl[DEC_GMAX];
+    __shared__ float red[4][DEC_GMAX][HD];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LPP, cg = lane % LPP;
+    const int G = a.G;
+
+    int jb, je;  // logical positions [jb, je) of this block
+    if (PAGED) {
+        const int L = a.seq_lens[seq];
+        jb = split * a.chunk;
+        je = min(L, jb + a.chunk);
+    } else {
+        jb = a.j0 + split * a.chunk;
+        je = min(a.cur_len, jb + a.chunk);
+    }
+    const int n = je - jb;
+    const size_t part = ((size_t)seq * a.KV + kvh) * a.splits + split;
+    if (n <= 0) {
+        if (threadIdx.x < G) {
+            a.ml_part[(part * G + threadIdx.x) * 2] = -INFINITY;
+            a.ml_part[(part * G + threadIdx.x) * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    const int ring_cap = a.cache_max - a.pinned;
+    auto row_of = [&](int j) -> size_t {  // element offset of row (position j, kvh)
+        size_t slot;
+        if (PAGED) {
+            const int page = a.page_table[(size_t)seq * a.max_pages + j / a.page_size];
+            slot = (size_t)page * a.page_size + j % a.page_size;
+        } else {
+            slot = j < a.pinned ? (size_t)j
+                                : (size_t)a.pinned + (size_t)((a.ring_start + (j - a.pinned)) % (ring_cap > 0 ? ring_cap : 1));
+        }
+        return (slot * a.KV + kvh) * HD;
+    };
+
+    float qr[DEC_GMAX][8];
+    const float* qb = a.q + ((size_t)seq * a.H + (size_t)kvh * G) * HD + cg * 8;
+#pragma unroll
+    for (int g = 0; g < DEC_GMAX; ++g) {
+        if (g < G) {
+            const float4 x0 = *(const float4*)(qb + (size_t)g * HD), x1 = *(const float4*)(qb + (size_t)g * HD + 4);
+            qr[g][0] = x0.x; qr[g][1] = x0.y; qr[g][2] = x0.z; qr[g][3] = x0.w;
+            qr[g][4] = x1.x; qr[g][5] = x1.y; qr[g][6] = x1.z; qr[g][7] = x1.w;
+        }
+    }
+    // ---- scores
+    for (int base = wave * PPS; base < n; base += 4 * PPS) {
+        const int p = base + sub;
+        const bool ok = p < n;
+        float kf[8];
+        if (ok) {
+            const uint4 r = *(const uint4*)(a.k + row_of(jb + p) + cg * 8);
+            widen8<PAGED>(r, kf);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] = 0.f;
+        }
+#pragma unroll
+        for (int g = 0; g < DEC_GMAX; ++g) {
+            if (g >= G) break;
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = fmaf(qr[g][i], kf[i], s);
+#pragma unroll
+            for (int o = LPP >> 1; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+            if (ok && cg == 0) sc[g][p] = s * a.scale;
+        }
+    }
+    __syncthreads();
+    // ---- softmax statistics of this run (one wave per head)
+    for (int g = wave; g < G; g += 4) {
+        float m = -INFINITY;
+        for (int p = lane; p < n; p += 64) m = fmaxf(m, sc[g][p]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int p = lane; p < n; p += 64) {
+            const float e = expf(sc[g][p] - m);
+            sc[g][p] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            sm[g] = m;
+            sl[g] = l;
+        }
+    }
+    __syncthreads();
+    // ---- o = sum p v over the run
+    float acc[DEC_GMAX][8];
+#pragma unroll
+    for (int g = 0; g < DEC_GMAX; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    for (int base = wave * PPS; base < n; base += 4 * PPS) {
+        const int p = base + sub;
+        if (p < n) {
+            float vf[8];
+            const uint4 r = *(const uint4*)(a.v + row_of(jb + p) + cg * 8);
+            widen8<PAGED>(r, vf);
+#pragma unroll
+            for (int g = 0; g < DEC_GMAX; ++g) {
+                if (g >= G) break;
+                const float w = sc[g][p];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(w, vf[i], acc[g][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < DEC_GMAX; ++g) {
+        if (g >= G) break;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float v = acc[g][i];
+#pragma unroll
+            for (int o = LPP; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+            if (sub == 0) red[wave][g][cg * 8 + i] = v;
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * HD; e += 256) {
+        const int g = e / HD, c = e % HD;
+        a.o_part[(part * G + g) * HD + c] = red[0][g][c] + red[1][g][c] + red[2][g][c] + red[3][g][c];
+    }
+    if (threadIdx.x < G) {
+        a.ml_part[(part * G + threadIdx.x) * 2] = sm[threadIdx.x];
+        a.ml_part[(part * G + threadIdx.x) * 2 + 1] = sl[threadIdx.x];
+    }
+}
+
+// Merge the split partials: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
+// An empty context (no positions) gives zeros (core/attn_cpu.cpp:244-246).
+__global__ void k_attn_combine(const float* __restrict__ o_part, const float* __restrict__ ml, float* __restrict__ out,
+                               int H, int KV, int G, int splits, int hd) {
+    const int h = blockIdx.x, seq = blockIdx.y;
+    const int kvh = h / G, g = h % G;
+    const size_t base = ((size_t)seq * KV + kvh) * splits;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) {
+        const float* p = ml + ((base + s) * G + g) * 2;
+        if (p[1] > 0.f) M = fmaxf(M, p[0]);
+    }
+    float L = 0.f;
+    for (int s = 0; s < splits; ++s) {
+        const float* p = ml + ((base + s) * G + g) * 2;
+        if (p[1] > 0.f) L += expf(p[0] - M) * p[1];
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.0f;
+    for (int c = threadIdx.x; c < hd; c += blockDim.x) {
+        float acc = 0.f;
+        for (int s = 0; s < splits; ++s) {
+            const float* p = ml + ((base + s) * G + g) * 2;
+            if (p[1] > 0.f) acc += expf(p[0] - M) * o_part[((base + s) * G + g) * hd + c];
+        }
+        out[((size_t)seq * H + h) * hd + c] = acc * inv;
+    }
+}
+
+static int pick_chunk(int len, int blocks_other) {
+    // enough blocks to fill the chip, runs of 64..512 positions
+    const int target = 4 * num_cus();
+    int per = cdiv(target, blocks_other > 0 ? blocks_other : 1);
+    int chunk = cdiv(len > 0 ? len : 1, per > 0 ? per : 1);
+    chunk = (chunk + 63) / 64 * 64;
+    if (chunk < 64) chunk = 64;
+    if (chunk > DEC_CHUNK_MAX) chunk = DEC_CHUNK_MAX;
+    return chunk;
+}
+
+template <bool PAGED>
+static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
+    a.chunk = pick_chunk(span, a.KV * S);
+    a.splits = cdiv(span > 0 ? span : 1, a.chunk);
+    float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
+    float* ml = (float*)workspace(WS_ATTN_ML, (size_t)S * a.KV * a.splits * a.G * 2 * 4);
+    if (!o || !ml) return fail(GH_ENOMEM, "attention decode: workspace");
+    a.o_part = o;
+    a.ml_part = ml;
+    const dim3 grid(a.splits, a.KV, S);
+    switch (hd) {
+        case 16: hipLaunchKernelGGL((k_attn_decode<16, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 32: hipLaunchKernelGGL((k_attn_decode<32, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 64: hipLaunchKernelGGL((k_attn_decode<64, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 128: hipLaunchKernelGGL((k_attn_decode<128, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        default: return fail(GH_EUNSUPPORTED, "attention decode: head_dim %d (supported: 16, 32, 64, 128)", hd);
+    }
+    GH_LAUNCHED("k_attn_decode");
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.H, S), dim3(hd < 256 ? hd : 256), 0, stream(), o, ml, out, a.H, a.KV,
+                       a.G, a.splits, hd);
+    GH_LAUNCHED("k_attn_combine");
+    return GH_OK;
+}
+
+// ============================================================== prefill
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int PF_BQ = 128, PF_BK = 64;
+
+// q/k/v/out fp32, [B][T][H|KV][HD]
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, float* __restrict__ out,
+                                                           int T, int H, int KV, float scale, int window) {
+    constexpr int KS = HD + 8;  // LDS row stride of K (bf16)
+    constexpr int VS = PF_BK + 8;
+    __shared__ __attribute__((aligned(16))) __bf16 sK[PF_BK * KS];
+    __shared__ __attribute__((aligned(16))) __bf16 sVt[HD * VS];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nqt = cdiv(T, PF_BQ);
+    const int qt = nqt - 1 - (int)blockIdx.x;  // heavy (late) tiles first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int G = H / KV, kvh = h / G;
+    const int q0 = qt * PF_BQ + wave * 32;
+    const size_t qs = (size_t)T * H * HD, kvs = (size_t)T * KV * HD;
+    const float* qb = q + b * qs;
+    const float* kb = k + b * kvs;
+    const float* vb = v + b * kvs;
+
+    // B operand of S^T = K Q^T: lane holds query j = lane%32, dims 16s + 8(lane/32) + 0..7
+    const int qj = q0 + (lane & 31), hf = lane >> 5;
+    bf16x8 qreg[HD / 16];
+#pragma unroll
+    for (int s = 0; s < HD / 16; ++s) {
+        if (qj < T) {
+            const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
+            const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
+            qreg[s][0] = (__bf16)a0.x; qreg[s][1] = (__bf16)a0.y; qreg[s][2] = (__bf16)a0.z; qreg[s][3] = (__bf16)a0.w;
+            qreg[s][4] = (__bf16)a1.x; qreg[s][5] = (__bf16)a1.y; qreg[s][6] = (__bf16)a1.z; qreg[s][7] = (__bf16)a1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qreg[s][e] = (__bf16)0.f;
+        }
+    }
+    f32x16 oacc[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;  // for query qj (both halves keep copies)
+
+    const int kend = min(T, qt * PF_BQ + PF_BQ);  // causal: keys < last query of the tile + 1
+    int kbeg = 0;
+    if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
+    for (int k0 = kbeg; k0 < kend; k0 += PF_BK) {
+        __syncthreads();
+        // stage K [64][HD] and V^T [HD][64] as bf16
+        for (int e = threadIdx.x; e < PF_BK * HD / 4; e += 256) {
+            const int r = e / (HD / 4), c4 = (e % (HD / 4)) * 4;
+            const int key = k0 + r;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (key < T) {
+                kv = *(const float4*)(kb + ((size_t)key * KV + kvh) * HD + c4);
+                vv = *(const float4*)(vb + ((size_t)key * KV + kvh) * HD + c4);
+            }
+            __bf16* kd = sK + r * KS + c4;
+            kd[0] = (__bf16)kv.x; kd[1] = (__bf16)kv.y; kd[2] = (__bf16)kv.z; kd[3] = (__bf16)kv.w;
+            sVt[(c4 + 0) * VS + r] = (__bf16)vv.x;
+            sVt[(c4 + 1) * VS + r] = (__bf16)vv.y;
+            sVt[(c4 + 2) * VS + r] = (__bf16)vv.z;
+            sVt[(c4 + 3) * VS + r] = (__bf16)vv.w;
+        }
+        __syncthreads();
+        if (k0 > q0 + 31) continue;  // whole tile in this wave's future (uniform per wave)
+        // S^T tiles: keys 32t + row(e), query lane%32
+        f32x16 st[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
+#pragma unroll
+            for (int s = 0; s < HD / 16; ++s) {
+                const bf16x8 ka = *(const bf16x8*)(sK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
+                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], st[t], 0, 0, 0);
+            }
+        }
+        // mask + scale; key of element e in tile t: k0 + 32t + 8(e/4) + 4hf + e%4
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
+                const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
+                const float s = vis ? st[t][e] * scale : -INFINITY;
+                st[t][e] = s;
+                tmax = fmaxf(tmax, s);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = (m_new == -INFINITY) ? 1.f : expf(m_run - m_new);
+        float psum = 0.f;
+        bf16x8 pa[4];  // A operands of P V for the 4 k-slices of 16 keys
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = (st[t][e] == -INFINITY) ? 0.f : expf(st[t][e] - m_new);
+                psum += p;
+                pa[2 * t + (e >> 3)][e & 7] = (__bf16)p;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        // rescale O rows: the O layout holds query rows 8(e/4)+4hf+e%4 of the
+        // wave's 32; lane r holds alpha of query row r
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * hf + (e & 3), 64);
+#pragma unroll
+            for (int c = 0; c < HD / 32; ++c) oacc[c][e] *= ar;
+        }
+        // O += P V. k-slice u (16 keys) of P holds, for lane half hf, keys
+        // 32(u/2) + 8(2(u%2) + i/4) + 4hf + i%4 (i = 0..7); V^T is read with the same keys.
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kbase = 32 * (u >> 1) + 16 * (u & 1) + 4 * hf;
+#pragma unroll
+            for (int c = 0; c < HD / 32; ++c) {
+                const __bf16* vr = sVt + (32 * c + (lane & 31)) * VS;
+                bf16x8 vb8;
+                const bf16x4 lo = *(const bf16x4*)(vr + kbase), hi = *(const bf16x4*)(vr + kbase + 8);
+                vb8[0] = lo[0]; vb8[1] = lo[1]; vb8[2] = lo[2]; vb8[3] = lo[3];
+                vb8[4] = hi[0]; vb8[5] = hi[1]; vb8[6] = hi[2]; vb8[7] = hi[3];
+                oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[u], vb8, oacc[c], 0, 0, 0);
+            }
+        }
+    }
+    // normalise rows by 1/l and store. O element (c, e): query row 8(e/4)+4hf+e%4, channel 32c + lane%32
+    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int r = 8 * (e >> 2) + 4 * hf + (e & 3);
+        const float inv = __shfl(linv, r, 64);
+        const int qi = q0 + r;
+        if (qi >= T) continue;
+        float* dst = out + b * qs + ((size_t)qi * H + h) * HD;
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) dst[32 * c + (lane & 31)] = oacc[c][e] * inv;
+    }
+}
+
+// Any head_dim (<= 256, multiple of 4): one wave per (query, head), online
+// softmax over keys, fp32 throughout. Used for shapes the MFMA kernel does
+// not cover.
+__global__ void __launch_bounds__(64) k_attn_prefill_simple(const float* __restrict__ q, const float* __restrict__ k,
+                                                            const float* __restrict__ v, float* __restrict__ out,
+                                                            int T, int H, int KV, int hd, float scale, int window) {
+    const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+    const int kvh = h / (H / KV);
+    const size_t qs = (size_t)T * H * hd, kvs = (size_t)T * KV * hd;
+    const float* qh = q + b * qs + ((size_t)t * H + h) * hd;
+    float qv[4], o[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) qv[i] = (lane + 64 * i < hd) ? qh[lane + 64 * i] : 0.f;
+    float m = -INFINITY, l = 0.f;
+    const int j0 = (window > 0) ? max(t - window + 1, 0) : 0;
+    for (int j = j0; j <= t; ++j) {
+        const float* kh = k + b * kvs + ((size_t)j * KV + kvh) * hd;
+        float s = 0.f;
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i < hd) s = fmaf(qv[i], kh[lane + 64 * i], s);
+        s = wave_sum(s) * scale;
+        const float mn = fmaxf(m, s), al = expf(m - mn), p = expf(s - mn);
+        l = l * al + p;
+        const float* vh = v + b * kvs + ((size_t)j * KV + kvh) * hd;
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i < hd) o[i] = o[i] * al + p * vh[lane + 64 * i];
+        m = mn;
+    }
+    float* oh = out + b * qs + ((size_t)t * H + h) * hd;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    for (int i = 0; i < 4; ++i)
+        if (lane + 64 * i < hd) oh[lane + 64 * i] = o[i] * inv;
+}
+
+int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,
+                      float scale, int window) {
+    if (hd == 64 || hd == 128) {
+        const dim3 grid(cdiv(T, PF_BQ), H, B);
+        if (hd == 64) hipLaunchKernelGGL(k_attn_prefill_mfma<64>, grid, dim3(256), 0, stream(), q, k, v, out, T, H, KV, scale, window);
+        else hipLaunchKernelGGL(k_attn_prefill_mfma<128>, grid, dim3(256), 0, stream(), q, k, v, out, T, H, KV, scale, window);
+        GH_LAUNCHED("k_attn_prefill_mfma");
+        return GH_OK;
+    }
+    GH_REQUIRE(hd <= 256, "attention_forward_ex: head_dim %d > 256", hd);
+    hipLaunchKernelGGL(k_attn_prefill_simple, dim3(T, H, B), dim3(64), 0, stream(), q, k, v, out, T, H, KV, hd, scale,
+                       window);
+    GH_LAUNCHED("k_attn_prefill_simple");
+    return GH_OK;
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" {
+
+int gh_attention_forward_ex(const float* q, const float* k, const float* v, float* out, float* probs, int B, int T,
+                            int H, int KV, int hd, float scale, int window, const int32_t* segment_ids) {
+    GH_REQUIRE(probs == nullptr, "attention_forward_ex: probs output is a training feature, not supported");
+    GH_REQUIRE(segment_ids == nullptr, "attention_forward_ex: segment masks are not supported");
+    GH_REQUIRE(q && k && v && out, "attention_forward_ex: null pointer");
+    GH_REQUIRE(B >= 0 && T >= 0 && H > 0 && KV > 0 && H % KV == 0 && hd > 0 && hd % 4 == 0,
+               "attention_forward_ex: bad shape B=%d T=%d H=%d KV=%d hd=%d", B, T, H, KV, hd);
+    if (B == 0 || T == 0) return GH_OK;
+    return attention_prefill(q, k, v, out, B, T, H, KV, hd, scale, window);
+}
+
+int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV,
+                                  int hd, int ring_start, int pinned, int cur_len, int cache_max, float scale,
+                                  float* scratch, int window) {
+    (void)scratch;
+    // core/attn_cpu.cpp:211-222
+    GH_REQUIRE(H > 0 && KV > 0 && hd > 0, "attention_decode_ring_fp16: empty shape");
+    GH_REQUIRE(H % KV == 0, "attention_decode_ring_fp16: H must be a multiple of KV");
+    GH_REQUIRE(cur_len >= 0 && cache_max >= 0 && cur_len <= cache_max,
+               "attention_decode_ring_fp16: length exceeds cache capacity");
+    GH_REQUIRE(pinned >= 0 && pinned <= cur_len, "attention_decode_ring_fp16: pinned prefix out of range");
+    const int cap = cache_max - pinned;
+    if (cur_len > pinned) {
+        GH_REQUIRE(cap > 0, "attention_decode_ring_fp16: ring has no rolling slots");
+        GH_REQUIRE(ring_start >= 0 && ring_start < cap, "attention_decode_ring_fp16: ring start out of range");
+    }
+    GH_REQUIRE(H / KV <= DEC_GMAX, "attention_decode_ring_fp16: group size %d > %d", H / KV, DEC_GMAX);
+    GH_REQUIRE(q && kc && vc && out, "attention_decode_ring_fp16: null pointer");
+    DecodeArgs a{};
+    a.q = q; a.k = kc; a.v = vc; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
+    a.ring_start = ring_start; a.pinned = pinned; a.cur_len = cur_len; a.cache_max = cache_max;
+    a.j0 = (window > 0 && cur_len > window) ? cur_len - window : 0;
+    return launch_decode<false>(a, hd, 1, cur_len - a.j0, out);
+}
+
+int gh_attention_decode_paged_bf16(const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* page_table,
+                                   const int32_t* seq_lens, int n_seqs, int max_pages, int page_size, int max_len,
+                                   float* out, int H, int KV, int hd, float scale) {
+    GH_REQUIRE(H > 0 && KV > 0 && hd > 0 && H % KV == 0, "attention_decode_paged_bf16: bad heads");
+    GH_REQUIRE(H / KV <= DEC_GMAX, "attention_decode_paged_bf16: group size %d > %d", H / KV, DEC_GMAX);
+    GH_REQUIRE(n_seqs >= 0 && page_size > 0 && max_pages > 0 && max_len >= 0 && max_len <= max_pages * page_size,
+               "attention_decode_paged_bf16: bad paging arguments");
+    GH_REQUIRE(q && kp && vp && page_table && seq_lens && out, "attention_decode_paged_bf16: null pointer");
+    if (n_seqs == 0) return GH_OK;
+    DecodeArgs a{};
+    a.q = q; a.k = kp; a.v = vp; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
+    a.page_table = page_table; a.seq_lens = seq_lens; a.max_pages = max_pages; a.page_size = page_size;
+    return launch_decode<true>(a, hd, n_seqs, max_len, out);
+}
+
+}  // extern "C"

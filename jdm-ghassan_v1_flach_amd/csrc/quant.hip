@@ -1,0 +1,415 @@
+// Quantized weights on the device: block decode (dequantise /
+// quant_materialize) and the dequant-fused decode GEMV.
+//
+// Replaces cuda/kernels.cu:482-598 (k_dequant_quant, k_linear_q4_fused: one
+// thread per output walking K with 1-2 byte loads) and the fp16 / fp32
+// linear paths used for the lm_head and the router (cuda/kernels.cu:447-633).
+//
+// GEMV layout (M <= 8, HBM-bound): a wave owns R output rows and walks K in
+// "tasks" of 64 values; a task is one contiguous, 4-byte aligned byte run of
+// the packed row (Q8_0: 2 blocks = 68 B, Q4_0: 36 B, Q4_1: 40 B, Q4_K: the
+// 16 B block header + 32 B of nibbles for 2 sub-blocks, fp16: 128 B, fp32:
+// 256 B). Lanes take consecutive tasks, so one wave-wide load instruction
+// covers a contiguous stretch of the row and every fetched byte is used. The
+// 64 activation values of a task stay in registers and are reused for all R
+// rows of the wave, which keeps the activation re-reads off the critical L1
+// path. Partial sums are reduced with cross-lane shuffles.
+#include "gh_common.h"
+
+namespace gh {
+
+// ------------------------------------------------------------ block decode
+// Value j of a block, with exactly the reference's arithmetic
+// (core/ops.cpp:310-328 for kinds 0-2; GGML block_q4_K for kind 3):
+// no multiply-add fusion, so the fp32 result is bit-identical to the CPU's.
+__device__ __forceinline__ float deq_value(int kind, const uint8_t* blk, int j) {
+#pragma clang fp contract(off)
+    const float d = f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    if (kind == 2) return (float)(int8_t)blk[2 + j] * d;
+    if (kind == 0) {
+        const uint8_t b = blk[2 + (j & 15)];
+        const int q = (j < 16) ? (b & 0xF) : (b >> 4);
+        return (float)(q - 8) * d;
+    }
+    if (kind == 1) {
+        const float mn = f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+        const uint8_t b = blk[4 + (j & 15)];
+        const int q = (j < 16) ? (b & 0xF) : (b >> 4);
+        return (float)q * d + mn;
+    }
+    // Q4_K
+    const float dmin = f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+    const uint8_t* sc = blk + 4;
+    const int s = j >> 5, l = j & 31;
+    int scv, mv;
+    if (s < 4) {
+        scv = sc[s] & 63;
+        mv = sc[s + 4] & 63;
+    } else {
+        scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
+        mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
+    }
+    const uint8_t byte = blk[16 + 32 * (s >> 1) + l];
+    const int q = (s & 1) ? (byte >> 4) : (byte & 0xF);
+    const float d1 = d * (float)scv, m1 = dmin * (float)mv;
+    return d1 * (float)q - m1;
+}
+
+// One thread per 8 consecutive values (a block is 32 or 256 values).
+template <bool TO_F16>
+__global__ void __launch_bounds__(256) k_dequant(const uint8_t* __restrict__ p, int kind, int64_t n,
+                                                 void* __restrict__ out) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i0 = g * 8;
+    if (i0 >= n) return;
+    const int bv = block_values(kind), bb = block_bytes(kind);
+    const uint8_t* blk = p + (i0 / bv) * bb;
+    const int j0 = (int)(i0 % bv);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        if (i0 + t >= n) break;
+        const float v = deq_value(kind, blk, j0 + t);
+        if (TO_F16) ((uint16_t*)out)[i0 + t] = f32_to_f16(v);
+        else ((float*)out)[i0 + t] = v;
+    }
+}
+
+// ----------------------------------------------------------------- GEMV
+// internal kinds beyond the packed ones
+constexpr int KF16 = 4, KF32 = 5;
+
+template <int KIND>
+struct Task;  // bytes per 64-value task and the dot of one task
+
+__device__ __forceinline__ float i8f(uint32_t w, int b) {  // signed byte b of w
+    return (float)(int)__builtin_amdgcn_sbfe((int)w, 8 * b, 8);
+}
+__device__ __forceinline__ float u4f(uint32_t w, int n) {  // nibble n of w
+    return (float)__builtin_amdgcn_ubfe(w, 4 * n, 4);
+}
+
+// Q8_0: two 34-byte blocks. dwords: [d0|q0 q1][q2..q5]...; block 1 starts at byte 34.
+template <>
+struct Task<2> {
+    static constexpr int DW = 17;
+    __device__ static float dot(const uint32_t* w, const float* x) {
+        auto byte = [&](int b) { return i8f(w[b >> 2], b & 3); };
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s0 = fmaf(x[i], byte(2 + i), s0);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) s1 = fmaf(x[32 + i], byte(36 + i), s1);
+        const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF));
+        const float d1 = f16_to_f32((uint16_t)(w[8] >> 16));
+        return fmaf(d0, s0, d1 * s1);
+    }
+};
+// Q4_0: two 18-byte blocks; low nibble = value j, high nibble = j+16.
+template <>
+struct Task<0> {
+    static constexpr int DW = 9;
+    __device__ static float dot(const uint32_t* w, const float* x) {
+        auto nib = [&](int byte, int hi) {
+            return (float)__builtin_amdgcn_ubfe(w[byte >> 2], 8 * (byte & 3) + 4 * hi, 4);
+        };
+        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            s0 = fmaf(x[j], nib(2 + j, 0), s0);
+            s0 = fmaf(x[j + 16], nib(2 + j, 1), s0);
+            s1 = fmaf(x[32 + j], nib(20 + j, 0), s1);
+            s1 = fmaf(x[48 + j], nib(20 + j, 1), s1);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) { x0 += x[j]; x1 += x[32 + j]; }
+        const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF));
+        const float d1 = f16_to_f32((uint16_t)(w[4] >> 16));
+        // sum x*(q-8)*d = d*(sum x*q - 8*sum x)
+        return d0 * fmaf(-8.f, x0, s0) + d1 * fmaf(-8.f, x1, s1);
+    }
+};
+// Q4_1: two 20-byte blocks, value = q*d + m.
+template <>
+struct Task<1> {
+    static constexpr int DW = 10;
+    __device__ static float dot(const uint32_t* w, const float* x) {
+        auto nib = [&](int byte, int hi) {
+            return (float)__builtin_amdgcn_ubfe(w[byte >> 2], 8 * (byte & 3) + 4 * hi, 4);
+        };
+        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            s0 = fmaf(x[j], nib(4 + j, 0), s0);
+            s0 = fmaf(x[j + 16], nib(4 + j, 1), s0);
+            s1 = fmaf(x[32 + j], nib(24 + j, 0), s1);
+            s1 = fmaf(x[48 + j], nib(24 + j, 1), s1);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) { x0 += x[j]; x1 += x[32 + j]; }
+        const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF)), m0 = f16_to_f32((uint16_t)(w[0] >> 16));
+        const float d1 = f16_to_f32((uint16_t)(w[5] & 0xFFFF)), m1 = f16_to_f32((uint16_t)(w[5] >> 16));
+        return fmaf(d0, s0, m0 * x0) + fmaf(d1, s1, m1 * x1);
+    }
+};
+// Q4_K: w[0..3] = block header (d, dmin, scales[12]); w[4..11] = 32 bytes of
+// nibbles holding sub-blocks 2p (low) and 2p+1 (high); p is passed in.
+template <>
+struct Task<3> {
+    static constexpr int DW = 12;
+    __device__ static float dot(const uint32_t* w, const float* x, int p) {
+        auto scb = [&](int i) { return (int)((w[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF); };
+        auto scale_min = [&](int s, int& sc, int& m) {
+            if (s < 4) {
+                sc = scb(s) & 63;
+                m = scb(s + 4) & 63;
+            } else {
+                sc = (scb(s + 4) & 0xF) | ((scb(s - 4) >> 6) << 4);
+                m = (scb(s + 4) >> 4) | ((scb(s) >> 6) << 4);
+            }
+        };
+        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+#pragma unroll
+        for (int l = 0; l < 32; ++l) {
+            const uint32_t dw = w[4 + (l >> 2)];
+            s0 = fmaf(x[l], (float)__builtin_amdgcn_ubfe(dw, 8 * (l & 3), 4), s0);
+            s1 = fmaf(x[32 + l], (float)__builtin_amdgcn_ubfe(dw, 8 * (l & 3) + 4, 4), s1);
+            x0 += x[l];
+            x1 += x[32 + l];
+        }
+        const float d = f16_to_f32((uint16_t)(w[0] & 0xFFFF)), dmin = f16_to_f32((uint16_t)(w[0] >> 16));
+        int sc0, m0, sc1, m1;
+        scale_min(2 * p, sc0, m0);
+        scale_min(2 * p + 1, sc1, m1);
+        // sum x*(d*sc*q - dmin*m) = d*sc*sum(x q) - dmin*m*sum(x)
+        return d * ((float)sc0 * s0 + (float)sc1 * s1) - dmin * ((float)m0 * x0 + (float)m1 * x1);
+    }
+};
+template <>
+struct Task<KF16> {
+    static constexpr int DW = 32;
+    __device__ static float dot(const uint32_t* w, const float* x) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            s = fmaf(x[2 * i], f16_to_f32((uint16_t)(w[i] & 0xFFFF)), s);
+            s = fmaf(x[2 * i + 1], f16_to_f32((uint16_t)(w[i] >> 16)), s);
+        }
+        return s;
+    }
+};
+template <>
+struct Task<KF32> {
+    static constexpr int DW = 64;
+    __device__ static float dot(const uint32_t* w, const float* x) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 64; ++i) s = fmaf(x[i], __builtin_bit_cast(float, w[i]), s);
+        return s;
+    }
+};
+
+template <int KIND>
+__device__ __forceinline__ void load_task(const uint8_t* row, int t, uint32_t* w) {
+    if constexpr (KIND == 3) {
+        const uint8_t* sb = row + (size_t)(t >> 2) * 144;
+        const uint4 h = *(const uint4*)sb;
+        const uint4 a = *(const uint4*)(sb + 16 + 32 * (t & 3));
+        const uint4 b = *(const uint4*)(sb + 32 + 32 * (t & 3));
+        w[0] = h.x; w[1] = h.y; w[2] = h.z; w[3] = h.w;
+        w[4] = a.x; w[5] = a.y; w[6] = a.z; w[7] = a.w;
+        w[8] = b.x; w[9] = b.y; w[10] = b.z; w[11] = b.w;
+    } else if constexpr (KIND == KF16 || KIND == KF32) {
+        const uint4* s = (const uint4*)(row + (size_t)t * Task<KIND>::DW * 4);
+#pragma unroll
+        for (int i = 0; i < Task<KIND>::DW / 4; ++i) {
+            const uint4 v = s[i];
+            w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        }
+    } else {
+        const uint32_t* s = (const uint32_t*)(row + (size_t)t * Task<KIND>::DW * 4);
+#pragma unroll
+        for (int i = 0; i < Task<KIND>::DW; ++i) w[i] = __builtin_nontemporal_load(s + i);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ float task_dot(const uint32_t* w, const float* x, int t) {
+    if constexpr (KIND == 3) return Task<3>::dot(w, x, t & 3);
+    else return Task<KIND>::dot(w, x);
+}
+
+// grid: one wave per group of rows; 4 waves per block.
+// LPR lanes share one row (LPR | 64), 64/LPR rows run side by side, and each
+// lane repeats that for R rows, so a wave covers G = R*64/LPR rows.
+template <int KIND, int MT, int R>
+__global__ void __launch_bounds__(256) k_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                              float* __restrict__ y, int M, int K, int N, size_t rowb, int LPR) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int RP = 64 / LPR;
+    const int sub = lane % LPR, rp = lane / LPR;
+    const int T = K / 64;
+    const int row0 = wave * R * RP;
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
+
+    int rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = row0 + rp + RP * r;
+        rows[r] = n < N ? n : N - 1;
+    }
+    for (int t = sub; t < T; t += LPR) {
+        uint32_t w[R][Task<KIND>::DW];
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_task<KIND>(W + (size_t)rows[r] * rowb, t, w[r]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= M) break;
+            float xv[64];
+            const float4* xp = (const float4*)(x + (size_t)m * K + (size_t)t * 64);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 v = xp[i];
+                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][m] += task_dot<KIND>(w[r], xv, t);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m];
+            for (int o = LPR >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            const int n = row0 + rp + RP * r;
+            if (sub == 0 && m < M && n < N) y[(size_t)m * N + n] = v;
+        }
+}
+
+template <int KIND, int MT, int R>
+static int launch_gemv_t(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {
+    const int T = K / 64;
+    int LPR = 64;
+    while (LPR > 1 && LPR > T) LPR >>= 1;
+    const int rows_per_wave = R * (64 / LPR);
+    const int waves = cdiv(N, rows_per_wave);
+    hipLaunchKernelGGL((k_gemv<KIND, MT, R>), dim3(cdiv(waves, 4)), dim3(256), 0, stream(), x,
+                       (const uint8_t*)w, y, M, K, N, rowb, LPR);
+    GH_LAUNCHED("k_gemv");
+    return GH_OK;
+}
+
+template <int KIND>
+static int launch_gemv(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {
+    // R = 4 rows per lane when there are enough rows to fill the chip, else 1
+    const int T = K / 64;
+    int LPR = 64;
+    while (LPR > 1 && LPR > T) LPR >>= 1;
+    const bool wide = (long)N / (4L * (64 / LPR)) >= 2L * num_cus() * 4;
+    if (M == 1) return wide ? launch_gemv_t<KIND, 1, 4>(x, w, y, M, K, N, rowb)
+                            : launch_gemv_t<KIND, 1, 1>(x, w, y, M, K, N, rowb);
+    if (M == 2) return launch_gemv_t<KIND, 2, 2>(x, w, y, M, K, N, rowb);
+    if (M <= 4) return launch_gemv_t<KIND, 4, 2>(x, w, y, M, K, N, rowb);
+    return launch_gemv_t<KIND, 8, 1>(x, w, y, M, K, N, rowb);
+}
+
+int gemv_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    size_t rowb;
+    switch (kind) {
+        case 0: rowb = row_bytes(0, K); return launch_gemv<0>(x, w, y, M, K, N, rowb);
+        case 1: rowb = row_bytes(1, K); return launch_gemv<1>(x, w, y, M, K, N, rowb);
+        case 2: rowb = row_bytes(2, K); return launch_gemv<2>(x, w, y, M, K, N, rowb);
+        case 3: rowb = row_bytes(3, K); return launch_gemv<3>(x, w, y, M, K, N, rowb);
+        case KF16: return launch_gemv<KF16>(x, w, y, M, K, N, (size_t)K * 2);
+        case KF32: return launch_gemv<KF32>(x, w, y, M, K, N, (size_t)K * 4);
+    }
+    return fail(GH_EINVAL, "gemv: bad kind %d", kind);
+}
+
+int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // gemm.hip
+
+static bool g_fused_q4 = true;
+static const int kQuantSlots = 16;
+
+// GEMV path constraint: K a multiple of the 64-value task
+static int check_linear(const void* x, const void* w, const void* y, int M, int K, int N, int kind) {
+    GH_REQUIRE(x && w && y, "linear_forward: null pointer");
+    GH_REQUIRE(M >= 0 && N >= 0 && K > 0, "linear_forward: bad shape M=%d K=%d N=%d", M, K, N);
+    GH_REQUIRE(K % 64 == 0 && (kind != 3 || K % 256 == 0),
+               "linear_forward: K=%d must be a multiple of %d for kind %d", K, kind == 3 ? 256 : 64, kind);
+    GH_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0, "linear_forward: x and W must be 16-byte aligned");
+    return GH_OK;
+}
+
+int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    int rc = check_linear(x, w, y, M, K, N, kind);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return GH_OK;
+    if (M <= 8) return gemv_dispatch(x, w, y, M, K, N, kind);
+    return gemm_dispatch(x, w, y, M, K, N, kind);
+}
+
+int dequant_launch(const void* packed, int kind, int64_t n, void* out, bool to_f16) {
+    const int64_t threads = (n + 7) / 8;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (to_f16) hipLaunchKernelGGL(k_dequant<true>, grid, dim3(256), 0, stream(), (const uint8_t*)packed, kind, n, out);
+    else hipLaunchKernelGGL(k_dequant<false>, grid, dim3(256), 0, stream(), (const uint8_t*)packed, kind, n, out);
+    GH_LAUNCHED("k_dequant");
+    return GH_OK;
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" {
+
+int gh_linear_forward_q4(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    GH_REQUIRE(valid_kind(kind), "linear_forward_q4: unknown kind %d", kind);
+    return linear_any(x, w, y, M, K, N, kind);
+}
+
+int gh_linear_forward_fp16(const float* x, const uint16_t* w, float* y, int M, int K, int N) {
+    return linear_any(x, w, y, M, K, N, KF16);
+}
+
+int gh_linear_forward_f32(const float* x, const float* w, float* y, int M, int K, int N) {
+    return linear_any(x, w, y, M, K, N, KF32);
+}
+
+int gh_dequantize_f32(const void* packed, int kind, int64_t n, float* out) {
+    GH_REQUIRE(valid_kind(kind) && packed && out && n >= 0, "dequantize: bad arguments");
+    if (n == 0) return GH_OK;
+    return dequant_launch(packed, kind, n, out, false);
+}
+
+int gh_quant_materialize(const void* packed, int kind, int64_t n, int slot, const uint16_t** out) {
+    // core/ops.cpp:304-347
+    GH_REQUIRE(packed != nullptr && n > 0 && out != nullptr, "quant_materialize: bad arguments");
+    GH_REQUIRE(valid_kind(kind), "quant_materialize: unknown kind %d", kind);
+    if (slot < 0 || slot >= kQuantSlots) slot = 0;
+    void* dst = workspace(16 + slot, (size_t)n * 2);
+    if (!dst) return fail(GH_ENOMEM, "quant_materialize: scratch allocation of %lld halves failed", (long long)n);
+    int rc = dequant_launch(packed, kind, n, dst, true);
+    if (rc) return rc;
+    *out = (const uint16_t*)dst;
+    return GH_OK;
+}
+
+int gh_quant_scratch_free(void) {
+    free_workspaces();
+    return GH_OK;
+}
+
+int gh_set_fused_q4(int on) {
+    g_fused_q4 = on != 0;
+    return GH_OK;
+}
+int gh_fused_q4_enabled(void) { return g_fused_q4 ? 1 : 0; }
+
+}  // extern "C"
