@@ -13,7 +13,7 @@
 //
 // Prefill (attention_forward_ex, core/attn_cpu.cpp:29-94): causal flash
 // attention on the matrix cores. A block is one q head x 128 queries, each
-// wave 32 queries; per 64-key tile S^T = K Q^T (v_mfma_f32_32x32x16_bf16),
+// wave 32 queries; per 64-key tile S^T = K Q^T (v_mfma_f32_32x32x16_f16),
 // online softmax in registers, O += P V with P taken straight from the S^T
 // accumulator layout (no LDS round trip) and V staged transposed in LDS.
 #include "gh_common.h"
@@ -35,6 +35,9 @@ struct DecodeArgs {
     const int32_t* page_table;
     const int32_t* seq_lens;
     int max_pages, page_size;
+    // ring cache with its length / ring start / pinned prefix read from the
+    // device (graph-captured decode); null: the host scalars above are used
+    const int32_t* ctl;
 };
 
 template <bool BF16>
@@ -67,6 +70,11 @@ __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
     const int sub = lane / LPP, cg = lane % LPP;
     const int G = a.G;
 
+    if (!PAGED && a.ctl) {  // decode control block: token, len, start, pinned
+        a.cur_len = a.ctl[1];
+        a.ring_start = a.ctl[2];
+        a.pinned = min(a.ctl[3], a.cur_len);
+    }
     int jb, je;  // logical positions [jb, je) of this block
     if (PAGED) {
         const int L = a.seq_lens[seq];
@@ -257,8 +265,8 @@ static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
 }
 
 // ============================================================== prefill
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int PF_BQ = 128, PF_BK = 64;
@@ -270,8 +278,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
                                                            int T, int H, int KV, float scale, int window) {
     constexpr int KS = HD + 8;  // LDS row stride of K (bf16)
     constexpr int VS = PF_BK + 8;
-    __shared__ __attribute__((aligned(16))) __bf16 sK[PF_BK * KS];
-    __shared__ __attribute__((aligned(16))) __bf16 sVt[HD * VS];
+    __shared__ __attribute__((aligned(16))) _Float16 sK[PF_BK * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 sVt[HD * VS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nqt = cdiv(T, PF_BQ);
@@ -286,17 +294,17 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
 
     // B operand of S^T = K Q^T: lane holds query j = lane%32, dims 16s + 8(lane/32) + 0..7
     const int qj = q0 + (lane & 31), hf = lane >> 5;
-    bf16x8 qreg[HD / 16];
+    f16x8 qreg[HD / 16];
 #pragma unroll
     for (int s = 0; s < HD / 16; ++s) {
         if (qj < T) {
             const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
             const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
-            qreg[s][0] = (__bf16)a0.x; qreg[s][1] = (__bf16)a0.y; qreg[s][2] = (__bf16)a0.z; qreg[s][3] = (__bf16)a0.w;
-            qreg[s][4] = (__bf16)a1.x; qreg[s][5] = (__bf16)a1.y; qreg[s][6] = (__bf16)a1.z; qreg[s][7] = (__bf16)a1.w;
+            qreg[s][0] = (_Float16)a0.x; qreg[s][1] = (_Float16)a0.y; qreg[s][2] = (_Float16)a0.z; qreg[s][3] = (_Float16)a0.w;
+            qreg[s][4] = (_Float16)a1.x; qreg[s][5] = (_Float16)a1.y; qreg[s][6] = (_Float16)a1.z; qreg[s][7] = (_Float16)a1.w;
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qreg[s][e] = (__bf16)0.f;
+            for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
         }
     }
     f32x16 oacc[HD / 32];
@@ -311,7 +319,7 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
     if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
     for (int k0 = kbeg; k0 < kend; k0 += PF_BK) {
         __syncthreads();
-        // stage K [64][HD] and V^T [HD][64] as bf16
+        // stage K [64][HD] and V^T [HD][64] as fp16 (the cache precision)
         for (int e = threadIdx.x; e < PF_BK * HD / 4; e += 256) {
             const int r = e / (HD / 4), c4 = (e % (HD / 4)) * 4;
             const int key = k0 + r;
@@ -320,12 +328,12 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
                 kv = *(const float4*)(kb + ((size_t)key * KV + kvh) * HD + c4);
                 vv = *(const float4*)(vb + ((size_t)key * KV + kvh) * HD + c4);
             }
-            __bf16* kd = sK + r * KS + c4;
-            kd[0] = (__bf16)kv.x; kd[1] = (__bf16)kv.y; kd[2] = (__bf16)kv.z; kd[3] = (__bf16)kv.w;
-            sVt[(c4 + 0) * VS + r] = (__bf16)vv.x;
-            sVt[(c4 + 1) * VS + r] = (__bf16)vv.y;
-            sVt[(c4 + 2) * VS + r] = (__bf16)vv.z;
-            sVt[(c4 + 3) * VS + r] = (__bf16)vv.w;
+            _Float16* kd = sK + r * KS + c4;
+            kd[0] = (_Float16)kv.x; kd[1] = (_Float16)kv.y; kd[2] = (_Float16)kv.z; kd[3] = (_Float16)kv.w;
+            sVt[(c4 + 0) * VS + r] = (_Float16)vv.x;
+            sVt[(c4 + 1) * VS + r] = (_Float16)vv.y;
+            sVt[(c4 + 2) * VS + r] = (_Float16)vv.z;
+            sVt[(c4 + 3) * VS + r] = (_Float16)vv.w;
         }
         __syncthreads();
         if (k0 > q0 + 31) continue;  // whole tile in this wave's future (uniform per wave)
@@ -337,8 +345,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
             for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
 #pragma unroll
             for (int s = 0; s < HD / 16; ++s) {
-                const bf16x8 ka = *(const bf16x8*)(sK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], st[t], 0, 0, 0);
+                const f16x8 ka = *(const f16x8*)(sK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
+                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[s], st[t], 0, 0, 0);
             }
         }
         // mask + scale; key of element e in tile t: k0 + 32t + 8(e/4) + 4hf + e%4
@@ -357,14 +365,14 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = (m_new == -INFINITY) ? 1.f : expf(m_run - m_new);
         float psum = 0.f;
-        bf16x8 pa[4];  // A operands of P V for the 4 k-slices of 16 keys
+        f16x8 pa[4];  // A operands of P V for the 4 k-slices of 16 keys
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const float p = (st[t][e] == -INFINITY) ? 0.f : expf(st[t][e] - m_new);
                 psum += p;
-                pa[2 * t + (e >> 3)][e & 7] = (__bf16)p;
+                pa[2 * t + (e >> 3)][e & 7] = (_Float16)p;
             }
         psum += __shfl_xor(psum, 32, 64);
         l_run = l_run * alpha + psum;
@@ -384,12 +392,12 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
             const int kbase = 32 * (u >> 1) + 16 * (u & 1) + 4 * hf;
 #pragma unroll
             for (int c = 0; c < HD / 32; ++c) {
-                const __bf16* vr = sVt + (32 * c + (lane & 31)) * VS;
-                bf16x8 vb8;
-                const bf16x4 lo = *(const bf16x4*)(vr + kbase), hi = *(const bf16x4*)(vr + kbase + 8);
+                const _Float16* vr = sVt + (32 * c + (lane & 31)) * VS;
+                f16x8 vb8;
+                const f16x4 lo = *(const f16x4*)(vr + kbase), hi = *(const f16x4*)(vr + kbase + 8);
                 vb8[0] = lo[0]; vb8[1] = lo[1]; vb8[2] = lo[2]; vb8[3] = lo[3];
                 vb8[4] = hi[0]; vb8[5] = hi[1]; vb8[6] = hi[2]; vb8[7] = hi[3];
-                oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[u], vb8, oacc[c], 0, 0, 0);
+                oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
             }
         }
     }
@@ -438,6 +446,17 @@ __global__ void __launch_bounds__(64) k_attn_prefill_simple(const float* __restr
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     for (int i = 0; i < 4; ++i)
         if (lane + 64 * i < hd) oh[lane + 64 * i] = o[i] * inv;
+}
+
+// Decode over the fp16 ring cache with (len, ring start, pinned) taken from
+// the device control block; the grid covers the whole cache capacity so the
+// launch shape does not depend on the length (capturable in a graph).
+int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV, int hd,
+                       int cache_max, const int32_t* ctl, float scale) {
+    DecodeArgs a{};
+    a.q = q; a.k = kc; a.v = vc; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
+    a.cache_max = cache_max; a.ctl = ctl; a.j0 = 0;
+    return launch_decode<false>(a, hd, 1, cache_max, out);
 }
 
 int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,

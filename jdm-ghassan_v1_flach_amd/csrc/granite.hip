@@ -1,0 +1,494 @@
+// The caller side of the boundary for the Granite-4.0 hybrid: parameter
+// storage (model/model.cpp:959-1160), the KV cache (inference/kv_cache.*),
+// the prefill (inference/generator.cpp:627-983) and the greedy decode loop
+// (:221-443, :985-1098), written against the backend's own entry points.
+//
+// The decode step keeps all of its control state on the device (token,
+// cache length, ring start, slot), so the whole step -- embedding, 6 layers,
+// lm_head, argmax -- can be captured once into a hipGraph and replayed per
+// token without host round trips (the reference synchronises per MoE layer
+// and per sampled token, cuda/moe.cu:709-729).
+#include <map>
+#include <string>
+#include <vector>
+
+#include "gh_common.h"
+
+namespace gh {
+
+int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
+int launch_f32_to_f16(const float* s, uint16_t* d, int64_t n);
+int launch_argmax(const float* l, int V, int32_t* out_dev);
+int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,
+                      float scale, int window);
+int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV, int hd,
+                       int cache_max, const int32_t* ctl, float scale);
+int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
+                       const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
+                       float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind);
+
+// decode control block (device ints)
+enum { CTL_TOKEN = 0, CTL_LEN = 1, CTL_START = 2, CTL_PINNED = 3, CTL_CAP = 4, CTL_SLOT = 5, CTL_STEP = 6, CTL_N = 8 };
+
+// KVCache::allocate_slot (inference/kv_cache.h:74-92) on the device.
+__global__ void k_alloc_slot(int32_t* ctl) {
+    const int cap = ctl[CTL_CAP], pin = ctl[CTL_PINNED];
+    int len = ctl[CTL_LEN], start = ctl[CTL_START], slot;
+    if (len < cap) {
+        slot = len;
+        if (len >= pin) slot = pin + ((start + (len - pin)) % (cap - pin));
+        ++len;
+    } else {
+        slot = pin + (start % (cap - pin));
+        start = (start + 1) % (cap - pin);
+    }
+    ctl[CTL_LEN] = len;
+    ctl[CTL_START] = start;
+    ctl[CTL_SLOT] = slot;
+}
+
+// K/V of one token -> fp16 cache rows at the slot chosen by k_alloc_slot.
+__global__ void k_store_kv(const float* __restrict__ k, const float* __restrict__ v, uint16_t* __restrict__ kc,
+                           uint16_t* __restrict__ vc, const int32_t* __restrict__ ctl, int kvd) {
+    const size_t base = (size_t)ctl[CTL_SLOT] * kvd;
+    for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
+        kc[base + i] = f32_to_f16(k[i]);
+        vc[base + i] = f32_to_f16(v[i]);
+    }
+}
+
+// token -> ids[step++] after the argmax wrote ctl[CTL_TOKEN]
+__global__ void k_record_token(int32_t* ctl, int32_t* ids, int cap) {
+    const int s = ctl[CTL_STEP];
+    if (s < cap) ids[s] = ctl[CTL_TOKEN];
+    ctl[CTL_STEP] = s + 1;
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+struct Param {
+    std::string name;
+    int64_t numel;
+    int storage;  // 0 packed (qkind), 1 fp16, 2 fp32
+    size_t nbytes, off;
+};
+
+struct gh_granite {
+    int V, d, L, H, KV, hd, E, ne, K, SH, di, mh, mdh, mds, ck, qkind;
+    std::vector<int> lt;
+    float eps, scale;
+    int max_ctx, conv_dim, proj, qd, kvd, pinned_cfg;
+    std::vector<Param> params;
+    std::map<std::string, size_t> by_name;
+    uint8_t* wbuf = nullptr;
+    size_t wbytes = 0;
+    // state
+    std::map<int, float*> conv, ssm;
+    std::map<int, uint16_t*> kc, vc;
+    float* state_buf = nullptr;
+    // activations (prefill sized)
+    float *x = nullptr, *xb = nullptr, *pr = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
+          *logits = nullptr;
+    int32_t *ids = nullptr, *ctl = nullptr, *gen_ids = nullptr;
+    int act_rows = 0;
+    int host_len = 0;  // cache length mirror
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+
+    const void* W(const std::string& n) const {
+        auto it = by_name.find(n);
+        return it == by_name.end() ? nullptr : wbuf + params[it->second].off;
+    }
+    const float* F(const std::string& n) const { return (const float*)W(n); }
+};
+
+static void add_param(gh_granite* g, const std::string& name, int64_t numel, int storage) {
+    Param p;
+    p.name = name;
+    p.numel = numel;
+    p.storage = storage;
+    if (storage == 0) p.nbytes = (size_t)(numel / block_values(g->qkind)) * block_bytes(g->qkind);
+    else p.nbytes = (size_t)numel * (storage == 1 ? 2 : 4);
+    p.off = 0;
+    g->by_name[name] = g->params.size();
+    g->params.push_back(p);
+}
+
+static void free_all(gh_granite* g) {
+    if (g->graph_exec) (void)hipGraphExecDestroy(g->graph_exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    void* ptrs[] = {g->wbuf, g->state_buf, g->x, g->ids, g->ctl, g->gen_ids};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+}
+
+static int ensure_acts(gh_granite* g, int rows) {
+    if (rows <= g->act_rows) return GH_OK;
+    if (g->x) GH_HIP(hipFree(g->x));
+    const size_t d = g->d;
+    const size_t per = 2 * d + d + (size_t)g->qd + 2 * (size_t)g->kvd + g->qd;
+    size_t n = (size_t)rows * per + g->V + 64;
+    GH_HIP(hipMalloc(&g->x, n * 4));
+    g->xb = g->x + rows * d;
+    g->pr = g->xb + rows * d;
+    g->q = g->pr + rows * d;
+    g->k = g->q + (size_t)rows * g->qd;
+    g->v = g->k + (size_t)rows * g->kvd;
+    g->att = g->v + (size_t)rows * g->kvd;
+    g->logits = g->att + (size_t)rows * g->qd;
+    g->act_rows = rows;
+    return GH_OK;
+}
+
+#define GHC(call)                      \
+    do {                               \
+        int rc_ = (call);              \
+        if (rc_) return rc_;           \
+    } while (0)
+
+static int moe_layer(gh_granite* g, int l, const float* xb, float* out, int n) {
+    const std::string pre = "layers." + std::to_string(l) + ".";
+    return gh_moe_forward_bias_half(xb, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
+                                    g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"),
+                                    g->W(pre + "moe_sh_down"), out, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                    nullptr, n, g->d, g->E, g->ne, g->K, g->SH, g->qkind);
+}
+
+static int mamba_step(gh_granite* g, int l, const float* xin, float* out) {
+    const std::string mp = "layers." + std::to_string(l) + ".mamba.";
+    return gh_mamba2_step_half(xin, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"), g->F(mp + "conv1d.bias"),
+                               g->F(mp + "dt_bias"), g->F(mp + "A_log"), g->F(mp + "D"), g->F(mp + "norm.weight"),
+                               g->W(mp + "out_proj"), g->conv[l], g->ssm[l], out, g->d, g->di, g->conv_dim, g->mh,
+                               g->mdh, g->mds, g->ck, g->eps, g->qkind);
+}
+
+// One decode step for the token in ctl[CTL_TOKEN] (inference/generator.cpp:221-443),
+// ending with the greedy argmax written back to ctl[CTL_TOKEN] and recorded.
+static int decode_step_dev(gh_granite* g, bool argmax) {
+    const int d = g->d;
+    hipLaunchKernelGGL(k_alloc_slot, dim3(1), dim3(1), 0, stream(), g->ctl);
+    GHC(gh_embedding_forward_half(g->ctl + CTL_TOKEN, (const uint16_t*)g->W("tok_embeddings"), g->x, 1, d, g->V));
+    for (int l = 0; l < g->L; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, 1, d, g->eps));
+        if (g->lt[l] == 0) {
+            GHC(mamba_step(g, l, g->xb, g->pr));
+        } else {
+            GHC(linear_any(g->xb, g->W(pre + "wq"), g->q, 1, d, g->qd, g->qkind));
+            GHC(linear_any(g->xb, g->W(pre + "wk"), g->k, 1, d, g->kvd, g->qkind));
+            GHC(linear_any(g->xb, g->W(pre + "wv"), g->v, 1, d, g->kvd, g->qkind));
+            hipLaunchKernelGGL(k_store_kv, dim3(1), dim3(256), 0, stream(), g->k, g->v, g->kc[l], g->vc[l], g->ctl,
+                               g->kvd);
+            GHC(attn_decode_devctl(g->q, g->kc[l], g->vc[l], g->att, g->H, g->KV, g->hd, g->max_ctx, g->ctl, g->scale));
+            GHC(linear_any(g->att, g->W(pre + "wo"), g->pr, 1, g->qd, d, g->qkind));
+        }
+        GHC(gh_add_inplace(g->x, g->pr, d));
+        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, 1, d, g->eps));
+        GHC(moe_layer(g, l, g->xb, g->pr, 1));
+        GHC(gh_add_inplace(g->x, g->pr, d));
+    }
+    GHC(gh_rmsnorm_forward(g->x, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
+    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    if (argmax) {
+        GHC(launch_argmax(g->logits, g->V, g->ctl + CTL_TOKEN));
+        hipLaunchKernelGGL(k_record_token, dim3(1), dim3(1), 0, stream(), g->ctl, g->gen_ids, g->max_ctx);
+    }
+    GH_LAUNCHED("decode_step");
+    return GH_OK;
+}
+
+extern "C" {
+
+int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_granite** out) {
+    GH_REQUIRE(cfg && fcfg && out, "granite_create: null argument");
+    gh_granite* g = new gh_granite();
+    g->V = cfg[0]; g->d = cfg[1]; g->L = cfg[2]; g->H = cfg[3]; g->KV = cfg[4]; g->hd = cfg[5]; g->E = cfg[6];
+    g->ne = cfg[7]; g->K = cfg[8]; g->SH = cfg[9]; g->di = cfg[10]; g->mh = cfg[11]; g->mdh = cfg[12];
+    g->mds = cfg[13]; g->ck = cfg[14]; g->qkind = cfg[15];
+    g->lt.assign(cfg + 16, cfg + 16 + g->L);
+    g->eps = fcfg[0];
+    g->scale = fcfg[1];
+    g->max_ctx = max_ctx;
+    g->conv_dim = g->di + 2 * g->mds;
+    g->proj = g->di + g->conv_dim + g->mh;
+    g->qd = g->H * g->hd;
+    g->kvd = g->KV * g->hd;
+    g->pinned_cfg = max_ctx - 1 < 8 ? (max_ctx - 1 > 0 ? max_ctx - 1 : 0) : 8;  // generator.cpp:94
+    if (!valid_kind(g->qkind) || max_ctx < 2 || g->L <= 0 || g->H % g->KV) {
+        delete g;
+        return fail(GH_EINVAL, "granite_create: bad configuration");
+    }
+    // parameter table, model/model.cpp:1087-1160 (tied lm_head)
+    const int64_t d = g->d;
+    add_param(g, "tok_embeddings", (int64_t)g->V * d, 1);
+    for (int i = 0; i < g->L; ++i) {
+        const std::string pre = "layers." + std::to_string(i) + ".";
+        add_param(g, pre + "attn_norm", d, 2);
+        add_param(g, pre + "ffn_norm", d, 2);
+        if (g->lt[i] == 0) {
+            const std::string mp = pre + "mamba.";
+            add_param(g, mp + "in_proj", (int64_t)g->proj * d, 0);
+            add_param(g, mp + "conv1d.weight", (int64_t)g->conv_dim * g->ck, 2);
+            add_param(g, mp + "conv1d.bias", g->conv_dim, 2);
+            add_param(g, mp + "dt_bias", g->mh, 2);
+            add_param(g, mp + "A_log", g->mh, 2);
+            add_param(g, mp + "D", g->mh, 2);
+            add_param(g, mp + "norm.weight", g->di, 2);
+            add_param(g, mp + "out_proj", d * g->di, 0);
+        } else {
+            add_param(g, pre + "wq", (int64_t)g->qd * d, 0);
+            add_param(g, pre + "wk", (int64_t)g->kvd * d, 0);
+            add_param(g, pre + "wv", (int64_t)g->kvd * d, 0);
+            add_param(g, pre + "wo", d * g->qd, 0);
+        }
+        add_param(g, pre + "moe_router", (int64_t)g->ne * d, 2);
+        add_param(g, pre + "moe_gate", (int64_t)g->ne * g->E * d, 0);
+        add_param(g, pre + "moe_up", (int64_t)g->ne * g->E * d, 0);
+        add_param(g, pre + "moe_down", (int64_t)g->ne * d * g->E, 0);
+        add_param(g, pre + "moe_sh_gate", (int64_t)g->SH * d, 0);
+        add_param(g, pre + "moe_sh_up", (int64_t)g->SH * d, 0);
+        add_param(g, pre + "moe_sh_down", d * g->SH, 0);
+    }
+    add_param(g, "final_norm", d, 2);
+    size_t off = 0;
+    for (Param& p : g->params) {
+        p.off = off;
+        off += (p.nbytes + 255) & ~(size_t)255;
+    }
+    g->wbytes = off;
+    hipError_t e = hipMalloc(&g->wbuf, off);
+    if (e != hipSuccess) {
+        delete g;
+        return fail(GH_ENOMEM, "granite_create: %zu bytes of weights: %s", off, hipGetErrorString(e));
+    }
+    // recurrent state + KV caches in one allocation
+    size_t sbytes = 0;
+    for (int l = 0; l < g->L; ++l) {
+        if (g->lt[l] == 0) sbytes += ((size_t)g->conv_dim * (g->ck - 1) + (size_t)g->mh * g->mdh * g->mds) * 4;
+        else sbytes += (size_t)2 * g->max_ctx * g->kvd * 2;
+    }
+    e = hipMalloc(&g->state_buf, sbytes + 256);
+    if (e == hipSuccess) e = hipMalloc(&g->ids, (size_t)1024 * 4);
+    if (e == hipSuccess) e = hipMalloc(&g->ctl, CTL_N * 4);
+    if (e == hipSuccess) e = hipMalloc(&g->gen_ids, (size_t)(g->max_ctx + 1) * 4);
+    if (e != hipSuccess) {
+        free_all(g);
+        delete g;
+        return fail(GH_ENOMEM, "granite_create: state allocation failed");
+    }
+    uint8_t* sp = (uint8_t*)g->state_buf;
+    for (int l = 0; l < g->L; ++l) {
+        if (g->lt[l] == 0) {
+            g->conv[l] = (float*)sp;
+            sp += (size_t)g->conv_dim * (g->ck - 1) * 4;
+            g->ssm[l] = (float*)sp;
+            sp += (size_t)g->mh * g->mdh * g->mds * 4;
+        } else {
+            g->kc[l] = (uint16_t*)sp;
+            sp += (size_t)g->max_ctx * g->kvd * 2;
+            g->vc[l] = (uint16_t*)sp;
+            sp += (size_t)g->max_ctx * g->kvd * 2;
+        }
+    }
+    int rc = ensure_acts(g, 1);
+    if (rc == GH_OK) rc = gh_granite_reset(g);
+    if (rc) {
+        free_all(g);
+        delete g;
+        return rc;
+    }
+    *out = g;
+    return GH_OK;
+}
+
+int gh_granite_destroy(gh_granite* g) {
+    if (!g) return GH_OK;
+    (void)hipStreamSynchronize(stream());
+    free_all(g);
+    delete g;
+    return GH_OK;
+}
+
+int gh_granite_param_count(gh_granite* g) { return g ? (int)g->params.size() : 0; }
+
+int gh_granite_param_name(gh_granite* g, int i, const char** name, size_t* nbytes) {
+    GH_REQUIRE(g && i >= 0 && i < (int)g->params.size() && name && nbytes, "granite_param_name: bad arguments");
+    *name = g->params[(size_t)i].name.c_str();
+    *nbytes = g->params[(size_t)i].nbytes;
+    return GH_OK;
+}
+
+int gh_granite_set_param(gh_granite* g, const char* name, const void* host, size_t nbytes) {
+    GH_REQUIRE(g && name && host, "granite_set_param: null argument");
+    auto it = g->by_name.find(name);
+    GH_REQUIRE(it != g->by_name.end(), "granite_set_param: unknown parameter %s", name);
+    const Param& p = g->params[it->second];
+    GH_REQUIRE(nbytes == p.nbytes, "granite_set_param: %s expects %zu bytes, got %zu", name, p.nbytes, nbytes);
+    GH_HIP(hipMemcpy(g->wbuf + p.off, host, nbytes, hipMemcpyHostToDevice));
+    return GH_OK;
+}
+
+int gh_granite_get_param(gh_granite* g, const char* name, void* host, size_t nbytes) {
+    GH_REQUIRE(g && name && host, "granite_get_param: null argument");
+    auto it = g->by_name.find(name);
+    GH_REQUIRE(it != g->by_name.end(), "granite_get_param: unknown parameter %s", name);
+    const Param& p = g->params[it->second];
+    GH_REQUIRE(nbytes == p.nbytes, "granite_get_param: %s has %zu bytes", name, p.nbytes);
+    GH_HIP(hipMemcpy(host, g->wbuf + p.off, nbytes, hipMemcpyDeviceToHost));
+    return GH_OK;
+}
+
+int gh_granite_init_synthetic(gh_granite* g, uint64_t seed) {
+    GH_REQUIRE(g != nullptr, "granite_init_synthetic: null model");
+    std::vector<float> f;
+    std::vector<uint8_t> b;
+    for (const Param& p : g->params) {
+        f.resize((size_t)p.numel);
+        GHC(gh_synth_param_f32(p.name.c_str(), seed, f.data(), p.numel));
+        b.resize(p.nbytes);
+        if (p.storage == 0) {
+            GHC(gh_quantize_host(g->qkind, f.data(), b.data(), p.numel));
+        } else if (p.storage == 1) {
+            uint16_t* h = (uint16_t*)b.data();
+            for (int64_t i = 0; i < p.numel; ++i) h[i] = f32_to_f16(f[(size_t)i]);
+        } else {
+            memcpy(b.data(), f.data(), p.nbytes);
+        }
+        GHC(gh_granite_set_param(g, p.name.c_str(), b.data(), p.nbytes));
+    }
+    return GH_OK;
+}
+
+int gh_granite_reset(gh_granite* g) {
+    GH_REQUIRE(g != nullptr, "granite_reset: null model");
+    size_t sbytes = 0;
+    for (int l = 0; l < g->L; ++l) {
+        if (g->lt[l] == 0) sbytes += ((size_t)g->conv_dim * (g->ck - 1) + (size_t)g->mh * g->mdh * g->mds) * 4;
+        else sbytes += (size_t)2 * g->max_ctx * g->kvd * 2;
+    }
+    GH_HIP(hipMemsetAsync(g->state_buf, 0, sbytes, stream()));
+    const int32_t ctl[CTL_N] = {0, 0, 0, g->pinned_cfg, g->max_ctx, 0, 0, 0};
+    GH_HIP(hipMemcpyAsync(g->ctl, ctl, sizeof ctl, hipMemcpyHostToDevice, stream()));
+    GH_HIP(hipStreamSynchronize(stream()));
+    g->host_len = 0;
+    return GH_OK;
+}
+
+int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* logits_host, int mamba_mode) {
+    GH_REQUIRE(g && ids_host && P > 0, "granite_prefill: bad arguments");
+    GH_REQUIRE(g->host_len == 0, "granite_prefill: the cache is not empty (reset first)");
+    GH_REQUIRE(P <= 1024 && P < g->max_ctx, "granite_prefill: %d tokens (batched prefill takes <= 1024 and < ctx)", P);
+    const int d = g->d;
+    GHC(ensure_acts(g, P));
+    GH_HIP(hipMemcpyAsync(g->ids, ids_host, (size_t)P * 4, hipMemcpyHostToDevice, stream()));
+    GHC(gh_embedding_forward_half(g->ids, (const uint16_t*)g->W("tok_embeddings"), g->x, P, d, g->V));
+    for (int l = 0; l < g->L; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, P, d, g->eps));
+        if (g->lt[l] == 0) {
+            if (mamba_mode == 0) {
+                // token by token, the reference's order (inference/generator.cpp:743-760)
+                for (int t = 0; t < P; ++t) GHC(mamba_step(g, l, g->xb + (size_t)t * d, g->pr + (size_t)t * d));
+            } else {
+                const std::string mp = pre + "mamba.";
+                GHC(mamba_forward_impl(g->xb, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
+                                       g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"),
+                                       g->F(mp + "D"), g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->ssm[l],
+                                       g->conv[l], g->pr, P, d, g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck,
+                                       g->eps, g->qkind));
+            }
+        } else {
+            GHC(linear_any(g->xb, g->W(pre + "wq"), g->q, P, d, g->qd, g->qkind));
+            GHC(linear_any(g->xb, g->W(pre + "wk"), g->k, P, d, g->kvd, g->qkind));
+            GHC(linear_any(g->xb, g->W(pre + "wv"), g->v, P, d, g->kvd, g->qkind));
+            GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
+            GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
+            GHC(attention_prefill(g->q, g->k, g->v, g->att, 1, P, g->H, g->KV, g->hd, g->scale, 0));
+            GHC(linear_any(g->att, g->W(pre + "wo"), g->pr, P, g->qd, d, g->qkind));
+        }
+        GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, P, d, g->eps));
+        GHC(moe_layer(g, l, g->xb, g->pr, P));
+        GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+    }
+    // cache length P, ring start 0 (KVCache::set_length)
+    const int32_t lenstart[2] = {P, 0};
+    GH_HIP(hipMemcpyAsync(g->ctl + CTL_LEN, lenstart, 8, hipMemcpyHostToDevice, stream()));
+    const int32_t zero = 0;
+    GH_HIP(hipMemcpyAsync(g->ctl + CTL_STEP, &zero, 4, hipMemcpyHostToDevice, stream()));
+    g->host_len = P;
+    GHC(gh_rmsnorm_forward(g->x + (size_t)(P - 1) * d, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
+    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    if (logits_host) {
+        GH_HIP(hipMemcpyAsync(logits_host, g->logits, (size_t)g->V * 4, hipMemcpyDeviceToHost, stream()));
+    }
+    GH_HIP(hipStreamSynchronize(stream()));
+    return GH_OK;
+}
+
+int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host) {
+    GH_REQUIRE(g != nullptr, "granite_decode: null model");
+    GH_HIP(hipMemcpyAsync(g->ctl + CTL_TOKEN, &token, 4, hipMemcpyHostToDevice, stream()));
+    GHC(decode_step_dev(g, false));
+    g->host_len = g->host_len < g->max_ctx ? g->host_len + 1 : g->host_len;
+    if (logits_host) GH_HIP(hipMemcpyAsync(logits_host, g->logits, (size_t)g->V * 4, hipMemcpyDeviceToHost, stream()));
+    GH_HIP(hipStreamSynchronize(stream()));
+    return GH_OK;
+}
+
+int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int use_graph) {
+    GH_REQUIRE(g && ids_host && n_new >= 0, "granite_generate: bad arguments");
+    GH_REQUIRE(g->host_len + n_new <= g->max_ctx, "granite_generate: %d + %d tokens exceed the context %d",
+               g->host_len, n_new, g->max_ctx);
+    if (n_new == 0) return GH_OK;
+    const int32_t zero = 0;
+    GH_HIP(hipMemcpyAsync(g->ctl + CTL_STEP, &zero, 4, hipMemcpyHostToDevice, stream()));
+    // first id from the prefill logits
+    GHC(launch_argmax(g->logits, g->V, g->ctl + CTL_TOKEN));
+    hipLaunchKernelGGL(k_record_token, dim3(1), dim3(1), 0, stream(), g->ctl, g->gen_ids, g->max_ctx);
+    int done = 1;
+    if (n_new > 1) {
+        // one plain step (also sizes every workspace before a capture)
+        GHC(decode_step_dev(g, true));
+        ++done;
+    }
+    if (use_graph && done < n_new) {
+        if (!g->graph_exec) {
+            hipStream_t s = stream();
+            bool own = false;
+            if (s == nullptr) {  // capture needs a non-null stream
+                GH_HIP(hipStreamCreate(&s));
+                own = true;
+                GH_HIP(hipDeviceSynchronize());
+                gh_set_stream((void*)s);
+            }
+            GH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            int rc = decode_step_dev(g, true);
+            hipGraph_t graph = nullptr;
+            hipError_t e = hipStreamEndCapture(s, &graph);
+            if (own) {
+                gh_set_stream(nullptr);
+            }
+            if (rc) return rc;
+            if (e != hipSuccess) return fail(GH_EHIP, "decode graph capture: %s", hipGetErrorString(e));
+            g->graph = graph;
+            GH_HIP(hipGraphInstantiate(&g->graph_exec, graph, nullptr, nullptr, 0));
+            if (own) {
+                GH_HIP(hipStreamSynchronize(s));
+                GH_HIP(hipStreamDestroy(s));
+            }
+        }
+        for (; done < n_new; ++done) GH_HIP(hipGraphLaunch(g->graph_exec, stream()));
+    } else {
+        for (; done < n_new; ++done) GHC(decode_step_dev(g, true));
+    }
+    GH_HIP(hipMemcpyAsync(ids_host, g->gen_ids, (size_t)n_new * 4, hipMemcpyDeviceToHost, stream()));
+    GH_HIP(hipStreamSynchronize(stream()));
+    g->host_len += n_new - 1;
+    return GH_OK;
+}
+
+}  // extern "C"

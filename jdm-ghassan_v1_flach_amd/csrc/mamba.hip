@@ -1,0 +1,535 @@
+// Mamba-2 (Granite-4.0 hybrid) on CDNA4: causal depthwise conv1d, the
+// chunked SSD scan and the single-token state update.
+//
+// The reference runs the selective scan as the sequential per-token
+// recurrence (core/mamba_cpu.cpp:120-170, cuda/mamba.cu:148-222: one block
+// per (b,h,p) row, serial over T). Here a prefill uses the chunked "state
+// space duality" form (chunk L = 256, n_groups = 1):
+//   a_t = A_h dt_t,  cum_t = inclusive sum of a within the chunk,
+//   y_t = sum_{tau<=t} (C_t.B_tau) e^(cum_t-cum_tau) dt_tau x_tau
+//         + e^(cum_t) C_t S_in + D x_t
+//   S_out = e^(cum_end) S_in + sum_tau e^(cum_end-cum_tau) dt_tau x_tau B_tau^T
+// in four launches: G = C B^T per chunk (shared by all heads), the per-chunk
+// state contributions dS on the matrix cores, a wave-level pass carrying the
+// state across chunks, and the chunk outputs (intra-chunk M X and the
+// C S_in correction on the matrix cores). Decode is one fused conv+update
+// kernel between the two projections.
+#include "gh_common.h"
+
+namespace gh {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
+
+__device__ __forceinline__ float softplus_ref(float v) {
+    // core/mamba_cpu.cpp:139-140 (identity above 20)
+    return (v > 20.0f) ? v : log1pf(expf(v));
+}
+
+// ================================================================ conv1d
+// out[t][c] = silu(b_c + sum_j w[c][j] * raw[t-(k-1)+j][c]), raw = the bc
+// part of the projection; the window starts at zero for every sequence
+// (core/mamba_cpu.cpp:70-118). Every (t, c) is independent.
+__global__ void k_conv1d(const float* __restrict__ proj, int proj_ld, int col0, const float* __restrict__ w,
+                         const float* __restrict__ b, float* __restrict__ out, int B, int T, int C, int k) {
+#pragma clang fp contract(off)
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int row = blockIdx.y;  // b*T + t
+    if (c >= C) return;
+    const int t = row % T;
+    float acc = b ? b[c] : 0.0f;
+    for (int j = 0; j < k; ++j) {
+        const int tt = t - (k - 1) + j;
+        const float v = tt >= 0 ? proj[(size_t)(row - (k - 1) + j) * proj_ld + col0 + c] : 0.0f;
+        acc += w[(size_t)c * k + j] * v;
+    }
+    out[(size_t)row * C + c] = acc / (1.0f + expf(-acc));
+}
+
+// dt = softplus(dt_raw + dt_bias), A = -exp(A_log), and the chunk-local
+// inclusive cumulative sums of A*dt. One wave per (chunk, head).
+__global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in, int dt_ld,
+                                                 const float* __restrict__ dt_bias, const float* __restrict__ A_in,
+                                                 const float* __restrict__ a_log, float* __restrict__ dt_out,
+                                                 float* __restrict__ cum, int T, int H, int L) {
+    const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int t0 = c * L, len = min(L, T - t0);
+    const float A = A_in ? A_in[h] : -expf(a_log[h]);
+    float carry = 0.f;
+    for (int base = 0; base < len; base += 64) {
+        const int i = base + lane;
+        float dt = 0.f, a = 0.f;
+        if (i < len) {
+            const float raw = dt_in[(size_t)(t0 + i) * dt_ld + h];
+            dt = dt_bias ? softplus_ref(raw + dt_bias[h]) : raw;
+            a = A * dt;
+        }
+        float inc = a;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float v = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += v;
+        }
+        if (i < len) {
+            dt_out[(size_t)(t0 + i) * H + h] = dt;
+            cum[(size_t)(t0 + i) * H + h] = carry + inc;
+        }
+        carry += __shfl(inc, 63, 64);
+    }
+}
+
+// G[c][t][tau] = C_t . B_tau inside chunk c (fp32, 64x64 tiles).
+__global__ void __launch_bounds__(256) k_ssd_cb(const float* __restrict__ Bm, const float* __restrict__ Cm, int ld,
+                                                float* __restrict__ G, int T, int N, int L) {
+    __shared__ float sC[64][33], sB[64][33];
+    const int c = blockIdx.z, ti = blockIdx.y * 64, si = blockIdx.x * 64;
+    const int t0 = c * L;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    float acc[4][4] = {};
+    for (int n0 = 0; n0 < N; n0 += 32) {
+        for (int e = threadIdx.x; e < 64 * 32; e += 256) {
+            const int r = e >> 5, k = e & 31;
+            const int tr = t0 + ti + r, sr = t0 + si + r;
+            sC[r][k] = (ti + r < L && tr < T) ? Cm[(size_t)tr * ld + n0 + k] : 0.f;
+            sB[r][k] = (si + r < L && sr < T) ? Bm[(size_t)sr * ld + n0 + k] : 0.f;
+        }
+        __syncthreads();
+        for (int k = 0; k < 32; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(sC[ty * 4 + i][k], sB[tx * 4 + j][k], acc[i][j]);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = ti + ty * 4 + i, s = si + tx * 4 + j;
+            if (t < L && s < L) G[((size_t)c * L + t) * L + s] = acc[i][j];
+        }
+}
+
+// dS[c][h][p][n] = sum_tau e^(cum_end - cum_tau) dt_tau x_tau[p] B_tau[n]
+// (P = 64 rows, N cols in 32-wide MFMA tiles), fp16 operands, fp32 acc.
+template <int N>
+__global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict__ xs, int ldx,
+                                                         const float* __restrict__ Bm, int ldb,
+                                                         const float* __restrict__ dt, const float* __restrict__ cum,
+                                                         float* __restrict__ dS, float* __restrict__ decay, int T,
+                                                         int H, int L) {
+    constexpr int P = 64, TK = 64, S = TK + 8;
+    __shared__ __attribute__((aligned(16))) _Float16 sX[P * S];  // [p][tau]
+    __shared__ __attribute__((aligned(16))) _Float16 sB[N * S];  // [n][tau]
+    __shared__ float sw[TK];
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = c * L, len = min(L, T - t0);
+    const float cend = cum[(size_t)(t0 + len - 1) * H + h];
+    constexpr int NT = (P / 32) * (N / 32);  // output tiles
+    constexpr int TPW = NT / 4;              // tiles per wave
+    f32x16 acc[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+    for (int k0 = 0; k0 < len; k0 += TK) {
+        __syncthreads();
+        if (threadIdx.x < TK) {
+            const int tau = k0 + threadIdx.x;
+            sw[threadIdx.x] = tau < len ? expf(cend - cum[(size_t)(t0 + tau) * H + h]) * dt[(size_t)(t0 + tau) * H + h]
+                                        : 0.f;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < TK * P; e += 256) {
+            const int tau = e / P, p = e % P;
+            const float v = (k0 + tau < len) ? xs[(size_t)(t0 + k0 + tau) * ldx + h * P + p] * sw[tau] : 0.f;
+            sX[p * S + tau] = (_Float16)v;
+        }
+        for (int e = threadIdx.x; e < TK * N; e += 256) {
+            const int tau = e / N, n = e % N;
+            const float v = (k0 + tau < len) ? Bm[(size_t)(t0 + k0 + tau) * ldb + n] : 0.f;
+            sB[n * S + tau] = (_Float16)v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ++ks) {
+            const int ko = ks * 16 + 8 * (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < TPW; ++i) {
+                const int tile = wave * TPW + i;
+                const int pt = tile % (P / 32), nt = tile / (P / 32);
+                const f16x8 a = *(const f16x8*)(sX + (pt * 32 + (lane & 31)) * S + ko);
+                const f16x8 b = *(const f16x8*)(sB + (nt * 32 + (lane & 31)) * S + ko);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+            }
+        }
+    }
+    float* out = dS + ((size_t)c * H + h) * P * N;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        const int tile = wave * TPW + i;
+        const int pt = tile % (P / 32), nt = tile / (P / 32);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const int n = nt * 32 + (lane & 31);
+            out[(size_t)p * N + n] = acc[i][e];
+        }
+    }
+    if (threadIdx.x == 0) decay[(size_t)c * H + h] = expf(cend);
+}
+
+// Inter-chunk pass: S_in[c] = state before chunk c; state <- S_in*decay + dS.
+// One thread per (h, p, n): the recurrence over chunks is serial, the
+// elements are independent and their loads coalesce.
+__global__ void k_ssd_state_pass(float* __restrict__ state, const float* __restrict__ dS,
+                                 const float* __restrict__ decay, float* __restrict__ Sin, int nchunks, int H,
+                                 int PN) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)H * PN) return;
+    const int h = (int)(i / PN);
+    float s = state[i];
+    for (int c = 0; c < nchunks; ++c) {
+        Sin[(size_t)c * H * PN + i] = s;
+        s = s * decay[(size_t)c * H + h] + dS[(size_t)c * H * PN + i];
+    }
+    state[i] = s;
+}
+
+// Chunk outputs: y[t][p] = sum_{tau<=t} G[t][tau] e^(cum_t-cum_tau) dt_tau x_tau[p]
+//                 + e^(cum_t) sum_n C_t[n] S_in[p][n] + D x_t[p].
+// Block = (chunk, head, 64-row t tile): 4 waves x (32 t rows x 32 p cols),
+// MFMA 32x32x16 with fp16 operands and fp32 accumulation.
+template <int N>
+__global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__ xs, int ldx,
+                                                       const float* __restrict__ Cm, int ldc,
+                                                       const float* __restrict__ G, const float* __restrict__ dt,
+                                                       const float* __restrict__ cum, const float* __restrict__ Sin,
+                                                       const float* __restrict__ D, float* __restrict__ y, int ldy,
+                                                       int T, int H, int L) {
+    constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
+    __shared__ __attribute__((aligned(16))) _Float16 sXt[P * S];   // [p][tau]
+    __shared__ __attribute__((aligned(16))) _Float16 sS[P * SN];   // [p][n]  (S_in)
+    __shared__ float scum[TK], sdt[TK];
+    const int c = blockIdx.x, h = blockIdx.y, tt = blockIdx.z * 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = c * L, len = min(L, T - t0);
+    if (tt >= len) return;
+    const int wt = (wave >> 1) * 32, wp = (wave & 1) * 32;  // wave tile: t rows tt+wt.., p cols wp..
+    const int trow = tt + wt + (lane & 31);                  // A-operand row of this lane
+    const bool trow_ok = trow < len;
+    const float cum_t = trow_ok ? cum[(size_t)(t0 + trow) * H + h] : 0.f;
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+
+    // ---- inter-chunk term: e^(cum_t) C_t S_in^T
+    const float* Sc = Sin + ((size_t)c * H + h) * P * N;
+    for (int e = threadIdx.x; e < P * N; e += 256) sS[(e / N) * SN + (e % N)] = (_Float16)Sc[e];
+    __syncthreads();
+    {
+        const float sc = trow_ok ? expf(cum_t) : 0.f;
+        const float* crow = Cm + (size_t)(t0 + (trow_ok ? trow : 0)) * ldc;
+#pragma unroll 4
+        for (int ks = 0; ks < N / 16; ++ks) {
+            const int ko = ks * 16 + 8 * (lane >> 5);
+            f16x8 a;
+            const float4 c0 = *(const float4*)(crow + ko), c1 = *(const float4*)(crow + ko + 4);
+            a[0] = (_Float16)(c0.x * sc); a[1] = (_Float16)(c0.y * sc); a[2] = (_Float16)(c0.z * sc); a[3] = (_Float16)(c0.w * sc);
+            a[4] = (_Float16)(c1.x * sc); a[5] = (_Float16)(c1.y * sc); a[6] = (_Float16)(c1.z * sc); a[7] = (_Float16)(c1.w * sc);
+            const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+        }
+    }
+    // ---- intra-chunk term over tau tiles up to the last row of this block
+    const int kend = min(len, tt + 64);
+    for (int k0 = 0; k0 < kend; k0 += TK) {
+        __syncthreads();
+        if (threadIdx.x < TK) {
+            const int tau = k0 + threadIdx.x;
+            scum[threadIdx.x] = tau < len ? cum[(size_t)(t0 + tau) * H + h] : 0.f;
+            sdt[threadIdx.x] = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
+        }
+        for (int e = threadIdx.x; e < TK * P; e += 256) {
+            const int tau = e / P, p = e % P;
+            sXt[p * S + tau] = (_Float16)((k0 + tau < len) ? xs[(size_t)(t0 + k0 + tau) * ldx + h * P + p] : 0.f);
+        }
+        __syncthreads();
+        if (k0 > tt + wt + 31) continue;  // wave-uniform: tile entirely in this wave's future
+        const float* grow = G + ((size_t)c * L + (trow_ok ? trow : 0)) * L + k0;
+#pragma unroll
+        for (int ks = 0; ks < TK / 16; ++ks) {
+            const int ko = ks * 16 + 8 * (lane >> 5);
+            f16x8 a;
+            const float4 g0 = *(const float4*)(grow + ko), g1 = *(const float4*)(grow + ko + 4);
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int tau = k0 + ko + i;
+                const bool vis = trow_ok && tau <= trow && tau < len;
+                const float m = vis ? gv[i] * expf(cum_t - scum[ko + i]) * sdt[ko + i] : 0.f;
+                a[i] = (_Float16)m;
+            }
+            const f16x8 b = *(const f16x8*)(sXt + (wp + (lane & 31)) * S + ko);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+        }
+    }
+    // ---- + D x, store. acc element e: t row wt + 8(e/4)+4(lane/32)+e%4, p col wp + lane%32
+    const float Dh = D[h];
+    const int p = wp + (lane & 31);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int t = tt + wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (t < len) {
+            const size_t row = (size_t)(t0 + t);
+            y[row * ldy + h * P + p] = acc[e] + Dh * xs[row * ldx + h * P + p];
+        }
+    }
+}
+
+// Runs the chunked scan over rows [0, T) of one sequence.
+static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, int ldbc, const float* dt_raw, int dt_ld,
+                   const float* dt_bias, const float* A, const float* a_log, const float* D, float* state, float* y,
+                   int ldy, int T, int H, int P, int N, int L) {
+    GH_REQUIRE(P == 64, "ssd scan: head_dim %d (the kernels are built for 64)", P);
+    GH_REQUIRE(N == 64 || N == 128, "ssd scan: d_state %d (64 or 128)", N);
+    GH_REQUIRE(L >= 64 && L <= 256 && L % 64 == 0, "ssd scan: chunk %d (64..256, multiple of 64)", L);
+    GH_REQUIRE(ldx % 4 == 0 && ldbc % 4 == 0, "ssd scan: row strides must be multiples of 4");
+    const int nch = cdiv(T, L);
+    const size_t PN = (size_t)P * N;
+    // workspace: dt, cum [T][H]; G [nch][L][L]; dS, Sin [nch][H][P][N]; decay [nch][H]
+    const size_t f_dt = (size_t)T * H, f_G = (size_t)nch * L * L, f_S = (size_t)nch * H * PN;
+    float* ws = (float*)workspace(WS_MAMBA_CHUNK, (2 * f_dt + f_G + 2 * f_S + (size_t)nch * H + 64) * 4);
+    if (!ws) return fail(GH_ENOMEM, "ssd scan: workspace");
+    float* dt = ws;
+    float* cum = dt + f_dt;
+    float* G = cum + f_dt;
+    float* dS = G + f_G;
+    float* Sin = dS + f_S;
+    float* decay = Sin + f_S;
+    hipLaunchKernelGGL(k_ssd_prep, dim3(nch, H), dim3(64), 0, stream(), dt_raw, dt_ld, dt_bias, A, a_log, dt, cum, T,
+                       H, L);
+    hipLaunchKernelGGL(k_ssd_cb, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, N, L);
+    if (N == 128) {
+        hipLaunchKernelGGL(k_ssd_chunk_state<128>, dim3(nch, H), dim3(256), 0, stream(), xs, ldx, Bm, ldbc, dt, cum, dS,
+                           decay, T, H, L);
+    } else {
+        hipLaunchKernelGGL(k_ssd_chunk_state<64>, dim3(nch, H), dim3(256), 0, stream(), xs, ldx, Bm, ldbc, dt, cum, dS,
+                           decay, T, H, L);
+    }
+    const int64_t nst = (int64_t)H * PN;
+    hipLaunchKernelGGL(k_ssd_state_pass, dim3((unsigned)((nst + 255) / 256)), dim3(256), 0, stream(), state, dS, decay,
+                       Sin, nch, H, (int)PN);
+    if (N == 128) {
+        hipLaunchKernelGGL(k_ssd_chunk_out<128>, dim3(nch, H, L / 64), dim3(256), 0, stream(), xs, ldx, Cm, ldbc, G,
+                           dt, cum, Sin, D, y, ldy, T, H, L);
+    } else {
+        hipLaunchKernelGGL(k_ssd_chunk_out<64>, dim3(nch, H, L / 64), dim3(256), 0, stream(), xs, ldx, Cm, ldbc, G,
+                           dt, cum, Sin, D, y, ldy, T, H, L);
+    }
+    GH_LAUNCHED("k_ssd_*");
+    return GH_OK;
+}
+
+// ============================================================ gated norm
+// rmsnorm(y * silu(z)) * w with the sum of squares in double and the
+// inverse root in fp32 (core/mamba_cpu.cpp:172-193). One block per row.
+__global__ void __launch_bounds__(256) k_gated_norm(const float* __restrict__ y, int ldy, const float* __restrict__ z,
+                                                    int ldz, const float* __restrict__ w, float* __restrict__ out,
+                                                    int n, float eps) {
+    const int r = blockIdx.x;
+    const float* yr = y + (size_t)r * ldy;
+    const float* zr = z + (size_t)r * ldz;
+    float* o = out + (size_t)r * n;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float g = zr[i] / (1.0f + expf(-zr[i]));
+        const float v = yr[i] * g;
+        o[i] = v;
+        ss += (double)v * v;
+    }
+    __shared__ double red[4];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const double var = (red[0] + red[1] + red[2] + red[3]) / (double)n;
+    const float inv = 1.0f / sqrtf((float)var + eps);
+    for (int i = threadIdx.x; i < n; i += 256) o[i] = o[i] * inv * w[i];
+}
+
+// ======================================================== decode step
+// Conv over the carried window [conv_dim][k-1] + the new raw value, SiLU,
+// window shift (inference/generator.cpp:534-559). One thread per channel.
+__global__ void k_step_conv(const float* __restrict__ raw, const float* __restrict__ w, const float* __restrict__ b,
+                            float* __restrict__ win, float* __restrict__ out, int C, int k) {
+#pragma clang fp contract(off)
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    const int wl = k > 1 ? k - 1 : 1;
+    float* wc = win + (size_t)c * wl;
+    const float rv = raw[c];
+    float acc = b ? b[c] : 0.0f;
+    for (int j = 0; j < k; ++j) acc += w[(size_t)c * k + j] * ((j == k - 1) ? rv : wc[j]);
+    out[c] = acc / (1.0f + expf(-acc));
+    for (int j = 0; j + 1 < wl; ++j) wc[j] = wc[j + 1];
+    wc[wl - 1] = rv;
+}
+
+// State update of one token (inference/generator.cpp:570-594):
+// s = e^(A dt) s + (B dt) x,  y = C.s + D x. Block = (head, 16 rows of P);
+// thread = (row, 8 consecutive states); the 1.5 MB state streams through
+// once in 16-byte loads/stores.
+template <int N>
+__global__ void __launch_bounds__(256) k_step_scan(const float* __restrict__ xbc, const float* __restrict__ dtr,
+                                                   const float* __restrict__ dt_bias, const float* __restrict__ a_log,
+                                                   const float* __restrict__ D, float* __restrict__ ssm,
+                                                   float* __restrict__ y, int d_inner, int P) {
+    constexpr int TPR = N / 8;          // threads per state row
+    constexpr int ROWS = 256 / TPR;     // rows per block
+    const int h = blockIdx.y, r0 = blockIdx.x * ROWS;
+    const int tr = threadIdx.x / TPR, tc = threadIdx.x % TPR;
+    const int p = r0 + tr;
+    if (p >= P) return;
+    const float a = -expf(a_log[h]);
+    const float dtb = dtr[h] + dt_bias[h];
+    const float dt = (dtb > 20.0f) ? dtb : log1pf(expf(dtb));
+    const float dA = expf(a * dt);
+    const int i = h * P + p;
+    const float xv = xbc[i];
+    const float* Bm = xbc + d_inner;
+    const float* Cm = Bm + N;
+    float* srow = ssm + (size_t)i * N + tc * 8;
+    float4 s0 = *(float4*)srow, s1 = *(float4*)(srow + 4);
+    float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int n = tc * 8 + j;
+        s[j] = dA * s[j] + (Bm[n] * dt) * xv;
+        acc = fmaf(Cm[n], s[j], acc);
+    }
+    *(float4*)srow = make_float4(s[0], s[1], s[2], s[3]);
+    *(float4*)(srow + 4) = make_float4(s[4], s[5], s[6], s[7]);
+#pragma unroll
+    for (int o = TPR >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (tc == 0) y[i] = acc + D[h] * xv;
+}
+
+// conv window after a batched prefill: the last k-1 raw xBC rows
+__global__ void k_save_window(const float* __restrict__ proj, int proj_ld, int col0, float* __restrict__ win, int T,
+                              int C, int k) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= C) return;
+    const int wl = k > 1 ? k - 1 : 1;
+    for (int j = 0; j < wl; ++j) {
+        const int t = T - wl + j;
+        win[(size_t)c * wl + j] = t >= 0 ? proj[(size_t)t * proj_ld + col0 + c] : 0.f;
+    }
+}
+
+// One sequence of T tokens: in_proj, conv1d (+ optionally the conv window
+// left for decode), chunked scan, gated norm, out_proj. kind 0-3 packed,
+// 4 fp16 weights.
+int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
+                       const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
+                       float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind) {
+    GH_REQUIRE(conv_dim - d_inner == 2 * d_state, "mamba: inconsistent conv_dim / d_state (n_groups must be 1)");
+    GH_REQUIRE(n_heads * d_head == d_inner, "mamba: n_heads * d_head != d_inner");
+    const int proj = d_inner + conv_dim + n_heads;
+    float* pr = (float*)workspace(WS_MAMBA_PROJ, (size_t)T * proj * 4);
+    float* xbc = (float*)workspace(WS_MAMBA_XBC, (size_t)T * conv_dim * 4);
+    float* yb = (float*)workspace(WS_MAMBA_Y, (size_t)T * d_inner * 4 * 2);
+    if (!pr || !xbc || !yb) return fail(GH_ENOMEM, "mamba: workspace");
+    float* normed = yb + (size_t)T * d_inner;
+    int rc = linear_any(x, w_in, pr, T, d, proj, kind);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_conv1d, dim3(cdiv(conv_dim, 256), T), dim3(256), 0, stream(), pr, proj, d_inner, conv_w,
+                       conv_b, xbc, 1, T, conv_dim, k);
+    GH_LAUNCHED("k_conv1d");
+    if (conv_state) {
+        hipLaunchKernelGGL(k_save_window, dim3(cdiv(conv_dim, 256)), dim3(256), 0, stream(), pr, proj, d_inner,
+                           conv_state, T, conv_dim, k);
+        GH_LAUNCHED("k_save_window");
+    }
+    rc = ssd_run(xbc, conv_dim, xbc + d_inner, xbc + d_inner + d_state, conv_dim, pr + d_inner + conv_dim, proj,
+                 dt_bias, nullptr, a_log, D, state, yb, d_inner, T, n_heads, d_head, d_state, 256);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_gated_norm, dim3(T), dim3(256), 0, stream(), yb, d_inner, pr, proj, norm_w, normed, d_inner,
+                       eps);
+    GH_LAUNCHED("k_gated_norm");
+    return linear_any(normed, w_out, out, T, d_inner, d, kind);
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" {
+
+int gh_ssd_scan(const float* xs, const float* Bm, const float* Cm, const float* dt, const float* A, const float* D,
+                float* state, float* y, int T, int H, int P, int N, int chunk) {
+    GH_REQUIRE(xs && Bm && Cm && dt && A && D && state && y, "ssd_scan: null pointer");
+    if (T <= 0) return GH_OK;
+    if (chunk <= 0) chunk = 256;
+    // B and C are separate [T][N] arrays here: both use row stride N
+    return ssd_run(xs, H * P, Bm, Cm, N, dt, H, nullptr, A, nullptr, D, state, y, H * P, T, H, P, N, chunk);
+}
+
+int gh_mamba2_forward_half(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
+                           const float* dt_bias, const float* a_log, const float* D, const float* norm_w,
+                           const void* w_out, float* state, float* out, int B, int T, int d, int d_inner,
+                           int conv_dim, int n_heads, int d_head, int d_state, int k, float eps, int qkind) {
+    if (B <= 0 || T <= 0) return GH_OK;
+    GH_REQUIRE(x && w_in && conv_w && dt_bias && a_log && D && norm_w && w_out && state && out,
+               "mamba2_forward: null pointer");
+    GH_REQUIRE(qkind >= -1 && qkind <= 3, "mamba: unknown qkind %d", qkind);
+    const int kind = qkind < 0 ? 4 : qkind;  // fp16 weights use the fp16 linear path
+    for (int b = 0; b < B; ++b) {
+        int rc = mamba_forward_impl(x + (size_t)b * T * d, w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w, w_out,
+                                    state + (size_t)b * n_heads * d_head * d_state, nullptr, out + (size_t)b * T * d,
+                                    T, d, d_inner, conv_dim, n_heads, d_head, d_state, k, eps, kind);
+        if (rc) return rc;
+    }
+    return GH_OK;
+}
+
+int gh_mamba2_step_half(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
+                        const float* dt_bias, const float* a_log, const float* D, const float* norm_w,
+                        const void* w_out, float* conv_state, float* ssm_state, float* out, int d, int d_inner,
+                        int conv_dim, int n_heads, int d_head, int d_state, int k, float eps, int qkind) {
+    GH_REQUIRE(x && w_in && conv_w && dt_bias && a_log && D && norm_w && w_out && conv_state && ssm_state && out,
+               "mamba2_step: null pointer");
+    GH_REQUIRE(conv_dim - d_inner == 2 * d_state, "mamba: inconsistent conv_dim / d_state (n_groups must be 1)");
+    GH_REQUIRE(n_heads * d_head == d_inner, "mamba: n_heads * d_head != d_inner");
+    GH_REQUIRE(d_state == 64 || d_state == 128, "mamba2_step: d_state %d (64 or 128)", d_state);
+    GH_REQUIRE(qkind >= -1 && qkind <= 3, "mamba: unknown qkind %d", qkind);
+    const int kind = qkind < 0 ? 4 : qkind;
+    const int proj = d_inner + conv_dim + n_heads;
+    float* pr = (float*)workspace(WS_MAMBA_PROJ, (size_t)proj * 4);
+    float* xbc = (float*)workspace(WS_MAMBA_XBC, (size_t)conv_dim * 4);
+    float* yb = (float*)workspace(WS_MAMBA_Y, (size_t)d_inner * 4 * 2);
+    if (!pr || !xbc || !yb) return fail(GH_ENOMEM, "mamba: workspace");
+    float* normed = yb + d_inner;
+    int rc = linear_any(x, w_in, pr, 1, d, proj, kind);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_step_conv, dim3(cdiv(conv_dim, 256)), dim3(256), 0, stream(), pr + d_inner, conv_w, conv_b,
+                       conv_state, xbc, conv_dim, k);
+    const int rows_per_block = 256 / (d_state / 8);
+    if (d_state == 128)
+        hipLaunchKernelGGL(k_step_scan<128>, dim3(cdiv(d_head, rows_per_block), n_heads), dim3(256), 0, stream(), xbc,
+                           pr + d_inner + conv_dim, dt_bias, a_log, D, ssm_state, yb, d_inner, d_head);
+    else
+        hipLaunchKernelGGL(k_step_scan<64>, dim3(cdiv(d_head, rows_per_block), n_heads), dim3(256), 0, stream(), xbc,
+                           pr + d_inner + conv_dim, dt_bias, a_log, D, ssm_state, yb, d_inner, d_head);
+    hipLaunchKernelGGL(k_gated_norm, dim3(1), dim3(256), 0, stream(), yb, d_inner, pr, proj, norm_w, normed, d_inner,
+                       eps);
+    GH_LAUNCHED("k_step_*");
+    return linear_any(normed, w_out, out, 1, d_inner, d, kind);
+}
+
+}  // extern "C"

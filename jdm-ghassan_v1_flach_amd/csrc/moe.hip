@@ -1,0 +1,581 @@
+// Mixture-of-experts FFN: router top-k, deterministic token permutation,
+// grouped expert GEMV (decode) / grouped MFMA GEMM (prefill) with the SwiGLU
+// fused into the gate/up epilogue, and an ordered combine.
+//
+// Replaces cuda/moe.cu:170-905: there the grouping is an atomic counting
+// sort (non-deterministic slot order), the offsets are copied to the host
+// (a sync per layer), every expert is one GEMV/GEMM launch per matrix and the
+// combine is an atomicAdd scatter. Here the whole FFN is 6-7 launches with
+// no host sync, independent of the expert count, and every output is
+// bit-reproducible run to run.
+#include "gemm_tile.h"
+#include "gemv_tasks.h"
+
+namespace gh {
+
+// =============================================================== router
+// core/moe_cpu.cpp:218-256, one wave per token, same arithmetic order:
+// logit_e = dot_row (4 products grouped left to right, no fused multiply-
+// add), softmax_row (core/math_cpu.cpp:546-558, sequential sum), selection
+// on p + bias by K rounds of strict '>' argmax (lowest index wins), weights
+// from the unbiased p renormalised (uniform if their sum <= 1e-8).
+__global__ void __launch_bounds__(64) k_route(const float* __restrict__ x, const float* __restrict__ rw,
+                                              const float* __restrict__ bias, float* __restrict__ probs,
+                                              int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
+                                              int K) {
+#pragma clang fp contract(off)
+    extern __shared__ float sx[];
+    __shared__ float sp[64];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float* xt = x + (size_t)t * d;
+    for (int i = lane; i < d; i += 64) sx[i] = xt[i];
+    __syncthreads();
+    if (lane < ne) {
+        const float* r = rw + (size_t)lane * d;
+        float s = 0.0f;
+        int i = 0;
+        for (; i + 4 <= d; i += 4) {
+            const float4 w = *(const float4*)(r + i);
+            const float p0 = sx[i] * w.x, p1 = sx[i + 1] * w.y, p2 = sx[i + 2] * w.z, p3 = sx[i + 3] * w.w;
+            s += ((p0 + p1) + p2) + p3;
+        }
+        for (; i < d; ++i) s += sx[i] * r[i];
+        sp[lane] = s;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float mx = sp[0];
+        for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
+        float sum = 0.f;
+        for (int e = 0; e < ne; ++e) {
+            // exp rounded once from double: the correctly rounded expf
+            const float ev = (float)exp((double)(sp[e] - mx));
+            sp[e] = ev;
+            sum += ev;
+        }
+        const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
+        for (int e = 0; e < ne; ++e) sp[e] *= inv;
+        int sel[8];
+        float wv[8];
+        for (int k = 0; k < K; ++k) {
+            int best = -1;
+            float bv = -1e30f;
+            for (int e = 0; e < ne; ++e) {
+                bool taken = false;
+                for (int j = 0; j < k; ++j) taken |= (sel[j] == e);
+                const float v = sp[e] + (bias ? bias[e] : 0.0f);
+                if (!taken && v > bv) {
+                    bv = v;
+                    best = e;
+                }
+            }
+            if (best < 0) best = 0;
+            sel[k] = best;
+        }
+        float sw = 0.f;
+        for (int k = 0; k < K; ++k) {
+            wv[k] = sp[sel[k]];
+            sw += wv[k];
+        }
+        if (sw > 1e-8f) {
+            const float iw = 1.0f / sw;
+            for (int k = 0; k < K; ++k) wv[k] *= iw;
+        } else {
+            for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
+        }
+        for (int k = 0; k < K; ++k) {
+            idx[(size_t)t * K + k] = sel[k];
+            wout[(size_t)t * K + k] = wv[k];
+        }
+    }
+    __syncthreads();
+    if (probs && lane < ne) probs[(size_t)t * ne + lane] = sp[lane];
+}
+
+// ========================================================== permutation
+// Stable counting sort of slot ids s = t*K+k by expert, in three
+// deterministic passes over 64-slot chunks (wave ballots give each lane its
+// rank among equal experts of lower lanes).
+__global__ void __launch_bounds__(64) k_perm_count(const int32_t* __restrict__ idx, int S, int ne,
+                                                   int32_t* __restrict__ counts) {
+    const int c = blockIdx.x, lane = threadIdx.x, s = c * 64 + lane;
+    const int e_l = s < S ? idx[s] : -1;
+    int mine = 0;
+    for (int e = 0; e < ne; ++e) {
+        const unsigned long long m = __ballot(e_l == e);
+        if (lane == e) mine = __popcll(m);
+    }
+    if (lane < ne) counts[(size_t)c * ne + lane] = mine;
+}
+
+// one wave: lane e scans its column; offsets = exclusive scan of totals;
+// tile table for the grouped GEMM (tiles of `bm` rows per expert segment).
+__global__ void __launch_bounds__(64) k_perm_scan(int32_t* __restrict__ counts, int nchunks, int ne, int S,
+                                                  int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
+                                                  int bm) {
+    const int e = threadIdx.x;
+    int run = 0;
+    if (e < ne)
+        for (int c = 0; c < nchunks; ++c) {
+            const int v = counts[(size_t)c * ne + e];
+            counts[(size_t)c * ne + e] = run;
+            run += v;
+        }
+    // exclusive scan over lanes
+    int incl = run;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (e >= o) incl += v;
+    }
+    const int excl = incl - run;
+    if (e < ne) {
+        offsets[e] = excl;
+        for (int c = 0; c < nchunks; ++c) counts[(size_t)c * ne + e] += excl;
+    }
+    if (e == 0) offsets[ne] = S;
+    __threadfence_block();
+    __syncthreads();
+    if (e == 0 && tiles) {
+        // tiles[0] = count, then (group, m0) pairs
+        int nt = 0;
+        for (int g = 0; g < ne; ++g) {
+            const int lo = offsets[g], hi = offsets[g + 1];
+            for (int m0 = lo; m0 < hi; m0 += bm) {
+                tiles[1 + 2 * nt] = g;
+                tiles[2 + 2 * nt] = m0;
+                ++nt;
+            }
+        }
+        tiles[0] = nt;
+    }
+}
+
+__global__ void __launch_bounds__(64) k_perm_scatter(const int32_t* __restrict__ idx, int S, int ne,
+                                                     const int32_t* __restrict__ base, int32_t* __restrict__ grouped,
+                                                     int32_t* __restrict__ pos_of_slot) {
+    const int c = blockIdx.x, lane = threadIdx.x, s = c * 64 + lane;
+    const int e_l = s < S ? idx[s] : -1;
+    int rank = 0;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int e = 0; e < ne; ++e) {
+        const unsigned long long m = __ballot(e_l == e);
+        if (e_l == e) rank = __popcll(m & below);
+    }
+    if (s < S) {
+        const int pos = base[(size_t)c * ne + e_l] + rank;
+        grouped[pos] = s;
+        if (pos_of_slot) pos_of_slot[s] = pos;
+    }
+}
+
+static int permute(const int32_t* idx, int S, int ne, int32_t* grouped, int32_t* offsets, int32_t* pos_of_slot,
+                   int32_t* tiles, int bm) {
+    const int nch = cdiv(S > 0 ? S : 1, 64);
+    int32_t* counts = (int32_t*)workspace(WS_MOE_PERM, (size_t)nch * ne * 4);
+    if (!counts) return fail(GH_ENOMEM, "moe permute: workspace");
+    hipLaunchKernelGGL(k_perm_count, dim3(nch), dim3(64), 0, stream(), idx, S, ne, counts);
+    hipLaunchKernelGGL(k_perm_scan, dim3(1), dim3(64), 0, stream(), counts, nch, ne, S, offsets, tiles, bm);
+    hipLaunchKernelGGL(k_perm_scatter, dim3(nch), dim3(64), 0, stream(), idx, S, ne, counts, grouped, pos_of_slot);
+    GH_LAUNCHED("k_perm_*");
+    return GH_OK;
+}
+
+// ====================================================== decode: grouped GEMV
+// Jobs 0..S-1 are routed slots (token s/K, expert idx[s]), jobs S..S+N-1 the
+// shared expert of token j-S. A wave computes RP rows of gate AND up of one
+// job with one activation chunk in registers, then writes silu(g)*u.
+struct GemvJobs {
+    const float* x;          // [N][d] (gate/up) or activations (down)
+    const int32_t* idx;      // [S]
+    int S, N, K, d;          // K = top-k
+    const uint8_t* wa;       // routed gate (or down) base
+    const uint8_t* wb;       // routed up base (gate/up only)
+    size_t estride;          // bytes per expert matrix
+    const uint8_t* sa;       // shared gate (or down), may be null
+    const uint8_t* sb;       // shared up
+    int rows_r, rows_s;      // rows of routed / shared matrices
+    int kin_r, kin_s;        // input length (K dim) of routed / shared
+    size_t rowb_r, rowb_s;   // bytes per weight row
+    float* out_r;            // [S][rows_r]
+    float* out_s;            // [N][rows_s]
+    const float* in_s;       // shared input (down: shared act)
+};
+
+template <int KIND, bool DUAL>
+__global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
+    const int job = blockIdx.y;
+    const bool shared = job >= J.S;
+    const int rows = shared ? J.rows_s : J.rows_r;
+    const int kin = shared ? J.kin_s : J.kin_r;
+    const size_t rowb = shared ? J.rowb_s : J.rowb_r;
+    const int T = kin / 64;
+    int LPR = 64;
+    while (LPR > 1 && LPR > T) LPR >>= 1;
+    const int RP = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rp = lane / LPR;
+    const int row = (blockIdx.x * 4 + wave) * RP + rp;
+    if ((blockIdx.x * 4 + wave) * RP >= rows) return;  // whole wave idle (uniform)
+    const int rr = row < rows ? row : rows - 1;
+    const float* xin;
+    const uint8_t *Wa, *Wb = nullptr;
+    if (shared) {
+        const int t = job - J.S;
+        xin = (DUAL ? J.x + (size_t)t * J.d : J.in_s + (size_t)t * kin);
+        Wa = J.sa;
+        if (DUAL) Wb = J.sb;
+    } else {
+        const int e = J.idx[job];
+        xin = DUAL ? J.x + (size_t)(job / J.K) * J.d : J.x + (size_t)job * kin;
+        Wa = J.wa + (size_t)e * J.estride;
+        if (DUAL) Wb = J.wb + (size_t)e * J.estride;
+    }
+    float ga = 0.f, ub = 0.f;
+    for (int t = sub; t < T; t += LPR) {
+        uint32_t w0[Task<KIND>::DW], w1[Task<KIND>::DW];
+        load_task<KIND>(Wa + (size_t)rr * rowb, t, w0);
+        if (DUAL) load_task<KIND>(Wb + (size_t)rr * rowb, t, w1);
+        float xv[64];
+        const float4* xp = (const float4*)(xin + (size_t)t * 64);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+        }
+        ga += task_dot<KIND>(w0, xv, t);
+        if (DUAL) ub += task_dot<KIND>(w1, xv, t);
+    }
+    for (int o = LPR >> 1; o > 0; o >>= 1) {
+        ga += __shfl_xor(ga, o, 64);
+        if (DUAL) ub += __shfl_xor(ub, o, 64);
+    }
+    if (sub == 0 && row < rows) {
+        const float v = DUAL ? ga / (1.0f + expf(-ga)) * ub : ga;
+        if (shared) J.out_s[(size_t)(job - J.S) * rows + row] = v;
+        else J.out_r[(size_t)job * rows + row] = v;
+    }
+}
+
+// out[t] = shared[t] + sum_k w[t,k] * y[slot(t,k)], k in order
+// (core/moe_cpu.cpp:265-287). pos maps a slot to its row in y (NULL: y is
+// in slot order).
+__global__ void k_moe_combine(const float* __restrict__ ysh, const float* __restrict__ y,
+                              const int32_t* __restrict__ pos, const float* __restrict__ w, float* __restrict__ out,
+                              int N, int K, int d) {
+    const int t = blockIdx.x;
+    for (int j = threadIdx.x; j < d; j += blockDim.x) {
+        float acc = ysh ? ysh[(size_t)t * d + j] : 0.f;
+        for (int k = 0; k < K; ++k) {
+            const int s = t * K + k;
+            const int r = pos ? pos[s] : s;
+            acc += w[s] * y[(size_t)r * d + j];
+        }
+        out[(size_t)t * d + j] = acc;
+    }
+}
+
+// ===================================================== prefill: grouped GEMM
+// Tiles of 128 grouped rows x (64 outputs, DUAL: gate and up interleaved per
+// wave so one lane holds matching g and u) x 64 K. Rows of a group come from
+// `gather` (slot ids -> token rows of x) or are contiguous.
+struct GroupGemm {
+    const float* A;            // activations
+    int lda;                   // row length of A (= K)
+    const int32_t* gather;     // grouped position -> slot id (row = slot / topk), or null
+    int topk;
+    const int32_t* tiles;      // [0]=count, then (group, m0)
+    const int32_t* offsets;    // group row ranges [g, g+1)
+    const uint8_t* W0;         // group g weights at W0 + g*gstride
+    const uint8_t* W1;         // DUAL: up
+    size_t gstride, rowb;
+    int K, N;                  // K = input length, N = output rows per group
+    float* out;                // [rows][N], row = grouped position
+};
+
+template <int KIND, bool DUAL>
+__global__ void __launch_bounds__(256) k_moe_group_gemm(GroupGemm P) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[BN * LDS_STRIDE];
+    const int tile = blockIdx.x;
+    if (tile >= P.tiles[0]) return;
+    const int g = P.tiles[1 + 2 * tile], m0 = P.tiles[2 + 2 * tile];
+    const int mend = P.offsets[g + 1];
+    const int NT = DUAL ? 64 : BN;  // output columns per block
+    const int n0 = blockIdx.y * NT;
+    if (n0 >= P.N) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = tid >> 1, lh = tid & 1;
+    const int am = m0 + lr;
+    const bool arow_ok = am < mend;
+    int arow = arow_ok ? am : m0;
+    if (P.gather) arow = P.gather[arow] / P.topk;
+    const float* xrow = P.A + (size_t)arow * P.lda;
+    // weight row of LDS row lr
+    int brow;
+    const uint8_t* Wm;
+    if (DUAL) {
+        const int wn = lr >> 6, r = lr & 63;
+        brow = n0 + 32 * wn + (r & 31);
+        Wm = (r < 32 ? P.W0 : P.W1) + (size_t)g * P.gstride;
+    } else {
+        brow = n0 + lr;
+        Wm = P.W0 + (size_t)g * P.gstride;
+    }
+    const bool brow_ok = brow < P.N;
+    const uint8_t* wrow = Wm + (size_t)(brow_ok ? brow : 0) * P.rowb;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int T = P.K / BK;
+    float4 xa[8];
+    WLoad<KIND> wl;
+    auto gload = [&](int t) {
+        const float4* xp = (const float4*)(xrow + (size_t)t * BK + lh * 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xa[i] = xp[i];
+        wl.load(wrow, t, lh);
+    };
+    gload(0);
+    for (int t = 0; t < T; ++t) {
+        {
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[4 * i] = xa[i].x; v[4 * i + 1] = xa[i].y; v[4 * i + 2] = xa[i].z; v[4 * i + 3] = xa[i].w;
+            }
+            if (!arow_ok) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = 0.f;
+            }
+            store_f16x32(sA + lr * LDS_STRIDE + lh * 32, v);
+            wl.decode(v);
+            if (!brow_ok) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = 0.f;
+            }
+            store_f16x32(sB + lr * LDS_STRIDE + lh * 32, v);
+        }
+        __syncthreads();
+        if (t + 1 < T) gload(t + 1);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int kofs = ks * 16 + (lane >> 5) * 8;
+            f16x8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = *(const f16x8*)(sA + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+                b[i] = *(const f16x8*)(sB + (wn + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (row >= mend) continue;
+            if (DUAL) {
+                const int col = n0 + 32 * (wave & 1) + (lane & 31);
+                if (col < P.N) {
+                    const float gv = acc[i][0][e], uv = acc[i][1][e];
+                    P.out[(size_t)row * P.N + col] = gv / (1.0f + expf(-gv)) * uv;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + j * 32 + (lane & 31);
+                    if (col < P.N) P.out[(size_t)row * P.N + col] = acc[i][j][e];
+                }
+            }
+        }
+    }
+}
+
+// tile table of one group covering rows [0, N)
+__global__ void k_single_group_tiles(int32_t* tiles, int32_t* offs, int N, int bm) {
+    const int nt = (N + bm - 1) / bm;
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+        tiles[1 + 2 * i] = 0;
+        tiles[2 + 2 * i] = i * bm;
+    }
+    if (threadIdx.x == 0) {
+        tiles[0] = nt;
+        offs[0] = 0;
+        offs[1] = N;
+    }
+}
+
+template <int KIND>
+static int moe_kind(const float* x, const float* w_route, const int32_t* idx, const void* gates, const void* ups,
+                    const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, float* out, int N, int d,
+                    int E, int ne, int K, int SH) {
+    const int S = N * K;
+    const bool has_sh = sh_g && sh_u && sh_d;
+    const size_t rowb_d = KIND == 4 ? (size_t)d * 2 : row_bytes(KIND, d);
+    const size_t rowb_E = KIND == 4 ? (size_t)E * 2 : row_bytes(KIND, E);
+    const size_t rowb_SH = KIND == 4 ? (size_t)SH * 2 : row_bytes(KIND, SH);
+    float* act = (float*)workspace(WS_MOE_ACT, (size_t)S * E * 4);
+    float* yr = (float*)workspace(WS_MOE_OUT, (size_t)S * d * 4);
+    float* shb = (float*)workspace(WS_MOE_SHARED, (size_t)N * ((size_t)SH + d) * 4);
+    if (!act || !yr || !shb) return fail(GH_ENOMEM, "moe: workspace");
+    float* sh_act = shb;
+    float* sh_y = shb + (size_t)N * SH;
+
+    if (N <= 8) {
+        // decode: two grouped GEMV launches (gate+up+SwiGLU, down) + combine
+        GemvJobs J{};
+        J.x = x; J.idx = idx; J.S = S; J.N = has_sh ? N : 0; J.K = K; J.d = d;
+        J.wa = (const uint8_t*)gates; J.wb = (const uint8_t*)ups; J.estride = (size_t)E * rowb_d;
+        J.sa = (const uint8_t*)sh_g; J.sb = (const uint8_t*)sh_u;
+        J.rows_r = E; J.rows_s = SH; J.kin_r = d; J.kin_s = d; J.rowb_r = rowb_d; J.rowb_s = rowb_d;
+        J.out_r = act; J.out_s = sh_act;
+        const int maxrows = has_sh ? (E > SH ? E : SH) : E;
+        auto rows_per_block = [&](int kin) {
+            int T = kin / 64, LPR = 64;
+            while (LPR > 1 && LPR > T) LPR >>= 1;
+            return 4 * (64 / LPR);
+        };
+        dim3 g1(cdiv(maxrows, rows_per_block(d)), S + J.N);
+        hipLaunchKernelGGL((k_moe_gemv<KIND, true>), g1, dim3(256), 0, stream(), J);
+        GH_LAUNCHED("k_moe_gemv(gate/up)");
+        GemvJobs D{};
+        D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
+        D.wa = (const uint8_t*)downs; D.estride = (size_t)d * rowb_E; D.sa = (const uint8_t*)sh_d;
+        D.rows_r = d; D.rows_s = d; D.kin_r = E; D.kin_s = SH; D.rowb_r = rowb_E; D.rowb_s = rowb_SH;
+        D.out_r = yr; D.out_s = sh_y; D.in_s = sh_act;
+        const int rpb = rows_per_block(E) < rows_per_block(SH) ? rows_per_block(E) : rows_per_block(SH);
+        dim3 g2(cdiv(d, rpb), S + D.N);
+        hipLaunchKernelGGL((k_moe_gemv<KIND, false>), g2, dim3(256), 0, stream(), D);
+        GH_LAUNCHED("k_moe_gemv(down)");
+        hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, nullptr,
+                           w_route, out, N, K, d);
+        GH_LAUNCHED("k_moe_combine");
+        return GH_OK;
+    }
+    // prefill: permutation, grouped gate/up GEMM, grouped down GEMM, combine
+    int32_t* perm = (int32_t*)workspace(WS_MOE_XG, ((size_t)2 * S + ne + 1 + 1 + 2 * ((size_t)S / BM + ne + 1)) * 4);
+    if (!perm) return fail(GH_ENOMEM, "moe: workspace");
+    int32_t* grouped = perm;
+    int32_t* pos = perm + S;
+    int32_t* offsets = pos + S;
+    int32_t* tiles = offsets + ne + 1;
+    const int max_tiles = S / BM + ne + 1;
+    int rc = permute(idx, S, ne, grouped, offsets, pos, tiles, BM);
+    if (rc) return rc;
+    GroupGemm P{};
+    P.A = x; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
+    P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
+    P.K = d; P.N = E; P.out = act;
+    hipLaunchKernelGGL((k_moe_group_gemm<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
+    GH_LAUNCHED("k_moe_group_gemm(gate/up)");
+    GroupGemm Q{};
+    Q.A = act; Q.lda = E; Q.gather = nullptr; Q.topk = 1; Q.tiles = tiles; Q.offsets = offsets;
+    Q.W0 = (const uint8_t*)downs; Q.gstride = (size_t)d * rowb_E; Q.rowb = rowb_E; Q.K = E; Q.N = d; Q.out = yr;
+    hipLaunchKernelGGL((k_moe_group_gemm<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
+    GH_LAUNCHED("k_moe_group_gemm(down)");
+    if (has_sh) {
+        // the shared expert is one group over all N tokens
+        int32_t* sh_tiles = (int32_t*)workspace(WS_MOE_H, ((size_t)2 * (N / BM + 2) + 1 + 2) * 4);
+        if (!sh_tiles) return fail(GH_ENOMEM, "moe: workspace");
+        int32_t* sh_off = sh_tiles + 2 * (N / BM + 2) + 1;
+        const int nt = cdiv(N, BM);
+        hipLaunchKernelGGL(k_single_group_tiles, dim3(1), dim3(64), 0, stream(), sh_tiles, sh_off, N, BM);
+        GH_LAUNCHED("k_single_group_tiles");
+        GroupGemm R{};
+        R.A = x; R.lda = d; R.gather = nullptr; R.topk = 1; R.tiles = sh_tiles; R.offsets = sh_off;
+        R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.gstride = 0; R.rowb = rowb_d;
+        R.K = d; R.N = SH; R.out = sh_act;
+        hipLaunchKernelGGL((k_moe_group_gemm<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
+        GroupGemm U{};
+        U.A = sh_act; U.lda = SH; U.gather = nullptr; U.topk = 1; U.tiles = sh_tiles; U.offsets = sh_off;
+        U.W0 = (const uint8_t*)sh_d; U.gstride = 0; U.rowb = rowb_SH; U.K = SH; U.N = d; U.out = sh_y;
+        hipLaunchKernelGGL((k_moe_group_gemm<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
+        GH_LAUNCHED("k_moe_group_gemm(shared)");
+    }
+    hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
+                       out, N, K, d);
+    GH_LAUNCHED("k_moe_combine");
+    return GH_OK;
+}
+
+int moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int N, int d,
+              int ne, int K) {
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(64), (size_t)d * 4, stream(), x, rw, bias, probs, idx, w, d, ne, K);
+    GH_LAUNCHED("k_route");
+    return GH_OK;
+}
+
+}  // namespace gh
+
+using namespace gh;
+
+extern "C" {
+
+int gh_moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int64_t N,
+                 int d, int ne, int K) {
+    GH_REQUIRE(K >= 1 && K <= 8, "moe_forward: K must be in [1,8]");
+    GH_REQUIRE(ne > 0 && ne <= 64, "moe_forward: ne out of range");
+    GH_REQUIRE(d > 0 && d % 4 == 0, "moe_forward: bad dims");
+    GH_REQUIRE(x && rw && idx && w, "moe_route: null pointer");
+    if (N <= 0) return GH_OK;
+    return moe_route(x, rw, bias, probs, idx, w, (int)N, d, ne, K);
+}
+
+int gh_moe_permute(const int32_t* idx, int64_t N, int K, int ne, int32_t* grouped, int32_t* offsets) {
+    GH_REQUIRE(idx && grouped && offsets && ne > 0 && ne <= 64 && K >= 1, "moe_permute: bad arguments");
+    return permute(idx, (int)(N * K), ne, grouped, offsets, nullptr, nullptr, BM);
+}
+
+int gh_moe_forward_bias_half(const float* x, const float* router_w, const float* router_bias, const void* gates,
+                             const void* ups, const void* downs, const void* sh_g, const void* sh_u,
+                             const void* sh_d, float* out, float* probs_cache, int32_t* idx_cache, float* w_cache,
+                             float* s_gate, float* s_up, float* s_act, int64_t N, int d, int E, int ne, int K, int SH,
+                             int qkind) {
+    (void)s_gate;
+    (void)s_up;
+    (void)s_act;
+    if (N <= 0) return GH_OK;
+    // core/moe_cpu.cpp:207-209
+    GH_REQUIRE(K >= 1 && K <= 8, "moe_forward: K must be in [1,8]");
+    GH_REQUIRE(ne > 0 && ne <= 64, "moe_forward: ne out of range");
+    GH_REQUIRE(d > 0 && E > 0, "moe_forward: bad dims");
+    GH_REQUIRE(x && router_w && gates && ups && downs && out, "moe_forward: null pointer");
+    GH_REQUIRE(qkind >= -1 && qkind <= 3, "moe_forward: unknown qkind %d", qkind);
+    const int bv = qkind == 3 ? 256 : 64;
+    const bool has_sh = sh_g && sh_u && sh_d;
+    GH_REQUIRE(d % bv == 0 && E % bv == 0 && (!has_sh || SH % bv == 0),
+               "moe_forward: d=%d, E=%d, SH=%d must be multiples of %d", d, E, SH, bv);
+    GH_REQUIRE(N <= 8192, "moe_forward: at most 8192 tokens per call");
+    const int S = (int)N * K;
+    int32_t* idx = idx_cache;
+    float* w = w_cache;
+    if (!idx || !w) {
+        char* r = (char*)workspace(WS_MOE_ROUTE, (size_t)S * 8);
+        if (!r) return fail(GH_ENOMEM, "moe: workspace");
+        if (!idx) idx = (int32_t*)r;
+        if (!w) w = (float*)(r + (size_t)S * 4);
+    }
+    int rc = moe_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
+    if (rc) return rc;
+    switch (qkind) {
+        case -1: return moe_kind<4>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
+        case 0: return moe_kind<0>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
+        case 1: return moe_kind<1>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
+        case 2: return moe_kind<2>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
+        default: return moe_kind<3>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
+    }
+}
+
+}  // extern "C"

@@ -35,8 +35,8 @@ hipStream_t stream() { return g_stream; }
 int num_cus() {
     if (g_cus == 0) {
         int dev = 0;
-        hipGetDevice(&dev);
-        hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev);
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (g_cus <= 0) g_cus = 256;
     }
     return g_cus;
@@ -54,8 +54,8 @@ void* workspace(int slot, size_t bytes) {
     if (w.bytes < bytes) {
         // grow-only; the old buffer may still be read by queued work
         if (w.ptr) {
-            hipStreamSynchronize(g_stream);
-            hipFree(w.ptr);
+            (void)hipStreamSynchronize(g_stream);
+            (void)hipFree(w.ptr);
         }
         size_t nb = bytes < 256 ? 256 : bytes;
         nb = (nb + 255) & ~(size_t)255;
@@ -70,9 +70,9 @@ void* workspace(int slot, size_t bytes) {
 }
 
 void free_workspaces() {
-    hipStreamSynchronize(g_stream);
+    (void)hipStreamSynchronize(g_stream);
     for (Workspace& w : g_ws) {
-        if (w.ptr) hipFree(w.ptr);
+        if (w.ptr) (void)hipFree(w.ptr);
         w = Workspace{};
     }
 }

@@ -162,7 +162,9 @@ struct Xoshiro {
 // four 8-lane FMA accumulators over 32-wide strides, lane-wise combine
 // (s0+s1)+(s2+s3), fold the two 128-bit halves, then movehl + shuffle, then
 // a scalar tail. core/simd_cpu.h:84-99 is the scalar 4-way path for n < 32.
-float dot_f32(const float* a, const float* b, int n) {
+// (std::fma is compiled to the FMA3 instruction here, as in the reference's
+// AVX2 kernel; the result is exactly rounded either way.)
+__attribute__((target("avx2,fma"))) float dot_f32(const float* a, const float* b, int n) {
     if (n >= 32) {
         float acc[4][8] = {};
         const int n32 = n & ~31;
@@ -193,7 +195,7 @@ float dot_f32(const float* a, const float* b, int n) {
 }
 
 // core/simd_cpu.h:53-75 and :101-117 (y += a*x)
-void axpy_f32(float* y, const float* x, float a, int n) {
+__attribute__((target("avx2,fma"))) void axpy_f32(float* y, const float* x, float a, int n) {
     int i = 0;
     if (n >= 32) {
         const int n32 = n & ~31;

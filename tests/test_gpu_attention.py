@@ -1,0 +1,190 @@
+"""GPU parity of GQA attention against the CPU oracle (and through it the
+reference's golden fixtures): decode over the fp16 ring cache (fp32
+accumulate, normwise rel-err 1e-3), paged bf16 ragged decode (1e-3), causal
+prefill (bf16 MFMA operands, 2e-2; the generic fp32 kernel 1e-3)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import golden, relerr
+
+pytestmark = pytest.mark.gpu
+
+
+def ring_decode(gh, q, kc, vc, H, KV, hd, rs, pin, cl, cm, sc, win):
+    dq, dk, dv = gh.Buf.from_array(q), gh.Buf.from_array(kc), gh.Buf.from_array(vc)
+    out = gh.Buf.zeros(H * hd, np.float32)
+    gh.call("gh_attention_decode_ring_fp16", dq.p, dk.p, dv.p, out.p, H, KV, hd, rs, pin, cl, cm, gh.fl(sc), None,
+            win)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("tag", ["r0", "r1", "r2", "r3", "r4"])
+def test_decode_ring_golden(gh, tag):
+    g = golden("attention")
+    H, KV, hd, rs, pin, cl, cm, win = [int(v) for v in g[f"{tag}_shape"]]
+    got = ring_decode(gh, g[f"{tag}_q"], g[f"{tag}_k"], g[f"{tag}_v"], H, KV, hd, rs, pin, cl, cm,
+                      float(g[f"{tag}_scale"]), win)
+    assert relerr(got, g[f"{tag}_out"]) <= 1e-3
+
+
+def _oracle_ring(q, kc, vc, H, KV, hd, rs, pin, cl, cm, sc, win):
+    out = np.zeros(H * hd, np.float32)
+    assert O.oracle().orc_attention_decode_ring_fp16(O.P(q), O.P(kc), O.P(vc), O.P(out), H, KV, hd, rs, pin, cl, cm,
+                                                     O.f(sc), win) == 0
+    return out
+
+
+@pytest.mark.parametrize("L", [1024, 8192, 32768])
+def test_decode_c4_lengths(gh, L):
+    """BASELINE config 4 decode, batch 1 (fp16 ring cache, no wrap)."""
+    H, KV, hd = 32, 8, 128
+    q = O.rng_normal(4, H * hd)
+    kc = O.f32_to_f16(O.rng_normal(41, L * KV * hd))
+    vc = O.f32_to_f16(O.rng_normal(42, L * KV * hd))
+    sc = 1.0 / np.sqrt(hd)
+    got = ring_decode(gh, q, kc, vc, H, KV, hd, 0, 8, L, L, sc, 0)
+    assert relerr(got, _oracle_ring(q, kc, vc, H, KV, hd, 0, 8, L, L, sc, 0)) <= 1e-3
+
+
+def test_decode_ring_rotation_invariance(gh):
+    """The same logical sequence stored at two ring rotations gives the same output."""
+    H, KV, hd, cm, pin = 8, 2, 64, 300, 8
+    L = cm
+    q = O.rng_normal(5, H * hd)
+    kl = O.rng_normal(51, L * KV * hd).reshape(L, KV * hd)
+    vl = O.rng_normal(52, L * KV * hd).reshape(L, KV * hd)
+    outs = []
+    for rs in (0, 37, 291):
+        kc = np.zeros_like(kl)
+        vc = np.zeros_like(vl)
+        for j in range(L):
+            slot = j if j < pin else pin + (rs + j - pin) % (cm - pin)
+            kc[slot], vc[slot] = kl[j], vl[j]
+        outs.append(ring_decode(gh, q, O.f32_to_f16(kc.ravel()), O.f32_to_f16(vc.ravel()), H, KV, hd, rs, pin, L,
+                                cm, 0.125, 0))
+    assert relerr(outs[1], outs[0]) <= 1e-5 and relerr(outs[2], outs[0]) <= 1e-5
+
+
+def test_decode_edge_cases(gh):
+    H, KV, hd = 4, 2, 64
+    q = O.rng_normal(6, H * hd)
+    kc = O.f32_to_f16(O.rng_normal(61, 16 * KV * hd))
+    vc = O.f32_to_f16(O.rng_normal(62, 16 * KV * hd))
+    # cur_len = 1: out = v[0] for every head of the kv group
+    got = ring_decode(gh, q, kc, vc, H, KV, hd, 0, 0, 1, 16, 0.125, 0)
+    v0 = O.f16_to_f32(vc[:KV * hd]).reshape(KV, hd)
+    assert np.allclose(got.reshape(H, hd), np.repeat(v0, H // KV, axis=0), atol=1e-6)
+    # empty context: zeros
+    got = ring_decode(gh, q, kc, vc, H, KV, hd, 0, 0, 0, 16, 0.125, 0)
+    assert np.all(got == 0)
+    # a zero query gives the mean of v
+    got = ring_decode(gh, np.zeros(H * hd, np.float32), kc, vc, H, KV, hd, 0, 0, 16, 16, 0.125, 0)
+    vm = O.f16_to_f32(vc).reshape(16, KV, hd).mean(0)
+    assert np.allclose(got.reshape(H, hd), np.repeat(vm, H // KV, axis=0), atol=1e-5)
+    # argument checks of core/attn_cpu.cpp:211-222 fail loudly
+    with pytest.raises(gh.GHError):
+        ring_decode(gh, q, kc, vc, H, KV, hd, 0, 5, 3, 16, 0.125, 0)  # pinned > cur_len
+    with pytest.raises(gh.GHError):
+        ring_decode(gh, q, kc, vc, H, KV, hd, 0, 0, 17, 16, 0.125, 0)  # cur_len > cache_max
+
+
+def paged_case(n_seqs, lens, H, KV, hd, page_size, seed):
+    max_pages = int(max(1, (max(lens) + page_size - 1) // page_size))
+    n_pages = sum((L + page_size - 1) // page_size for L in lens) + 3
+    perm = O.rng_below(seed, n_pages * 4, n_pages)
+    # distinct pages per sequence in a scrambled order
+    order = list(dict.fromkeys(perm.tolist())) + [p for p in range(n_pages) if p not in set(perm.tolist())]
+    pt = np.zeros((n_seqs, max_pages), np.int32)
+    k = 0
+    for s, L in enumerate(lens):
+        for i in range((L + page_size - 1) // page_size):
+            pt[s, i] = order[k]
+            k += 1
+    kp = O.f32_to_bf16(O.rng_normal(seed + 1, n_pages * page_size * KV * hd))
+    vp = O.f32_to_bf16(O.rng_normal(seed + 2, n_pages * page_size * KV * hd))
+    q = O.rng_normal(seed + 3, n_seqs * H * hd)
+    return q, kp, vp, pt, np.array(lens, np.int32), max_pages
+
+
+def run_paged(gh, q, kp, vp, pt, lens, max_pages, page_size, H, KV, hd, sc):
+    bufs = [gh.Buf.from_array(a) for a in (q, kp, vp, pt, lens)]
+    out = gh.Buf.zeros(len(lens) * H * hd, np.float32)
+    gh.call("gh_attention_decode_paged_bf16", *[b.p for b in bufs], len(lens), max_pages, page_size, int(lens.max()),
+            out.p, H, KV, hd, gh.fl(sc))
+    return out.numpy()
+
+
+def oracle_paged(q, kp, vp, pt, lens, max_pages, page_size, H, KV, hd, sc):
+    out = np.zeros(len(lens) * H * hd, np.float32)
+    assert O.oracle().orc_attention_decode_paged_bf16(O.P(q), O.P(kp), O.P(vp), O.P(pt), O.P(lens), len(lens),
+                                                      max_pages, page_size, O.P(out), H, KV, hd, O.f(sc)) == 0
+    return out
+
+
+def test_paged_small(gh):
+    H, KV, hd, ps = 8, 2, 64, 16
+    lens = [1, 17, 200, 0, 64]
+    args = paged_case(len(lens), lens, H, KV, hd, ps, 70)
+    got = run_paged(gh, *args, ps, H, KV, hd, 0.125)
+    assert relerr(got, oracle_paged(*args, ps, H, KV, hd, 0.125)) <= 1e-3
+
+
+def test_paged_c4_ragged_batch16(gh):
+    """ragged decode, 16 sequences, lengths U[512, 8192]."""
+    H, KV, hd, ps = 32, 8, 128, 64
+    lens = (512 + O.rng_below(4, 16, 8192 - 512 + 1)).tolist()
+    args = paged_case(16, lens, H, KV, hd, ps, 80)
+    sc = 1.0 / np.sqrt(hd)
+    got = run_paged(gh, *args, ps, H, KV, hd, sc)
+    assert relerr(got, oracle_paged(*args, ps, H, KV, hd, sc)) <= 1e-3
+
+
+def prefill(gh, q, k, v, B, T, H, KV, hd, sc, win):
+    dq, dk, dv = gh.Buf.from_array(q), gh.Buf.from_array(k), gh.Buf.from_array(v)
+    out = gh.Buf.zeros(B * T * H * hd, np.float32)
+    gh.call("gh_attention_forward_ex", dq.p, dk.p, dv.p, out.p, None, B, T, H, KV, hd, gh.fl(sc), win, None)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("tag", ["a", "b", "c"])
+def test_prefill_golden(gh, tag):
+    g = golden("attention")
+    T, H, KV, hd, win = [int(v) for v in g[f"pf{tag}_shape"]]
+    got = prefill(gh, g[f"pf{tag}_q"], g[f"pf{tag}_k"], g[f"pf{tag}_v"], 1, T, H, KV, hd, float(g[f"pf{tag}_scale"]),
+                  win)
+    tol = 2e-2 if hd in (64, 128) else 1e-3
+    assert relerr(got, g[f"pf{tag}_out"]) <= tol
+
+
+@pytest.mark.parametrize("B,T,H,KV,hd,win", [(1, 200, 8, 2, 64, 0), (2, 130, 4, 4, 128, 0), (1, 300, 8, 2, 64, 77),
+                                             (1, 1, 4, 1, 128, 0)])
+def test_prefill_mfma_vs_oracle(gh, B, T, H, KV, hd, win):
+    q = O.rng_normal(90, B * T * H * hd)
+    k = O.rng_normal(91, B * T * KV * hd)
+    v = O.rng_normal(92, B * T * KV * hd)
+    sc = 1.0 / np.sqrt(hd)
+    got = prefill(gh, q, k, v, B, T, H, KV, hd, sc, win)
+    ref = np.zeros_like(q)
+    O.oracle().orc_attention_forward_ex(O.P(q), O.P(k), O.P(v), O.P(ref), B, T, H, KV, hd, O.f(sc), win)
+    assert relerr(got, ref) <= 2e-2
+
+
+def test_prefill_c4_rows_match_decode(gh):
+    """BASELINE config 4 causal prefill, T=4096: row t equals decode with
+    cur_len = t+1 over the same (fp32 -> widened) keys, checked on sampled rows."""
+    T, H, KV, hd = 4096, 32, 8, 128
+    q = O.rng_normal(93, T * H * hd)
+    kf = O.rng_normal(94, T * KV * hd)
+    vf = O.rng_normal(95, T * KV * hd)
+    # use fp16-representable K/V so the fp16 decode path sees identical values
+    kh, vh = O.f32_to_f16(kf), O.f32_to_f16(vf)
+    k, v = O.f16_to_f32(kh), O.f16_to_f32(vh)
+    sc = 1.0 / np.sqrt(hd)
+    got = prefill(gh, q, k, v, 1, T, H, KV, hd, sc, 0).reshape(T, H * hd)
+    for t in (0, 1, 127, 128, 2047, 4095):
+        qt = np.ascontiguousarray(q.reshape(T, H * hd)[t])
+        ref = _oracle_ring(qt, kh, vh, H, KV, hd, 0, 0, t + 1, T, sc, 0)
+        assert relerr(got[t], ref) <= 2e-2, t
