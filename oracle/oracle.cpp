@@ -37,6 +37,7 @@
 #include "oracle.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -987,6 +988,16 @@ void orc_synth_param_f32(const char* name, uint64_t seed, float* out, int64_t n)
 int orc_granite_generate(const int32_t* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
                          const int32_t* prompt, int P, int n_new, int max_ctx, int32_t* out_ids,
                          float* out_margins) {
+    return orc_granite_generate_timed(cfg, fcfg, names, ptrs, nparams, prompt, P, n_new, max_ctx, out_ids,
+                                      out_margins, nullptr);
+}
+
+// As above; seconds (optional): [0] prefill wall time, [1] decode wall time.
+int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char** names, const void** ptrs,
+                               int nparams, const int32_t* prompt, int P, int n_new, int max_ctx, int32_t* out_ids,
+                               float* out_margins, double* seconds) {
+    using clk = std::chrono::steady_clock;
+    const auto t_start = clk::now();
     const int V = cfg[0], d = cfg[1], L = cfg[2], H = cfg[3], KV = cfg[4], hd = cfg[5], E = cfg[6], ne = cfg[7],
               K = cfg[8], SH = cfg[9], di = cfg[10], mh = cfg[11], mdh = cfg[12], mds = cfg[13], ck = cfg[14],
               qk = cfg[15];
@@ -1076,6 +1087,7 @@ int orc_granite_generate(const int32_t* cfg, const float* fcfg, const char** nam
         len = P;
         finish(x.data() + (size_t)(P - 1) * d);
     }
+    const auto t_prefill = clk::now();
     // ---- greedy decode (generator.cpp:985-1098 greedy + :221-443)
     std::vector<float> x((size_t)d), xb((size_t)d), pr((size_t)d), q((size_t)qd), k((size_t)kvd), v((size_t)kvd),
         att((size_t)qd);
@@ -1117,6 +1129,10 @@ int orc_granite_generate(const int32_t* cfg, const float* fcfg, const char** nam
             for (int i = 0; i < d; ++i) x[(size_t)i] += pr[(size_t)i];
         }
         finish(x.data());
+    }
+    if (seconds) {
+        seconds[0] = std::chrono::duration<double>(t_prefill - t_start).count();
+        seconds[1] = std::chrono::duration<double>(clk::now() - t_prefill).count();
     }
     return 0;
 }

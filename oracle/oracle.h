@@ -93,6 +93,10 @@ void orc_synth_param_f32(const char* name, uint64_t seed, float* out, int64_t n)
 int  orc_granite_generate(const int32_t* cfg, const float* fcfg, const char** names,
                           const void** ptrs, int nparams, const int32_t* prompt, int P,
                           int n_new, int max_ctx, int32_t* out_ids, float* out_margins);
+int  orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char** names,
+                                const void** ptrs, int nparams, const int32_t* prompt, int P,
+                                int n_new, int max_ctx, int32_t* out_ids, float* out_margins,
+                                double* seconds);
 
 #ifdef __cplusplus
 }

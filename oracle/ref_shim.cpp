@@ -1,8 +1,9 @@
 // extern "C" shim over the genuine reference engine's CPU path, compiled
 // from /root/reference by oracle/ref.mk into oracle/_ref/libgai_ref.so.
-// TEST INFRASTRUCTURE ONLY: tests/golden/make_golden.py loads it in this
-// container to write golden fixtures. It never travels to the GPU box in a
-// form anything loads there (the fixtures do), and the product never links it.
+// TEST INFRASTRUCTURE ONLY: tests/golden/make_golden.py loads it in the build
+// container to write golden fixtures, and bench.py's cpu_baseline leg times
+// the reference CPU Generator through it (the built .so travels with the
+// tree; no reference source does). The product never links it.
 //
 // The Generator's per-token host path is private in the reference; the shim
 // reaches it by opening the class (test code only), so the greedy loop below
@@ -135,8 +136,21 @@ int ref_moe_forward_bias_half(const float* x, const float* rw, const float* bias
 // cfg / fcfg use the same layout as orc_granite_generate (oracle/oracle.h).
 // Parameters are set by name from caller buffers holding the storage bytes
 // (Q-kind blocks for matrices, fp16 for tok_embeddings, fp32 for vectors).
+int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
+                               const i32* prompt, int P, int n_new, int max_ctx, i32* out_ids, float* out_margins,
+                               double* seconds);
+
 int ref_granite_generate(const i32* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
                          const i32* prompt, int P, int n_new, int max_ctx, i32* out_ids, float* out_margins) {
+    return ref_granite_generate_timed(cfg, fcfg, names, ptrs, nparams, prompt, P, n_new, max_ctx, out_ids,
+                                      out_margins, nullptr);
+}
+
+// seconds (optional): [0] prefill wall time, [1] wall time of the n_new-1
+// decode steps (Generator::decode_step on the host path).
+int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
+                               const i32* prompt, int P, int n_new, int max_ctx, i32* out_ids, float* out_margins,
+                               double* seconds) {
     try {
         ModelConfig c;
         c.arch = ModelConfig::ArchGranite;
@@ -178,7 +192,10 @@ int ref_granite_generate(const i32* cfg, const float* fcfg, const char** names, 
         Tokenizer tok;
         Generator g(m, tok, max_ctx);
         std::vector<i32> pr(prompt, prompt + P);
+        Timer tp;
         g.prefill(pr);
+        if (seconds) seconds[0] = tp.seconds();
+        Timer td;
         const int V = c.vocab_size;
         for (int step = 0; step < n_new; ++step) {
             const float* lg = g.logits_host_.data();
@@ -196,6 +213,7 @@ int ref_granite_generate(const i32* cfg, const float* fcfg, const char** names, 
             g.decode_step(next, (int)g.absolute_pos_);
             ++g.absolute_pos_;
         }
+        if (seconds) seconds[1] = td.seconds();
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_granite_generate: %s\n", e.what());
         return -2;

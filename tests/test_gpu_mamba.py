@@ -159,7 +159,7 @@ def test_mamba_step_vs_oracle(gh, shape):
                                             conv_dim, nh, dh, ds, k, O.f(1e-5), kind) == 0
         assert relerr(out.numpy(), ref) <= 1e-3, step
     assert relerr(dssm.numpy(), rssm) <= 1e-3
-    assert np.array_equal(dconv.numpy(), rconv)
+    assert relerr(dconv.numpy(), rconv) <= 1e-3  # the window holds raw in_proj outputs (GEMV rounding)
 
 
 def test_mamba_prefill_equals_steps(gh):
