@@ -202,28 +202,45 @@ __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
 }
 
 // Merge the split partials: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
+// One block per (head, sequence): the split weights are computed once into
+// LDS, then every thread reduces one channel over the splits (coalesced).
 // An empty context (no positions) gives zeros (core/attn_cpu.cpp:244-246).
-__global__ void k_attn_combine(const float* __restrict__ o_part, const float* __restrict__ ml, float* __restrict__ out,
-                               int H, int KV, int G, int splits, int hd) {
+constexpr int COMB_MAX_SPLITS = 1024;
+__global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ o_part, const float* __restrict__ ml,
+                                                      float* __restrict__ out, int H, int KV, int G, int splits,
+                                                      int hd) {
+    __shared__ float sw[COMB_MAX_SPLITS];
+    __shared__ float red[4];
     const int h = blockIdx.x, seq = blockIdx.y;
     const int kvh = h / G, g = h % G;
     const size_t base = ((size_t)seq * KV + kvh) * splits;
     float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) {
+    for (int s = threadIdx.x; s < splits; s += 256) {
         const float* p = ml + ((base + s) * G + g) * 2;
         if (p[1] > 0.f) M = fmaxf(M, p[0]);
     }
+    M = wave_max(M);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
     float L = 0.f;
-    for (int s = 0; s < splits; ++s) {
+    for (int s = threadIdx.x; s < splits; s += 256) {
         const float* p = ml + ((base + s) * G + g) * 2;
-        if (p[1] > 0.f) L += expf(p[0] - M) * p[1];
+        const float w = p[1] > 0.f ? expf(p[0] - M) : 0.f;
+        sw[s] = w;
+        L += w * p[1];
     }
+    L = wave_sum(L);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = L;
+    __syncthreads();
+    L = red[0] + red[1] + red[2] + red[3];
     const float inv = L > 0.f ? 1.0f / L : 0.0f;
-    for (int c = threadIdx.x; c < hd; c += blockDim.x) {
+    for (int c = threadIdx.x; c < hd; c += 256) {
         float acc = 0.f;
         for (int s = 0; s < splits; ++s) {
-            const float* p = ml + ((base + s) * G + g) * 2;
-            if (p[1] > 0.f) acc += expf(p[0] - M) * o_part[((base + s) * G + g) * hd + c];
+            const float w = sw[s];
+            if (w != 0.f) acc += w * o_part[((base + s) * G + g) * hd + c];
         }
         out[((size_t)seq * H + h) * hd + c] = acc * inv;
     }
@@ -231,11 +248,11 @@ __global__ void k_attn_combine(const float* __restrict__ o_part, const float* __
 
 static int pick_chunk(int len, int blocks_other) {
     // enough blocks to fill the chip, runs of 64..512 positions
-    const int target = 4 * num_cus();
+    const int target = 2 * num_cus();
     int per = cdiv(target, blocks_other > 0 ? blocks_other : 1);
     int chunk = cdiv(len > 0 ? len : 1, per > 0 ? per : 1);
     chunk = (chunk + 63) / 64 * 64;
-    if (chunk < 64) chunk = 64;
+    if (chunk < 128) chunk = 128;
     if (chunk > DEC_CHUNK_MAX) chunk = DEC_CHUNK_MAX;
     return chunk;
 }
@@ -258,8 +275,8 @@ static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
         default: return fail(GH_EUNSUPPORTED, "attention decode: head_dim %d (supported: 16, 32, 64, 128)", hd);
     }
     GH_LAUNCHED("k_attn_decode");
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.H, S), dim3(hd < 256 ? hd : 256), 0, stream(), o, ml, out, a.H, a.KV,
-                       a.G, a.splits, hd);
+    if (a.splits > COMB_MAX_SPLITS) return fail(GH_EUNSUPPORTED, "attention decode: %d splits", a.splits);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.H, S), dim3(256), 0, stream(), o, ml, out, a.H, a.KV, a.G, a.splits, hd);
     GH_LAUNCHED("k_attn_combine");
     return GH_OK;
 }

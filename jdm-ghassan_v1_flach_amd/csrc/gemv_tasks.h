@@ -12,82 +12,89 @@ constexpr int KF16 = 4, KF32 = 5;
 template <int KIND>
 struct Task;  // bytes per 64-value task and the dot of one task
 
-__device__ __forceinline__ float i8f(uint32_t w, int b) {  // signed byte b of w
-    return (float)(int)__builtin_amdgcn_sbfe((int)w, 8 * b, 8);
-}
-__device__ __forceinline__ float u4f(uint32_t w, int n) {  // nibble n of w
-    return (float)__builtin_amdgcn_ubfe(w, 4 * n, 4);
-}
+// Unsigned byte b of a dword as float: compiles to v_cvt_f32_ubyte{b}.
+__device__ __forceinline__ float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
 
-// Q8_0: two 34-byte blocks. dwords: [d0|q0 q1][q2..q5]...; block 1 starts at byte 34.
+// The dot of one task: w = raw dwords, x = 64 activations, xs = sums of
+// x[0..31] and x[32..63] (computed once per task and reused by every row).
+// Integer codes are turned into floats straight from bytes (low nibbles by
+// masking 0x0F0F0F0F, high nibbles by shifting first, signed Q8_0 bytes by
+// flipping the sign bit: q = u - 128), so a weight costs about one convert
+// and one FMA.
+
+// Q8_0: two 34-byte blocks; block 0 quants are stream bytes 2..33, block 1
+// quants 36..67, scales at bytes 0-1 and 34-35.
 template <>
 struct Task<2> {
     static constexpr int DW = 17;
-    __device__ static float dot(const uint32_t* w, const float* x) {
-        auto byte = [&](int b) { return i8f(w[b >> 2], b & 3); };
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs) {
+        uint32_t u[17];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) u[i] = w[i] ^ 0x80808080u;
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) s0 = fmaf(x[i], byte(2 + i), s0);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) s1 = fmaf(x[32 + i], byte(36 + i), s1);
+        for (int i = 0; i < 32; ++i) {
+            const int b0 = 2 + i, b1 = 36 + i;
+            s0 = fmaf(x[i], ub(u[b0 >> 2], b0 & 3), s0);
+            s1 = fmaf(x[32 + i], ub(u[b1 >> 2], b1 & 3), s1);
+        }
         const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF));
         const float d1 = f16_to_f32((uint16_t)(w[8] >> 16));
-        return fmaf(d0, s0, d1 * s1);
+        return d0 * fmaf(-128.f, xs[0], s0) + d1 * fmaf(-128.f, xs[1], s1);
     }
 };
-// Q4_0: two 18-byte blocks; low nibble = value j, high nibble = j+16.
+// Q4_0: two 18-byte blocks; low nibble = value j, high nibble = j+16,
+// value = (q - 8) * d.
 template <>
 struct Task<0> {
     static constexpr int DW = 9;
-    __device__ static float dot(const uint32_t* w, const float* x) {
-        auto nib = [&](int byte, int hi) {
-            return (float)__builtin_amdgcn_ubfe(w[byte >> 2], 8 * (byte & 3) + 4 * hi, 4);
-        };
-        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs) {
+        // block 0 nibble bytes are stream bytes 2..17, block 1 bytes 20..35
+        auto byte = [&](int b) { return (w[b >> 2] >> (8 * (b & 3))) & 0xFFu; };
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            s0 = fmaf(x[j], nib(2 + j, 0), s0);
-            s0 = fmaf(x[j + 16], nib(2 + j, 1), s0);
-            s1 = fmaf(x[32 + j], nib(20 + j, 0), s1);
-            s1 = fmaf(x[48 + j], nib(20 + j, 1), s1);
+            const uint32_t b0 = byte(2 + j), b1 = byte(20 + j);
+            s0 = fmaf(x[j], (float)(b0 & 0xF), s0);
+            s0 = fmaf(x[j + 16], (float)(b0 >> 4), s0);
+            s1 = fmaf(x[32 + j], (float)(b1 & 0xF), s1);
+            s1 = fmaf(x[48 + j], (float)(b1 >> 4), s1);
         }
-#pragma unroll
-        for (int j = 0; j < 32; ++j) { x0 += x[j]; x1 += x[32 + j]; }
         const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF));
         const float d1 = f16_to_f32((uint16_t)(w[4] >> 16));
-        // sum x*(q-8)*d = d*(sum x*q - 8*sum x)
-        return d0 * fmaf(-8.f, x0, s0) + d1 * fmaf(-8.f, x1, s1);
+        return d0 * fmaf(-8.f, xs[0], s0) + d1 * fmaf(-8.f, xs[1], s1);
     }
 };
-// Q4_1: two 20-byte blocks, value = q*d + m.
+// Q4_1: two 20-byte blocks (4-byte aligned), value = q*d + m.
 template <>
 struct Task<1> {
     static constexpr int DW = 10;
-    __device__ static float dot(const uint32_t* w, const float* x) {
-        auto nib = [&](int byte, int hi) {
-            return (float)__builtin_amdgcn_ubfe(w[byte >> 2], 8 * (byte & 3) + 4 * hi, 4);
-        };
-        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs) {
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            s0 = fmaf(x[j], nib(4 + j, 0), s0);
-            s0 = fmaf(x[j + 16], nib(4 + j, 1), s0);
-            s1 = fmaf(x[32 + j], nib(24 + j, 0), s1);
-            s1 = fmaf(x[48 + j], nib(24 + j, 1), s1);
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo0 = w[1 + i] & 0x0F0F0F0Fu, hi0 = (w[1 + i] >> 4) & 0x0F0F0F0Fu;
+            const uint32_t lo1 = w[6 + i] & 0x0F0F0F0Fu, hi1 = (w[6 + i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * i + b;
+                s0 = fmaf(x[j], ub(lo0, b), s0);
+                s0 = fmaf(x[j + 16], ub(hi0, b), s0);
+                s1 = fmaf(x[32 + j], ub(lo1, b), s1);
+                s1 = fmaf(x[48 + j], ub(hi1, b), s1);
+            }
         }
-#pragma unroll
-        for (int j = 0; j < 32; ++j) { x0 += x[j]; x1 += x[32 + j]; }
         const float d0 = f16_to_f32((uint16_t)(w[0] & 0xFFFF)), m0 = f16_to_f32((uint16_t)(w[0] >> 16));
         const float d1 = f16_to_f32((uint16_t)(w[5] & 0xFFFF)), m1 = f16_to_f32((uint16_t)(w[5] >> 16));
-        return fmaf(d0, s0, m0 * x0) + fmaf(d1, s1, m1 * x1);
+        return fmaf(d0, s0, m0 * xs[0]) + fmaf(d1, s1, m1 * xs[1]);
     }
 };
-// Q4_K: w[0..3] = block header (d, dmin, scales[12]); w[4..11] = 32 bytes of
-// nibbles holding sub-blocks 2p (low) and 2p+1 (high); p is passed in.
+// Q4_K: w[0..3] = block header (d, dmin, scales[12]); w[4..11] = the 32
+// nibble bytes holding sub-blocks 2p (low nibbles) and 2p+1 (high nibbles).
 template <>
 struct Task<3> {
     static constexpr int DW = 12;
-    __device__ static float dot(const uint32_t* w, const float* x, int p) {
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs, int p) {
         auto scb = [&](int i) { return (int)((w[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFF); };
         auto scale_min = [&](int s, int& sc, int& m) {
             if (s < 4) {
@@ -98,27 +105,29 @@ struct Task<3> {
                 m = (scb(s + 4) >> 4) | ((scb(s) >> 6) << 4);
             }
         };
-        float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int l = 0; l < 32; ++l) {
-            const uint32_t dw = w[4 + (l >> 2)];
-            s0 = fmaf(x[l], (float)__builtin_amdgcn_ubfe(dw, 8 * (l & 3), 4), s0);
-            s1 = fmaf(x[32 + l], (float)__builtin_amdgcn_ubfe(dw, 8 * (l & 3) + 4, 4), s1);
-            x0 += x[l];
-            x1 += x[32 + l];
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = w[4 + i] & 0x0F0F0F0Fu, hi = (w[4 + i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                s0 = fmaf(x[4 * i + b], ub(lo, b), s0);
+                s1 = fmaf(x[32 + 4 * i + b], ub(hi, b), s1);
+            }
         }
         const float d = f16_to_f32((uint16_t)(w[0] & 0xFFFF)), dmin = f16_to_f32((uint16_t)(w[0] >> 16));
         int sc0, m0, sc1, m1;
         scale_min(2 * p, sc0, m0);
         scale_min(2 * p + 1, sc1, m1);
         // sum x*(d*sc*q - dmin*m) = d*sc*sum(x q) - dmin*m*sum(x)
-        return d * ((float)sc0 * s0 + (float)sc1 * s1) - dmin * ((float)m0 * x0 + (float)m1 * x1);
+        return d * ((float)sc0 * s0 + (float)sc1 * s1) - dmin * ((float)m0 * xs[0] + (float)m1 * xs[1]);
     }
 };
 template <>
 struct Task<KF16> {
     static constexpr int DW = 32;
-    __device__ static float dot(const uint32_t* w, const float* x) {
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs) {
+        (void)xs;
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
@@ -131,13 +140,32 @@ struct Task<KF16> {
 template <>
 struct Task<KF32> {
     static constexpr int DW = 64;
-    __device__ static float dot(const uint32_t* w, const float* x) {
+    __device__ static float dot(const uint32_t* w, const float* x, const float* xs) {
+        (void)xs;
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 64; ++i) s = fmaf(x[i], __builtin_bit_cast(float, w[i]), s);
         return s;
     }
 };
+
+// sums of the two 32-value halves of a task's activations (only the
+// affine codecs need them)
+template <int KIND>
+__device__ __forceinline__ void task_xsum(const float* x, float* xs) {
+    if constexpr (KIND == KF16 || KIND == KF32) {
+        xs[0] = xs[1] = 0.f;
+    } else {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            a += x[i];
+            b += x[32 + i];
+        }
+        xs[0] = a;
+        xs[1] = b;
+    }
+}
 
 template <int KIND>
 __device__ __forceinline__ void load_task(const uint8_t* row, int t, uint32_t* w) {
@@ -164,9 +192,9 @@ __device__ __forceinline__ void load_task(const uint8_t* row, int t, uint32_t* w
 }
 
 template <int KIND>
-__device__ __forceinline__ float task_dot(const uint32_t* w, const float* x, int t) {
-    if constexpr (KIND == 3) return Task<3>::dot(w, x, t & 3);
-    else return Task<KIND>::dot(w, x);
+__device__ __forceinline__ float task_dot(const uint32_t* w, const float* x, const float* xs, int t) {
+    if constexpr (KIND == 3) return Task<3>::dot(w, x, xs, t & 3);
+    else return Task<KIND>::dot(w, x, xs);
 }
 
 

@@ -14,155 +14,195 @@
 namespace gh {
 
 // =============================================================== router
-// core/moe_cpu.cpp:218-256, one wave per token, same arithmetic order:
-// logit_e = dot_row (4 products grouped left to right, no fused multiply-
-// add), softmax_row (core/math_cpu.cpp:546-558, sequential sum), selection
-// on p + bias by K rounds of strict '>' argmax (lowest index wins), weights
-// from the unbiased p renormalised (uniform if their sum <= 1e-8).
-__global__ void __launch_bounds__(64) k_route(const float* __restrict__ x, const float* __restrict__ rw,
-                                              const float* __restrict__ bias, float* __restrict__ probs,
-                                              int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
-                                              int K) {
+// core/moe_cpu.cpp:218-256, one block per token, same arithmetic order:
+// logit_e = dot_row: s += ((p0 + p1) + p2) + p3 over groups of 4, left to
+// right, no fused multiply-add. The group terms are independent, so the
+// block computes them in parallel for 64 groups at a time into LDS and lane e
+// then adds its 64 terms in order -- the sequential sum stays exact while
+// the weight loads are spread over the block. softmax_row
+// (core/math_cpu.cpp:546-558: sequential sum, exp rounded once from double
+// = correctly rounded), selection on p + bias by K rounds of strict '>'
+// argmax with the lowest index winning ties, weights from the unbiased p
+// renormalised (uniform if their sum <= 1e-8).
+constexpr int ROUTE_G = 64;  // groups of 4 per pass
+__global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, const float* __restrict__ rw,
+                                               const float* __restrict__ bias, float* __restrict__ probs,
+                                               int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
+                                               int K) {
 #pragma clang fp contract(off)
     extern __shared__ float sx[];
+    __shared__ float term[64][ROUTE_G + 1];
     __shared__ float sp[64];
-    const int t = blockIdx.x, lane = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x;
     const float* xt = x + (size_t)t * d;
-    for (int i = lane; i < d; i += 64) sx[i] = xt[i];
+    for (int i = tid; i < d; i += 256) sx[i] = xt[i];
     __syncthreads();
-    if (lane < ne) {
-        const float* r = rw + (size_t)lane * d;
-        float s = 0.0f;
-        int i = 0;
-        for (; i + 4 <= d; i += 4) {
-            const float4 w = *(const float4*)(r + i);
+    const int ngroups = d / 4;
+    float s = 0.0f;  // lane e < ne of wave 0 owns logit e
+    for (int g0 = 0; g0 < ngroups; g0 += ROUTE_G) {
+        const int gn = min(ROUTE_G, ngroups - g0);
+        for (int j = tid; j < ne * gn; j += 256) {
+            const int e = j / gn, g = j % gn;
+            const int i = 4 * (g0 + g);
+            const float4 w = *(const float4*)(rw + (size_t)e * d + i);
             const float p0 = sx[i] * w.x, p1 = sx[i + 1] * w.y, p2 = sx[i + 2] * w.z, p3 = sx[i + 3] * w.w;
-            s += ((p0 + p1) + p2) + p3;
+            term[e][g] = ((p0 + p1) + p2) + p3;
         }
-        for (; i < d; ++i) s += sx[i] * r[i];
-        sp[lane] = s;
+        __syncthreads();
+        if (tid < ne)
+            for (int g = 0; g < gn; ++g) s += term[tid][g];
+        __syncthreads();
+    }
+    if (tid < ne) {
+        for (int i = 4 * ngroups; i < d; ++i) s += sx[i] * rw[(size_t)tid * d + i];
+        sp[tid] = s;
     }
     __syncthreads();
-    if (lane == 0) {
+    if (tid < 64) {
+        const int lane = tid;
         float mx = sp[0];
-        for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
+        if (lane == 0)
+            for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
+        mx = __shfl(mx, 0, 64);
+        const float ev = lane < ne ? (float)exp((double)(sp[lane] - mx)) : 0.f;
+        if (lane < ne) sp[lane] = ev;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float sum = 0.f;
-        for (int e = 0; e < ne; ++e) {
-            // exp rounded once from double: the correctly rounded expf
-            const float ev = (float)exp((double)(sp[e] - mx));
-            sp[e] = ev;
-            sum += ev;
-        }
+        if (lane == 0)
+            for (int e = 0; e < ne; ++e) sum += sp[e];
+        sum = __shfl(sum, 0, 64);
         const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
-        for (int e = 0; e < ne; ++e) sp[e] *= inv;
-        int sel[8];
-        float wv[8];
+        const float p = ev * inv;
+        const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
+        // K rounds of argmax: larger value wins, equal values -> lower index
+        bool taken = false;
+        int sel_idx[8];
         for (int k = 0; k < K; ++k) {
-            int best = -1;
-            float bv = -1e30f;
-            for (int e = 0; e < ne; ++e) {
-                bool taken = false;
-                for (int j = 0; j < k; ++j) taken |= (sel[j] == e);
-                const float v = sp[e] + (bias ? bias[e] : 0.0f);
-                if (!taken && v > bv) {
-                    bv = v;
-                    best = e;
+            float bv = (!taken && lane < ne && sel > -1e30f) ? sel : -INFINITY;
+            int bi = (!taken && lane < ne && sel > -1e30f) ? lane : 64;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o, 64);
+                const int oi = __shfl_xor(bi, o, 64);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
                 }
             }
-            if (best < 0) best = 0;
-            sel[k] = best;
+            if (bi >= 64) bi = 0;  // nothing selectable: the reference falls back to expert 0
+            sel_idx[k] = bi;
+            if (lane == bi) taken = true;
         }
-        float sw = 0.f;
+        // weights from the unbiased probabilities, renormalised in order
+        float wv[8], sw = 0.f;
         for (int k = 0; k < K; ++k) {
-            wv[k] = sp[sel[k]];
+            wv[k] = __shfl(p, sel_idx[k], 64);
             sw += wv[k];
         }
-        if (sw > 1e-8f) {
-            const float iw = 1.0f / sw;
-            for (int k = 0; k < K; ++k) wv[k] *= iw;
-        } else {
-            for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
+        if (lane == 0) {
+            if (sw > 1e-8f) {
+                const float iw = 1.0f / sw;
+                for (int k = 0; k < K; ++k) wv[k] *= iw;
+            } else {
+                for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
+            }
+            for (int k = 0; k < K; ++k) {
+                idx[(size_t)t * K + k] = sel_idx[k];
+                wout[(size_t)t * K + k] = wv[k];
+            }
         }
-        for (int k = 0; k < K; ++k) {
-            idx[(size_t)t * K + k] = sel[k];
-            wout[(size_t)t * K + k] = wv[k];
-        }
+        if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
     }
-    __syncthreads();
-    if (probs && lane < ne) probs[(size_t)t * ne + lane] = sp[lane];
 }
 
 // ========================================================== permutation
 // Stable counting sort of slot ids s = t*K+k by expert, in three
-// deterministic passes over 64-slot chunks (wave ballots give each lane its
-// rank among equal experts of lower lanes).
-__global__ void __launch_bounds__(64) k_perm_count(const int32_t* __restrict__ idx, int S, int ne,
-                                                   int32_t* __restrict__ counts) {
-    const int c = blockIdx.x, lane = threadIdx.x, s = c * 64 + lane;
-    const int e_l = s < S ? idx[s] : -1;
-    int mine = 0;
+// deterministic passes over 256-slot chunks (wave ballots give each lane its
+// rank among equal experts of lower lanes; lower waves come first).
+constexpr int PERM_CHUNK = 256, PERM_MAX_CHUNKS = 256;
+
+__device__ __forceinline__ void chunk_ranks(const int32_t* idx, int S, int ne, int c, int* wc /*[4][64] LDS*/,
+                                            int& e_l, int& rank) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s = c * PERM_CHUNK + threadIdx.x;
+    e_l = s < S ? idx[s] : -1;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    rank = 0;
     for (int e = 0; e < ne; ++e) {
         const unsigned long long m = __ballot(e_l == e);
-        if (lane == e) mine = __popcll(m);
+        if (e_l == e) rank = __popcll(m & below);
+        if (lane == e) wc[wave * 64 + e] = __popcll(m);
     }
-    if (lane < ne) counts[(size_t)c * ne + lane] = mine;
+    __syncthreads();
 }
 
-// one wave: lane e scans its column; offsets = exclusive scan of totals;
-// tile table for the grouped GEMM (tiles of `bm` rows per expert segment).
-__global__ void __launch_bounds__(64) k_perm_scan(int32_t* __restrict__ counts, int nchunks, int ne, int S,
-                                                  int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
-                                                  int bm) {
+__global__ void __launch_bounds__(256) k_perm_count(const int32_t* __restrict__ idx, int S, int ne,
+                                                    int32_t* __restrict__ counts) {
+    __shared__ int wc[4 * 64];
+    int e_l, rank;
+    chunk_ranks(idx, S, ne, blockIdx.x, wc, e_l, rank);
+    if (threadIdx.x < ne)
+        counts[(size_t)blockIdx.x * ne + threadIdx.x] =
+            wc[threadIdx.x] + wc[64 + threadIdx.x] + wc[128 + threadIdx.x] + wc[192 + threadIdx.x];
+}
+
+// counts[c][e] -> base[c][e] (first grouped position of expert e's slots in
+// chunk c); offsets = exclusive scan of the totals; tile table for the
+// grouped GEMM (tiles of `bm` rows per expert segment).
+__global__ void __launch_bounds__(256) k_perm_scan(int32_t* __restrict__ counts, int nchunks, int ne, int S,
+                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
+                                                   int bm) {
+    __shared__ int cnt[PERM_MAX_CHUNKS * 64];
+    __shared__ int offs[65];
+    const int n = nchunks * ne;
+    for (int i = threadIdx.x; i < n; i += 256) cnt[i] = counts[i];
+    __syncthreads();
     const int e = threadIdx.x;
     int run = 0;
     if (e < ne)
         for (int c = 0; c < nchunks; ++c) {
-            const int v = counts[(size_t)c * ne + e];
-            counts[(size_t)c * ne + e] = run;
+            const int v = cnt[c * ne + e];
+            cnt[c * ne + e] = run;
             run += v;
         }
-    // exclusive scan over lanes
-    int incl = run;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(incl, o, 64);
-        if (e >= o) incl += v;
+    if (e < 64) {
+        int incl = (e < ne) ? run : 0;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (e >= o) incl += v;
+        }
+        if (e < ne) offs[e] = incl - run;
+        if (e == 0) offs[ne] = S;
     }
-    const int excl = incl - run;
-    if (e < ne) {
-        offsets[e] = excl;
-        for (int c = 0; c < nchunks; ++c) counts[(size_t)c * ne + e] += excl;
-    }
-    if (e == 0) offsets[ne] = S;
-    __threadfence_block();
     __syncthreads();
-    if (e == 0 && tiles) {
-        // tiles[0] = count, then (group, m0) pairs
+    for (int i = threadIdx.x; i < n; i += 256) counts[i] = cnt[i] + offs[i % ne];
+    for (int i = threadIdx.x; i <= ne; i += 256) offsets[i] = offs[i];
+    if (threadIdx.x == 0 && tiles) {
         int nt = 0;
-        for (int g = 0; g < ne; ++g) {
-            const int lo = offsets[g], hi = offsets[g + 1];
-            for (int m0 = lo; m0 < hi; m0 += bm) {
+        for (int g = 0; g < ne; ++g)
+            for (int m0 = offs[g]; m0 < offs[g + 1]; m0 += bm) {
                 tiles[1 + 2 * nt] = g;
                 tiles[2 + 2 * nt] = m0;
                 ++nt;
             }
-        }
         tiles[0] = nt;
     }
 }
 
-__global__ void __launch_bounds__(64) k_perm_scatter(const int32_t* __restrict__ idx, int S, int ne,
-                                                     const int32_t* __restrict__ base, int32_t* __restrict__ grouped,
-                                                     int32_t* __restrict__ pos_of_slot) {
-    const int c = blockIdx.x, lane = threadIdx.x, s = c * 64 + lane;
-    const int e_l = s < S ? idx[s] : -1;
-    int rank = 0;
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int e = 0; e < ne; ++e) {
-        const unsigned long long m = __ballot(e_l == e);
-        if (e_l == e) rank = __popcll(m & below);
-    }
+__global__ void __launch_bounds__(256) k_perm_scatter(const int32_t* __restrict__ idx, int S, int ne,
+                                                      const int32_t* __restrict__ base, int32_t* __restrict__ grouped,
+                                                      int32_t* __restrict__ pos_of_slot) {
+    __shared__ int wc[4 * 64];
+    int e_l, rank;
+    chunk_ranks(idx, S, ne, blockIdx.x, wc, e_l, rank);
+    const int s = blockIdx.x * PERM_CHUNK + threadIdx.x;
     if (s < S) {
-        const int pos = base[(size_t)c * ne + e_l] + rank;
+        const int wave = threadIdx.x >> 6;
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += wc[w * 64 + e_l];
+        const int pos = base[(size_t)blockIdx.x * ne + e_l] + before + rank;
         grouped[pos] = s;
         if (pos_of_slot) pos_of_slot[s] = pos;
     }
@@ -170,12 +210,13 @@ __global__ void __launch_bounds__(64) k_perm_scatter(const int32_t* __restrict__
 
 static int permute(const int32_t* idx, int S, int ne, int32_t* grouped, int32_t* offsets, int32_t* pos_of_slot,
                    int32_t* tiles, int bm) {
-    const int nch = cdiv(S > 0 ? S : 1, 64);
+    const int nch = cdiv(S > 0 ? S : 1, PERM_CHUNK);
+    if (nch > PERM_MAX_CHUNKS) return fail(GH_EUNSUPPORTED, "moe permute: %d slots (max %d)", S, PERM_CHUNK * PERM_MAX_CHUNKS);
     int32_t* counts = (int32_t*)workspace(WS_MOE_PERM, (size_t)nch * ne * 4);
     if (!counts) return fail(GH_ENOMEM, "moe permute: workspace");
-    hipLaunchKernelGGL(k_perm_count, dim3(nch), dim3(64), 0, stream(), idx, S, ne, counts);
-    hipLaunchKernelGGL(k_perm_scan, dim3(1), dim3(64), 0, stream(), counts, nch, ne, S, offsets, tiles, bm);
-    hipLaunchKernelGGL(k_perm_scatter, dim3(nch), dim3(64), 0, stream(), idx, S, ne, counts, grouped, pos_of_slot);
+    hipLaunchKernelGGL(k_perm_count, dim3(nch), dim3(256), 0, stream(), idx, S, ne, counts);
+    hipLaunchKernelGGL(k_perm_scan, dim3(1), dim3(256), 0, stream(), counts, nch, ne, S, offsets, tiles, bm);
+    hipLaunchKernelGGL(k_perm_scatter, dim3(nch), dim3(256), 0, stream(), idx, S, ne, counts, grouped, pos_of_slot);
     GH_LAUNCHED("k_perm_*");
     return GH_OK;
 }
@@ -242,8 +283,10 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
             const float4 v = xp[i];
             xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
         }
-        ga += task_dot<KIND>(w0, xv, t);
-        if (DUAL) ub += task_dot<KIND>(w1, xv, t);
+        float xs[2];
+        task_xsum<KIND>(xv, xs);
+        ga += task_dot<KIND>(w0, xv, xs, t);
+        if (DUAL) ub += task_dot<KIND>(w1, xv, xs, t);
     }
     for (int o = LPR >> 1; o > 0; o >>= 1) {
         ga += __shfl_xor(ga, o, 64);
@@ -512,7 +555,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
 
 int moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int N, int d,
               int ne, int K) {
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(64), (size_t)d * 4, stream(), x, rw, bias, probs, idx, w, d, ne, K);
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), (size_t)d * 4, stream(), x, rw, bias, probs, idx, w, d, ne, K);
     GH_LAUNCHED("k_route");
     return GH_OK;
 }

@@ -14,6 +14,8 @@
 // 64 activation values of a task stay in registers and are reused for all R
 // rows of the wave, which keeps the activation re-reads off the critical L1
 // path. Partial sums are reduced with cross-lane shuffles.
+#include <stdlib.h>
+
 #include "gh_common.h"
 
 namespace gh {
@@ -80,57 +82,134 @@ __global__ void __launch_bounds__(256) k_dequant(const uint8_t* __restrict__ p, 
 
 namespace gh {
 
-// grid: one wave per group of rows; 4 waves per block.
-// LPR lanes share one row (LPR | 64), 64/LPR rows run side by side, and each
-// lane repeats that for R rows, so a wave covers G = R*64/LPR rows.
+// Persistent, software-pipelined GEMV. LPR lanes share one row (LPR | 64),
+// 64/LPR rows run side by side and each lane repeats that for R rows, so a
+// wave covers R*64/LPR rows per "group". Waves stride over the groups; the
+// packed bytes of the next (group, task) step are loaded before the current
+// step is decoded and multiplied, so every wave keeps a full set of weight
+// loads in flight while it computes.
 template <int KIND, int MT, int R>
 __global__ void __launch_bounds__(256) k_gemv(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                               float* __restrict__ y, int M, int K, int N, size_t rowb, int LPR) {
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int RP = 64 / LPR;
     const int sub = lane % LPR, rp = lane / LPR;
     const int T = K / 64;
-    const int row0 = wave * R * RP;
+    const int TI = (T + LPR - 1) / LPR;           // task iterations per row (lane-uniform count)
+    const int rows_per_wave = R * RP;
+    const int ngroups = (N + rows_per_wave - 1) / rows_per_wave;
+    const int wstride = gridDim.x * 4;
+    int grp = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (grp >= ngroups) return;
+    const int nsteps = ((ngroups - 1 - grp) / wstride + 1) * TI;
+
+    auto step_rows = [&](int g, int* rows) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = g * rows_per_wave + rp + RP * r;
+            rows[r] = n < N ? n : N - 1;
+        }
+    };
+    uint32_t wc[R][Task<KIND>::DW], wn[R][Task<KIND>::DW];
+    int rows[R];
+    step_rows(grp, rows);
+    {
+        const int t = sub < T ? sub : T - 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_task<KIND>(W + (size_t)rows[r] * rowb, t, wc[r]);
+    }
     float acc[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
-
-    int rows[R];
+    int ti = 0;
+    // MT == 1: the activations of the lane's task are loaded BEFORE the next
+    // step's weight prefetch is issued (vmcnt waits are in order, so loading
+    // them after the prefetch would make every step wait for the prefetch),
+    // and only once when the lane keeps the same task for all steps.
+    float x1[64], xs1[2];
+    auto load_x1 = [&](int t) {
+        const float4* xp = (const float4*)(x + (size_t)(t < T ? t : T - 1) * 64);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int n = row0 + rp + RP * r;
-        rows[r] = n < N ? n : N - 1;
-    }
-    for (int t = sub; t < T; t += LPR) {
-        uint32_t w[R][Task<KIND>::DW];
+        for (int i = 0; i < 16; ++i) {
+            const float4 v = xp[i];
+            x1[4 * i] = v.x; x1[4 * i + 1] = v.y; x1[4 * i + 2] = v.z; x1[4 * i + 3] = v.w;
+        }
+        task_xsum<KIND>(x1, xs1);
+    };
+    if (MT == 1) load_x1(sub);
+    for (int st = 0; st < nsteps; ++st) {
+        const int t = sub + ti * LPR;
+        if (MT == 1 && TI > 1 && st > 0) load_x1(t);
+        // prefetch the next step
+        const bool more = st + 1 < nsteps;
+        const int nti = (ti + 1 == TI) ? 0 : ti + 1;
+        const int ngrp = (ti + 1 == TI) ? grp + wstride : grp;
+        int nrows[R];
+        if (more) {
+            step_rows(ngrp, nrows);
+            int tn = sub + nti * LPR;
+            tn = tn < T ? tn : T - 1;
 #pragma unroll
-        for (int r = 0; r < R; ++r) load_task<KIND>(W + (size_t)rows[r] * rowb, t, w[r]);
+            for (int r = 0; r < R; ++r) load_task<KIND>(W + (size_t)nrows[r] * rowb, tn, wn[r]);
+        }
+        if (t < T) {
+            if (MT == 1) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (m >= M) break;
-            float xv[64];
-            const float4* xp = (const float4*)(x + (size_t)m * K + (size_t)t * 64);
+                for (int r = 0; r < R; ++r) acc[r][0] += task_dot<KIND>(wc[r], x1, xs1, t);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float4 v = xp[i];
-                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                for (int m = 0; m < MT; ++m) {
+                    if (m >= M) break;
+                    float xv[64];
+                    const float4* xp = (const float4*)(x + (size_t)m * K + (size_t)t * 64);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float4 v = xp[i];
+                        xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                    }
+                    float xs[2];
+                    task_xsum<KIND>(xv, xs);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r][m] += task_dot<KIND>(wc[r], xv, xs, t);
+                }
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r][m] += task_dot<KIND>(w[r], xv, t);
         }
+        if (ti + 1 == TI) {  // group done: reduce and store
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    float v = acc[r][m];
+                    for (int o = LPR >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                    const int n = grp * rows_per_wave + rp + RP * r;
+                    if (sub == 0 && m < M && n < N) y[(size_t)m * N + n] = v;
+                    acc[r][m] = 0.f;
+                }
+        }
+        grp = ngrp;
+        ti = nti;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < Task<KIND>::DW; ++i) wc[r][i] = wn[r][i];
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            float v = acc[r][m];
-            for (int o = LPR >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            const int n = row0 + rp + RP * r;
-            if (sub == 0 && m < M && n < N) y[(size_t)m * N + n] = v;
-        }
+}
+
+// tuning knobs (environment, read once): waves per CU of the persistent grid
+// and rows per lane of the single-token GEMV
+static int env_int(const char* n, int dflt) {
+    const char* v = getenv(n);
+    return v ? atoi(v) : dflt;
+}
+static int gemv_wpc() {
+    static const int v = env_int("GH_GEMV_WPC", 8);
+    return v;
+}
+static int gemv_r() {
+    static const int v = env_int("GH_GEMV_R", 2);
+    return v;
 }
 
 template <int KIND, int MT, int R>
@@ -139,7 +218,10 @@ static int launch_gemv_t(const float* x, const void* w, float* y, int M, int K, 
     int LPR = 64;
     while (LPR > 1 && LPR > T) LPR >>= 1;
     const int rows_per_wave = R * (64 / LPR);
-    const int waves = cdiv(N, rows_per_wave);
+    const int groups = cdiv(N, rows_per_wave);
+    // persistent grid: at most gemv_wpc() waves per CU, fewer when there is less work
+    const int max_waves = gemv_wpc() * num_cus();
+    const int waves = groups < max_waves ? groups : max_waves;
     hipLaunchKernelGGL((k_gemv<KIND, MT, R>), dim3(cdiv(waves, 4)), dim3(256), 0, stream(), x,
                        (const uint8_t*)w, y, M, K, N, rowb, LPR);
     GH_LAUNCHED("k_gemv");
@@ -148,19 +230,24 @@ static int launch_gemv_t(const float* x, const void* w, float* y, int M, int K, 
 
 template <int KIND>
 static int launch_gemv(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {
-    // R = 4 rows per lane when there are enough rows to fill the chip, else 1
-    const int T = K / 64;
-    int LPR = 64;
-    while (LPR > 1 && LPR > T) LPR >>= 1;
-    const bool wide = (long)N / (4L * (64 / LPR)) >= 2L * num_cus() * 4;
-    if (M == 1) return wide ? launch_gemv_t<KIND, 1, 4>(x, w, y, M, K, N, rowb)
-                            : launch_gemv_t<KIND, 1, 1>(x, w, y, M, K, N, rowb);
+    if (M == 1) {
+        const int r = gemv_r();
+        if (r == 1) return launch_gemv_t<KIND, 1, 1>(x, w, y, M, K, N, rowb);
+        if (r == 4) return launch_gemv_t<KIND, 1, 4>(x, w, y, M, K, N, rowb);
+        return launch_gemv_t<KIND, 1, 2>(x, w, y, M, K, N, rowb);
+    }
     if (M == 2) return launch_gemv_t<KIND, 2, 2>(x, w, y, M, K, N, rowb);
-    if (M <= 4) return launch_gemv_t<KIND, 4, 2>(x, w, y, M, K, N, rowb);
+    if (M <= 4) return launch_gemv_t<KIND, 4, 1>(x, w, y, M, K, N, rowb);
     return launch_gemv_t<KIND, 8, 1>(x, w, y, M, K, N, rowb);
 }
 
+int gemv1_dispatch(const float* x, const void* w, float* y, int K, int N, int kind, int* rc);  // gemv1.hip
+
 int gemv_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    if (M == 1) {
+        int rc;
+        if (gemv1_dispatch(x, w, y, K, N, kind, &rc)) return rc;
+    }
     size_t rowb;
     switch (kind) {
         case 0: rowb = row_bytes(0, K); return launch_gemv<0>(x, w, y, M, K, N, rowb);
