@@ -11,13 +11,16 @@ replayed from a captured hipGraph. `value` is decode tok/s (tokens /
 generate() wall time, the reference's GenerationStats::decode_tps); prefill
 tok/s is reported beside it.
 
-`roofline` is the dominant kernel of the decode step (the grouped expert
-GEMV), timed alone over repeated launches with HIP events on the backend
-stream; `kernels` gives the per-kernel figures for BASELINE configs 2-5 at
+`roofline` is the path's dominant HBM kernel at production shape, the
+single-token Q4_K GEMV of BASELINE config 2 (14336x4096), timed alone over
+repeated launches with HIP events on the backend stream; `traffic` comes from
+the committed rocprofv3 PMC summary of `--probe` (FETCH_SIZE + WRITE_SIZE per
+launch, scaled by what the counters read for a plain copy of known size); `kernels` gives the per-kernel figures for BASELINE configs 2-5 at
 full size. `cpu_baseline` times the CPU oracle (a restatement of the
 reference's CPU path) on a bounded sample of the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--eager-decode]
+python bench.py --probe     # 20 launches of the roofline GEMV + 20 plain 64 MiB copies, for PMC runs
 """
 import argparse
 import ctypes as C
@@ -59,6 +62,8 @@ class Model:
         gh.call("gh_granite_init_synthetic", self.h, C.c_uint64(0))
         self.ids = np.zeros(N_NEW, np.int32)
 
+    use_graph = 1
+
     def step(self, prompt, t_pf, t_dec):
         gh = self.gh
         gh.call("gh_granite_reset", self.h)
@@ -66,7 +71,7 @@ class Model:
         gh.call("gh_granite_prefill", self.h, prompt.ctypes.data_as(C.c_void_p), len(prompt), None, 1)
         a = t_pf.stop_ms()
         t_dec.start()
-        gh.call("gh_granite_generate_greedy", self.h, N_NEW, self.ids.ctypes.data_as(C.c_void_p), 1)
+        gh.call("gh_granite_generate_greedy", self.h, N_NEW, self.ids.ctypes.data_as(C.c_void_p), self.use_graph)
         b = t_dec.stop_ms()
         return a, b
 
@@ -248,6 +253,48 @@ def cpu_baseline(prompt, n_prefill=16, n_new=6):
                       f"prefill {secs[0]:.2f} s, decode {secs[1]:.2f} s"}
 
 
+def roofline_gemv(gh):
+    """The c2 headline GEMV (Q4_K, 14336x4096, M=1): buffers and a launcher."""
+    K2, N2 = 4096, 14336
+    w2 = gh.quantize(3, gh.rng_normal(2, N2 * K2, 0, 0.02))
+    x2 = gh.rng_normal(3, K2)
+    bufs = (gh.Buf.from_array(w2), gh.Buf.from_array(x2), gh.Buf.zeros(N2, np.float32))
+    nbytes = w2.nbytes + x2.nbytes + N2 * 4
+
+    def run():
+        gh.call("gh_linear_forward_q4", bufs[1].p, bufs[0].p, bufs[2].p, 1, K2, N2, 3)
+    return run, bufs, nbytes
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv1_q4k_c2_traffic.txt")
+COPY_FLOATS = 16 << 20  # 64 MiB per side
+
+
+def probe(gh):
+    run, bufs, nbytes = roofline_gemv(gh)
+    for _ in range(20):
+        run()
+    src = gh.Buf.from_array(np.ones(COPY_FLOATS, np.float32))
+    dst = gh.Buf.zeros(COPY_FLOATS, np.float32)
+    for _ in range(20):
+        gh.call("gh_copy", dst.p, src.p, gh.i64(COPY_FLOATS))
+    gh.sync()
+    log(f"probe: 20 x roofline GEMV ({nbytes} algorithmic bytes), 20 x k_copy ({COPY_FLOATS * 4} B read + written)")
+
+
+def read_traffic():
+    """HBM bytes per launch of the roofline GEMV from the committed PMC
+    summary (a line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(float(ln.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +302,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager-decode", action="store_true",
+                    help="launch the decode step's kernels one by one instead of replaying the captured graph")
+    ap.add_argument("--probe", action="store_true",
+                    help="only run the roofline GEMV and a plain copy of known size (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU sharding is a "
@@ -262,7 +313,10 @@ def main():
         sys.exit(2)
     import ghassan_hip as gh
     gh.load()
-    info = gh.load().gh_device_info
+    if args.probe:
+        probe(gh)
+        return
+    Model.use_graph = 0 if args.eager_decode else 1
     prompt = gh.rng_below(1, PROMPT, C1["V"])
 
     model = Model(gh, 3)
@@ -305,12 +359,8 @@ def main():
     inproj_ms = time_launches(gh, lambda: gh.call("gh_linear_forward_q4", dx.p, dw.p, dy.p, 1, C1["d"], proj, 3), 500)
 
     # c2 headline GEMV (Q4_K, 14336x4096, M=1) is the roofline object
-    K2, N2 = 4096, 14336
-    w2 = gh.quantize(3, gh.rng_normal(2, N2 * K2, 0, 0.02))
-    x2 = gh.rng_normal(3, K2)
-    dw2, dx2, dy2 = gh.Buf.from_array(w2), gh.Buf.from_array(x2), gh.Buf.zeros(N2, np.float32)
-    gemv_ms = time_launches(gh, lambda: gh.call("gh_linear_forward_q4", dx2.p, dw2.p, dy2.p, 1, K2, N2, 3), 500)
-    gemv_bytes = w2.nbytes + x2.nbytes + N2 * 4
+    run2, bufs2, gemv_bytes = roofline_gemv(gh)
+    gemv_ms = time_launches(gh, run2, 500)
     achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9
 
     kernels = {}
@@ -342,15 +392,16 @@ def main():
         "dtype": "fp32 activations, Q4_K weights (fp32 accumulate; fp16 MFMA operands in prefill)",
         "data": "synthetic (random-init weights by the seeded recipe, uniform prompt ids seed 1)",
         "config": {"workload": "BASELINE config 1 tiny Granite-hybrid (V4096 d512 [M,M,A,M,M,A], MoE 8x top-2 + "
-                               "shared) in Q4_K: 128-token prefill + 64 greedy tokens, decode graph-replayed",
+                               "shared) in Q4_K: 128-token prefill + 64 greedy tokens, decode "
+                               + ("eager" if args.eager_decode else "graph-replayed"),
                    "global_batch": 1, "seq_len": PROMPT + N_NEW, "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tps, 1),
         "decode_tok_s_q8_0": round(N_NEW * args.steps / (sum(d8) * 1e-3), 2),
         "prefill_tok_s_q8_0": round(PROMPT * args.steps / (sum(p8) * 1e-3), 1),
         "decode_ms_per_token": round(sum(dec_ms) / args.steps / N_NEW, 4),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<Q4_K,1,4> (BASELINE c2: 14336x4096, M=1)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv1<Q4_K> (BASELINE c2: 14336x4096, M=1)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "avg_launch_us": round(gemv_ms * 1e3, 3), "algorithmic_bytes": int(gemv_bytes)},
         "cpu_baseline": cpu,
         "kernels": kernels,
