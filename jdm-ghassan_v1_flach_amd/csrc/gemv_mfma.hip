@@ -1,0 +1,489 @@
+// Small-M GEMV (M = 1..8 tokens) for Q4_K and Q8_0 weights on the matrix
+// cores: y[t][n] = sum_k x[t][k] * w[n][k], the decode hot path of
+// linear_forward_q4 (core/ops.cpp:360-408).
+//
+// Why MFMA for a memory-bound op: the VALU budget at 8 TB/s is under three
+// lane-ops per Q4_K weight, and a scalar dot spends most of it turning
+// nibbles into numbers. Here a weight costs ~0.6 lane-ops: integer codes are
+// masked straight into fp16 *subnormals* (bits 0x000q are the number
+// q * 2^-24, exact) and v_mfma_f32_16x16x32_f16 multiplies them exactly,
+// accumulating in fp32. Per-sub-block scales are applied afterwards.
+//
+// Block-diagonal trick. In D[m][n] = sum_k A[m][k] B[k][n] (16x16x32), lane
+// l holds B[8g..8g+7][n] and D[4g..4g+3][n] with n = l%16, g = l/16. The
+// weights are B (16 rows of W = 16 columns n); lane (n, g) loads ITS OWN 8
+// codes per MFMA. The activations are A, and A row m is non-zero only in
+// k-slot g = m/4. So D[4g+e][n] is the dot of lane (n,g)'s own 8 codes with
+// activation vector e: every lane ends up with the partial sums of exactly
+// the codes it loaded, for 4 activation vectors e at once. e runs over
+// (token, hi/lo part): x = hi + lo with hi = fp16(x), lo = fp16(x - hi),
+// which keeps ~22 bits of each activation, so the result is as accurate as
+// an fp32-activation dot (the reference's CPU path, core/ops.cpp:304-338,
+// multiplies fp16-rounded weights with fp32 activations).
+//
+// Code types (u = a dword of 4 packed bytes; each 16-bit half must stay
+// below 0x0400, the subnormal range, so only bits 0..9 may hold a code):
+//   Q4_K  c0 = u & 0x000F000F        low nibbles of bytes 0,2    (value q)
+//         c1 = (u>>8) & 0x000F000F   low nibbles of bytes 1,3    (q)
+//         c2 = u & 0x00F000F0        high nibbles of bytes 0,2   (16 q)
+//         c3 = (u>>8) & 0x00F000F0   high nibbles of bytes 1,3   (16 q)
+//   Q8_0  v_perm_b32 spreads bytes (flipped: q + 128) into 16-bit halves.
+// Codes of one sub-block (Q4_K) or one block (Q8_0) share an MFMA
+// accumulation chain with a single power-of-two scale, removed exactly
+// afterwards. The
+// activations in LDS are laid out in the order the codes come out of the
+// dwords (the dot is invariant under a common permutation of k).
+//
+// Work: a tile is 16 rows; the K range of a tile is split over the WB waves
+// of a block (SBW super-blocks of 256 values each); the per-wave partials
+// are summed through LDS in a fixed order (deterministic). A block walks
+// over `tpb` consecutive tiles; a wave issues all its loads of a tile at
+// once (the first tile's before the activations are staged, the next
+// tile's as soon as the current one's bytes are consumed).
+#include <stdlib.h>
+
+#include "gh_common.h"
+
+namespace gh {
+
+typedef _Float16 gm_half8 __attribute__((ext_vector_type(8)));
+typedef float gm_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gm_u4 __attribute__((ext_vector_type(4)));
+
+template <int KIND>
+struct GmCfg;
+template <>
+struct GmCfg<3> {  // Q4_K: 144-byte super-blocks; a lane uses 16 B header + 32 B nibbles
+    static constexpr int DW = 12;
+    static constexpr int SB_BYTES = 144;
+};
+template <>
+struct GmCfg<2> {  // Q8_0: 8 blocks of 34 bytes; a lane uses two blocks (17 dwords)
+    static constexpr int DW = 17;
+    static constexpr int SB_BYTES = 272;
+};
+
+__device__ __forceinline__ float gm_lo16(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu)); }
+__device__ __forceinline__ float gm_hi16(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
+
+// This lane's bytes of super-block `sbl` of row n16 from the wave's LDS
+// slice (row stride RS bytes).
+template <int KIND>
+__device__ __forceinline__ void gm_lds_slice(const unsigned char* rowp, int sbl, int g, uint32_t* w) {
+    if constexpr (KIND == 3) {
+        const unsigned char* p = rowp + sbl * 144;
+        const uint4 h = *(const uint4*)p;
+        const uint4 a = *(const uint4*)(p + 16 + 32 * g);
+        const uint4 b = *(const uint4*)(p + 32 + 32 * g);
+        w[0] = h.x; w[1] = h.y; w[2] = h.z; w[3] = h.w;
+        w[4] = a.x; w[5] = a.y; w[6] = a.z; w[7] = a.w;
+        w[8] = b.x; w[9] = b.y; w[10] = b.z; w[11] = b.w;
+    } else {
+        const uint32_t* p = (const uint32_t*)(rowp + sbl * 272 + 68 * g);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) w[i] = p[i];
+    }
+}
+
+// Codes of MFMA (chain c, step r) for this lane, as the B operand.
+template <int KIND>
+__device__ __forceinline__ gm_half8 gm_codes(const uint32_t* w, const uint32_t* u, int c, int r) {
+    gm_u4 v;
+    if constexpr (KIND == 3) {
+        const uint32_t* q = w + 4 + 4 * r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t s = q[i];
+            const uint32_t t = (c & 1) ? (s >> 8) : s;
+            v[i] = t & ((c & 2) ? 0x00F000F0u : 0x000F000Fu);
+        }
+    } else {
+        // u = w ^ 0x80808080 (byte = q + 128). Block 0 quants: stream bytes
+        // 2..33, block 1: 36..67. Values 8r..8r+7 of block c.
+        if (c == 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int j = 2 * r + i;  // values 4j..4j+3 = bytes 4j+2..4j+5
+                v[2 * i] = __builtin_amdgcn_perm(u[j + 1], u[j], 0x0c030c02u);
+                v[2 * i + 1] = __builtin_amdgcn_perm(u[j + 1], u[j], 0x0c050c04u);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int j = 9 + 2 * r + i;  // values 4(j-9).. = bytes 4j..4j+3
+                v[2 * i] = __builtin_amdgcn_perm(0u, u[j], 0x0c010c00u);
+                v[2 * i + 1] = __builtin_amdgcn_perm(0u, u[j], 0x0c030c02u);
+            }
+        }
+    }
+    return __builtin_bit_cast(gm_half8, v);
+}
+
+// Position (within the 256-value super-block) of element el of the 8 codes
+// lane slot g feeds to MFMA r8 = chain*steps + step.
+template <int KIND>
+__host__ __device__ __forceinline__ int gm_kpos(int r8, int g, int el) {
+    if constexpr (KIND == 3) {
+        const int c = r8 >> 1, r = r8 & 1;
+        const int i = 4 * r + (el >> 1);
+        const int b = 4 * i + (c & 1) + 2 * (el & 1);
+        return 64 * g + (c >= 2 ? 32 : 0) + b;
+    } else {
+        const int c = r8 >> 2, r = r8 & 3;
+        return 64 * g + 32 * c + 8 * r + el;
+    }
+}
+
+// Inverse of gm_kpos: where value kk (0..255) of a super-block goes.
+template <int KIND>
+__device__ __forceinline__ void gm_kinv(int kk, int& r8, int& g, int& el) {
+    g = kk >> 6;
+    if constexpr (KIND == 3) {
+        const int half = (kk >> 5) & 1, b = kk & 31;
+        const int i = b >> 2, bb = b & 3;
+        const int c = half * 2 + (bb & 1);
+        r8 = c * 2 + (i >> 2);
+        el = 2 * (i & 3) + (bb >> 1);
+    } else {
+        r8 = ((kk >> 5) & 1) * 4 + ((kk >> 3) & 3);
+        el = kk & 7;
+    }
+}
+
+// Weight bytes move in "steps": SS consecutive super-blocks of the 16 rows
+// of a tile. A wave reads a step with contiguous 16-byte pieces (each row's
+// SS*SB_BYTES bytes are contiguous, so a load instruction touches few
+// cache lines), parks it in its own LDS slice, and every lane then reads
+// its MFMA-layout bytes back from there. The next step's pieces are loaded
+// into the same registers while the current step is multiplied.
+template <int KIND, int SS>
+struct GmStep {
+    static constexpr int PPR = SS * GmCfg<KIND>::SB_BYTES / 16;  // 16-byte pieces per row
+    static constexpr int PPL = (16 * PPR + 63) / 64;             // pieces per lane
+    static constexpr int RS = PPR * 16 + 16;                     // LDS row stride (padded: rows fall in distinct banks)
+    static constexpr int BYTES = 16 * RS;                        // LDS slice per wave
+};
+
+// LDS layout (bytes): [zero 16][A chunks: NSB*8*M*8 x 16][xsum: NSB*8*M f32]
+//                     [red: 2*WB*16*M f32][weight slices: WB x GmStep::BYTES]
+// Blocks of up to 16 waves for one token pair, up to 8 (twice the
+// registers per lane) for more.
+template <int KIND, int TP, int SS>
+__global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                    float* __restrict__ y, int M, int K, int N, size_t rowb,
+                                                    int WB, int tpb, int spw) {
+    constexpr int DW = GmCfg<KIND>::DW;
+    using St = GmStep<KIND, SS>;
+    extern __shared__ __align__(16) unsigned char gm_smem[];
+    const int NSB = K >> 8;
+    const int nsteps = NSB / SS;
+    uint4* zero = (uint4*)gm_smem;
+    uint4* achunk = zero + 1;
+    const int nchunks = NSB * 8 * M * 8;
+    float* xsum = (float*)(achunk + nchunks);
+    float* red = xsum + NSB * 8 * M;
+    unsigned char* slices = (unsigned char*)(red + 2 * WB * 16 * M);
+    const int tid = threadIdx.x, nth = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    unsigned char* slice = slices + wave * St::BYTES;
+    const int st0 = wave * spw;
+    const int ns = max(0, min(spw, nsteps - st0));  // steps of this wave per tile
+    // this lane's A chunk offset inside one (sb, r8) group (zero if off-diagonal)
+    const int e = n16 & 3;
+    const bool diag = (n16 >> 2) == g;
+    int aoff[TP];
+#pragma unroll
+    for (int p = 0; p < TP; ++p) {
+        const int t = 2 * p + (e >> 1);
+        aoff[p] = (diag && t < M) ? ((t * 4 + g) * 2 + (e & 1)) : -1;
+    }
+    const int ntiles = (N + 15) >> 4;
+    const int tile0 = blockIdx.x * tpb;
+    const int tile1 = min(ntiles, tile0 + tpb);
+    const int items = ns > 0 ? (tile1 - tile0) * ns : 0;
+
+    uint4 P[St::PPL];
+    auto load_item = [&](int it) {
+        const int tile = tile0 + it / ns, step = st0 + it % ns;
+        const uint8_t* base = W + (size_t)step * SS * GmCfg<KIND>::SB_BYTES;
+#pragma unroll
+        for (int i = 0; i < St::PPL; ++i) {
+            const int q = lane + 64 * i;
+            if (q < 16 * St::PPR) {
+                const int r = q / St::PPR, j = q - r * St::PPR;
+                int n = tile * 16 + r;
+                n = n < N ? n : N - 1;
+                P[i] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const gm_u4*)(base + (size_t)n * rowb + 16 * j)));
+            }
+        }
+    };
+    auto store_item = [&]() {
+#pragma unroll
+        for (int i = 0; i < St::PPL; ++i) {
+            const int q = lane + 64 * i;
+            if (q < 16 * St::PPR) {
+                const int r = q / St::PPR, j = q - r * St::PPR;
+                *(uint4*)(slice + r * St::RS + 16 * j) = P[i];
+            }
+        }
+    };
+    // ---- stage the activations: hi/lo fp16 parts in code order + the
+    // 32-value sums. Coalesced float4 reads; each group of 8 lanes covers
+    // one 32-value group and reduces its sum with shuffles. (K is a
+    // multiple of 256, so every wave runs the loop the same number of times.)
+    // The first activation reads are issued before the first step's weight
+    // reads (which would otherwise queue ahead of them), the conversion runs
+    // while the weight bytes are in flight.
+    if (tid == 0) *zero = make_uint4(0, 0, 0, 0);
+    const int K4 = K >> 2, xtotal = M * K4;
+    auto xload = [&](int idx) {
+        const int t = idx / K4, k = (idx - t * K4) * 4;
+        return *(const float4*)(x + (size_t)t * K + k);
+    };
+    uint16_t* a16 = (uint16_t*)achunk;
+    auto stage = [&](int idx, float4 v4) {
+        const int t = idx / K4, k = (idx - t * K4) * 4;
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+        const int sb = k >> 8;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kk = (k + j) & 255;
+            int r8, gg, el;
+            gm_kinv<KIND>(kk, r8, gg, el);
+            const _Float16 hi = (_Float16)vv[j];
+            const _Float16 lo = (_Float16)(vv[j] - (float)hi);
+            const int base = ((((sb * 8 + r8) * M + t) * 4 + gg) * 2) * 8 + el;
+            a16[base] = __builtin_bit_cast(uint16_t, hi);
+            a16[base + 8] = __builtin_bit_cast(uint16_t, lo);
+        }
+        float sum = (vv[0] + vv[1]) + (vv[2] + vv[3]);
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        if ((idx & 7) == 0) xsum[(k >> 5) * M + t] = sum;
+    };
+    constexpr int XP = 4;
+    float4 xpre[XP];
+#pragma unroll
+    for (int i = 0; i < XP; ++i)
+        if (tid + i * nth < xtotal) xpre[i] = xload(tid + i * nth);
+    if (items > 0) load_item(0);
+#pragma unroll
+    for (int i = 0; i < XP; ++i)
+        if (tid + i * nth < xtotal) stage(tid + i * nth, xpre[i]);
+    for (int idx = tid + XP * nth; idx < xtotal; idx += nth) stage(idx, xload(idx));
+    __syncthreads();
+
+    int buf = 0;
+    for (int tile = tile0; tile < tile1; ++tile) {
+        float acc[TP][2];
+#pragma unroll
+        for (int p = 0; p < TP; ++p) acc[p][0] = acc[p][1] = 0.f;
+        for (int sidx = 0; sidx < ns; ++sidx) {
+            const int it = (tile - tile0) * ns + sidx;
+            store_item();
+            if (it + 1 < items) load_item(it + 1);
+            const unsigned char* rowp = slice + n16 * St::RS;
+#pragma unroll
+            for (int sbl = 0; sbl < SS; ++sbl) {
+            const int sb = (st0 + sidx) * SS + sbl;
+            uint32_t w[DW];
+            gm_lds_slice<KIND>(rowp, sbl, g, w);
+            uint32_t u[DW];
+            if constexpr (KIND == 2) {
+#pragma unroll
+                for (int i = 0; i < DW; ++i) u[i] = w[i] ^ 0x80808080u;
+            }
+            gm_f4 D[TP][2];  // chain 0: sub-block 2g / block 2g; chain 1: 2g+1
+#pragma unroll
+            for (int p = 0; p < TP; ++p) D[p][0] = D[p][1] = gm_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r8 = 0; r8 < 8; ++r8) {
+                const int c = KIND == 3 ? (r8 >> 1) : (r8 >> 2);
+                const int r = KIND == 3 ? (r8 & 1) : (r8 & 3);
+                const gm_half8 b = gm_codes<KIND>(w, u, c, r);
+                const uint4* grp = achunk + (size_t)(sb * 8 + r8) * M * 8;
+#pragma unroll
+                for (int p = 0; p < TP; ++p) {
+                    const uint4 av = *(aoff[p] >= 0 ? grp + aoff[p] : zero);
+                    D[p][r8 >> 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(gm_half8, av), b,
+                                                                           D[p][r8 >> 2], 0, 0, 0);
+                }
+            }
+            // ---- epilogue: per-sub-block scales
+            const float* xs = xsum + (size_t)(sb * 8 + 2 * g) * M;  // sub-blocks 2g, 2g+1
+            if constexpr (KIND == 3) {
+                const float d = gm_lo16(w[0]), dmin = gm_hi16(w[0]);
+                const int j0 = 2 * (g & 1);
+                const uint32_t A2 = (w[1] >> (8 * j0)) & 0xFFFFu, B2 = (w[2] >> (8 * j0)) & 0xFFFFu,
+                               C2 = (w[3] >> (8 * j0)) & 0xFFFFu;
+                const uint32_t scp = g < 2 ? (A2 & 0x3F3Fu) : ((C2 & 0x0F0Fu) | ((A2 >> 2) & 0x3030u));
+                const uint32_t mp = g < 2 ? (B2 & 0x3F3Fu) : (((C2 >> 4) & 0x0F0Fu) | ((B2 >> 2) & 0x3030u));
+                const float a0 = d * (float)(scp & 0xFFu) * 16777216.f, a1 = d * (float)(scp >> 8) * 16777216.f;
+                const float b0 = dmin * (float)(mp & 0xFFu), b1 = dmin * (float)(mp >> 8);
+#pragma unroll
+                for (int p = 0; p < TP; ++p)
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const int t = 2 * p + tt;
+                        if (t >= M) break;
+                        const float s0 = D[p][0][2 * tt] + D[p][0][2 * tt + 1];
+                        const float s1 = (D[p][1][2 * tt] + D[p][1][2 * tt + 1]) * 0.0625f;
+                        acc[p][tt] += a0 * s0 + a1 * s1 - (b0 * xs[t] + b1 * xs[M + t]);
+                    }
+            } else {
+                const float d0 = gm_lo16(w[0]), d1 = gm_hi16(w[8]);
+#pragma unroll
+                for (int p = 0; p < TP; ++p)
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const int t = 2 * p + tt;
+                        if (t >= M) break;
+                        const float s0 = D[p][0][2 * tt] + D[p][0][2 * tt + 1];
+                        const float s1 = D[p][1][2 * tt] + D[p][1][2 * tt + 1];
+                        acc[p][tt] += d0 * fmaf(s0, 16777216.f, -128.f * xs[t]) +
+                                      d1 * fmaf(s1, 16777216.f, -128.f * xs[M + t]);
+                    }
+            }
+            }  // sbl
+        }  // steps
+        // ---- reduce over the 4 k-slot lanes of a row, then over the waves
+#pragma unroll
+        for (int p = 0; p < TP; ++p)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                float v = acc[p][tt];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                acc[p][tt] = v;
+            }
+        float* rb = red + (size_t)buf * WB * 16 * M;
+        if (wave < WB && g == 0) {
+#pragma unroll
+            for (int p = 0; p < TP; ++p)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int t = 2 * p + tt;
+                    if (t < M) rb[(wave * M + t) * 16 + n16] = acc[p][tt];
+                }
+        }
+        __syncthreads();
+        for (int i = tid; i < 16 * M; i += nth) {  // a 1-wave block has 64 threads for up to 128 outputs
+            const int t = i >> 4, nn = i & 15;
+            float v = 0.f;
+            for (int wv = 0; wv < WB; ++wv) v += rb[(wv * M + t) * 16 + nn];
+            const int n = tile * 16 + nn;
+            if (n < N) y[(size_t)t * N + n] = v;
+        }
+        buf ^= 1;
+    }
+}
+
+static int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+constexpr size_t GM_LDS_MAX = 160 * 1024;
+
+template <int KIND, int SS>
+static size_t gm_lds_bytes(int K, int M, int WB) {
+    const size_t nsb = K / 256;
+    return 16 + nsb * 8 * M * 8 * 16 + nsb * 8 * M * 4 + 2 * (size_t)WB * 16 * M * 4 +
+           (size_t)WB * GmStep<KIND, SS>::BYTES;
+}
+
+// Waves per block and steps per wave: as many waves as there are steps (up
+// to 16), fewer if the block's LDS would not fit. 0 if nothing fits.
+template <int KIND, int SS>
+static int gm_split(int K, int M, int& WB, int& spw) {
+    const int nsteps = K / 256 / SS;
+    const int wcap = M <= 2 ? 16 : 8;
+    int wmax = env_int("GH_GEMVM_WB", wcap);
+    if (wmax > wcap) wmax = wcap;
+    for (int wb = nsteps < wmax ? nsteps : wmax; wb >= 1; --wb) {
+        spw = (nsteps + wb - 1) / wb;
+        WB = (nsteps + spw - 1) / spw;
+        if (gm_lds_bytes<KIND, SS>(K, M, WB) <= GM_LDS_MAX) return 1;
+    }
+    return 0;
+}
+
+template <int KIND, int TP, int SS>
+static int gm_launch(const float* x, const void* w, float* y, int M, int K, int N) {
+    auto kern = k_gemv_mfma<KIND, TP, SS>;
+    int WB, spw;
+    if (!gm_split<KIND, SS>(K, M, WB, spw)) return fail(GH_EINVAL, "gemv_mfma: K=%d M=%d does not fit LDS", K, M);
+    const size_t lds = gm_lds_bytes<KIND, SS>(K, M, WB);
+    static bool attr_set = false;
+    if (!attr_set) {
+        GH_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GM_LDS_MAX));
+        attr_set = true;
+    }
+    const int ntiles = (N + 15) / 16;
+    const int wpc = env_int("GH_GEMVM_WPC", 16);
+    int bpc = wpc / WB;
+    if (bpc < 1) bpc = 1;
+    const int by_lds = (int)(GM_LDS_MAX / lds);
+    if (bpc > by_lds) bpc = by_lds;
+    int blocks = num_cus() * bpc;
+    if (blocks > ntiles) blocks = ntiles;
+    const int tpb = (ntiles + blocks - 1) / blocks;
+    blocks = (ntiles + tpb - 1) / tpb;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WB), lds, stream(), x, (const uint8_t*)w, y, M, K, N,
+                       row_bytes(KIND, K), WB, tpb, spw);
+    GH_LAUNCHED("k_gemv_mfma");
+    return GH_OK;
+}
+
+// Q4_K moves two super-blocks per step when K allows, Q8_0 one
+template <int KIND>
+static bool gm_fits(int K, int M) {
+    int WB, spw;
+    if constexpr (KIND == 3) {
+        if ((K / 256) % 2 == 0) return gm_split<KIND, 2>(K, M, WB, spw);
+    }
+    return gm_split<KIND, 1>(K, M, WB, spw);
+}
+
+template <int KIND, int TP>
+static int gm_ss(const float* x, const void* w, float* y, int M, int K, int N) {
+    if constexpr (KIND == 3) {
+        if ((K / 256) % 2 == 0) return gm_launch<KIND, TP, 2>(x, w, y, M, K, N);
+    }
+    return gm_launch<KIND, TP, 1>(x, w, y, M, K, N);
+}
+
+template <int KIND>
+static int gm_kind(const float* x, const void* w, float* y, int M, int K, int N) {
+    const int TP = (M + 1) / 2;
+    if (TP == 1) return gm_ss<KIND, 1>(x, w, y, M, K, N);
+    if (TP == 2) return gm_ss<KIND, 2>(x, w, y, M, K, N);
+    if (TP == 3) return gm_ss<KIND, 3>(x, w, y, M, K, N);
+    return gm_ss<KIND, 4>(x, w, y, M, K, N);
+}
+
+// Returns 1 if handled (Q4_K / Q8_0, 1 <= M <= 8, K a multiple of 256).
+// Token groups whose activations do not fit LDS together are run as
+// separate launches over the same weights.
+int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
+    static const int enabled = env_int("GH_GEMV_MFMA", 1);
+    static const int q8_m1 = env_int("GH_GEMV_MFMA_Q8M1", 1);
+    if (!enabled || (kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
+    if (kind == 2 && M == 1 && !q8_m1) return 0;
+    int mc = M;
+    while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc) : gm_fits<2>(K, mc))) --mc;
+    if (mc < 1) return 0;
+    // y is [M][N]; a token group [t0, t0+mc) is a contiguous slice of x and y
+    for (int t0 = 0; t0 < M; t0 += mc) {
+        const int m = M - t0 < mc ? M - t0 : mc;
+        const float* xs = x + (size_t)t0 * K;
+        float* ys = y + (size_t)t0 * N;
+        *rc = kind == 3 ? gm_kind<3>(xs, w, ys, m, K, N) : gm_kind<2>(xs, w, ys, m, K, N);
+        if (*rc) return 1;
+    }
+    return 1;
+}
+
+}  // namespace gh

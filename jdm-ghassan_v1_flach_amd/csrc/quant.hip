@@ -243,7 +243,13 @@ static int launch_gemv(const float* x, const void* w, float* y, int M, int K, in
 
 int gemv1_dispatch(const float* x, const void* w, float* y, int K, int N, int kind, int* rc);  // gemv1.hip
 
+int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc);  // gemv_mfma.hip
+
 int gemv_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    {
+        int rc;
+        if (gemv_mfma_dispatch(x, w, y, M, K, N, kind, &rc)) return rc;
+    }
     if (M == 1) {
         int rc;
         if (gemv1_dispatch(x, w, y, K, N, kind, &rc)) return rc;

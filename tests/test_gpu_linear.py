@@ -118,3 +118,40 @@ def test_fp16_and_f32_linear(gh):
     refg = np.empty(Mg * N, np.float32)
     O.oracle().orc_linear_forward_fp16(O.P(xg), O.P(wh), O.P(refg), Mg, K, N)
     assert relerr(yg.numpy(), refg) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("kind", [2, 3])
+@pytest.mark.parametrize("K,N", [(256, 37), (3072, 530), (16384, 300)])
+def test_small_m_gemv_every_m(gh, kind, K, N):
+    """Every token count of the small-M path (1..8) at one, many and the
+    maximum number of super-blocks (the last case runs in token groups),
+    ragged N (tiles of 16 rows)."""
+    w = _w(kind, N, K, seed=21)
+    dw = gh.Buf.from_array(w)
+    for M in range(1, 9):
+        x = O.rng_normal(22 + M, M * K)
+        dx = gh.Buf.from_array(x)
+        y = gh.Buf.zeros(M * N, np.float32)
+        gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
+        ref = O.linear_q(x, w, M, K, N, kind)
+        assert relerr(y.numpy().reshape(M, N), ref) <= GEMV_TOL, f"M={M}"
+
+
+@pytest.mark.parametrize("kind", [2, 3])
+def test_small_m_gemv_activation_range(gh, kind):
+    """Activations spanning 1e-4..1e3 in magnitude per token: the split of
+    each activation into two fp16 parts keeps the fp32-level accuracy."""
+    M, K, N = 3, 2048, 64
+    w = _w(kind, N, K, seed=31)
+    x = O.rng_normal(32, M * K).reshape(M, K)
+    x[0] *= 1e3
+    x[1] *= 1e-4
+    x[2, ::7] *= 50.0
+    x = np.ascontiguousarray(x.reshape(-1), np.float32)
+    dw, dx = gh.Buf.from_array(w), gh.Buf.from_array(x)
+    y = gh.Buf.zeros(M * N, np.float32)
+    gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
+    ref = O.linear_q(x, w, M, K, N, kind).reshape(M, N)
+    got = y.numpy().reshape(M, N)
+    for t in range(M):
+        assert relerr(got[t], ref[t]) <= GEMV_TOL, f"token {t}"
