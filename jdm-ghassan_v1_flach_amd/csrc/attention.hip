@@ -56,6 +56,7 @@ __device__ __forceinline__ void widen8(const uint4 r, float* f) {
 }
 
 constexpr int DEC_CHUNK_MAX = 512, DEC_GMAX = 8;
+constexpr int DEC_B = 4;  // steps of K / V rows loaded per batch
 
 template <int HD, bool PAGED>
 __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
@@ -116,27 +117,37 @@ __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
             qr[g][4] = x1.x; qr[g][5] = x1.y; qr[g][6] = x1.z; qr[g][7] = x1.w;
         }
     }
-    // ---- scores
-    for (int base = wave * PPS; base < n; base += 4 * PPS) {
-        const int p = base + sub;
-        const bool ok = p < n;
-        float kf[8];
-        if (ok) {
-            const uint4 r = *(const uint4*)(a.k + row_of(jb + p) + cg * 8);
-            widen8<PAGED>(r, kf);
-        } else {
+    // ---- scores; the K rows of DEC_B steps are requested together (one
+    // memory round trip per batch instead of per step)
+    for (int base0 = wave * PPS; base0 < n; base0 += 4 * PPS * DEC_B) {
+        uint4 kr[DEC_B];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = 0.f;
+        for (int b = 0; b < DEC_B; ++b) {
+            const int p = base0 + b * 4 * PPS + sub;
+            if (p < n) kr[b] = *(const uint4*)(a.k + row_of(jb + p) + cg * 8);
         }
 #pragma unroll
-        for (int g = 0; g < DEC_GMAX; ++g) {
-            if (g >= G) break;
-            float s = 0.f;
+        for (int b = 0; b < DEC_B; ++b) {
+            const int p = base0 + b * 4 * PPS + sub;
+            if (base0 + b * 4 * PPS >= n) break;  // wave-uniform
+            const bool ok = p < n;
+            float kf[8];
+            if (ok) {
+                widen8<PAGED>(kr[b], kf);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s = fmaf(qr[g][i], kf[i], s);
+                for (int i = 0; i < 8; ++i) kf[i] = 0.f;
+            }
 #pragma unroll
-            for (int o = LPP >> 1; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-            if (ok && cg == 0) sc[g][p] = s * a.scale;
+            for (int g = 0; g < DEC_GMAX; ++g) {
+                if (g >= G) break;
+                float sc_ = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sc_ = fmaf(qr[g][i], kf[i], sc_);
+#pragma unroll
+                for (int o = LPP >> 1; o > 0; o >>= 1) sc_ += __shfl_xor(sc_, o, 64);
+                if (ok && cg == 0) sc[g][p] = sc_ * a.scale;
+            }
         }
     }
     __syncthreads();
@@ -164,18 +175,26 @@ __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
     for (int g = 0; g < DEC_GMAX; ++g)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
-    for (int base = wave * PPS; base < n; base += 4 * PPS) {
-        const int p = base + sub;
-        if (p < n) {
-            float vf[8];
-            const uint4 r = *(const uint4*)(a.v + row_of(jb + p) + cg * 8);
-            widen8<PAGED>(r, vf);
+    for (int base0 = wave * PPS; base0 < n; base0 += 4 * PPS * DEC_B) {
+        uint4 vr[DEC_B];
 #pragma unroll
-            for (int g = 0; g < DEC_GMAX; ++g) {
-                if (g >= G) break;
-                const float w = sc[g][p];
+        for (int b = 0; b < DEC_B; ++b) {
+            const int p = base0 + b * 4 * PPS + sub;
+            if (p < n) vr[b] = *(const uint4*)(a.v + row_of(jb + p) + cg * 8);
+        }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(w, vf[i], acc[g][i]);
+        for (int b = 0; b < DEC_B; ++b) {
+            const int p = base0 + b * 4 * PPS + sub;
+            if (p < n) {
+                float vf[8];
+                widen8<PAGED>(vr[b], vf);
+#pragma unroll
+                for (int g = 0; g < DEC_GMAX; ++g) {
+                    if (g >= G) break;
+                    const float w = sc[g][p];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(w, vf[i], acc[g][i]);
+                }
             }
         }
     }
@@ -255,6 +274,29 @@ static int pick_chunk(int len, int blocks_other) {
     if (chunk < 128) chunk = 128;
     if (chunk > DEC_CHUNK_MAX) chunk = DEC_CHUNK_MAX;
     return chunk;
+}
+
+// Split-K partials only (no merge): the merge is left to the consumer
+// (the fused output projection merges them in its prologue).
+template <bool PAGED>
+static int launch_decode_partials(DecodeArgs& a, int hd, int S, int span) {
+    a.chunk = pick_chunk(span, a.KV * S);
+    a.splits = cdiv(span > 0 ? span : 1, a.chunk);
+    float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
+    float* ml = (float*)workspace(WS_ATTN_ML, (size_t)S * a.KV * a.splits * a.G * 2 * 4);
+    if (!o || !ml) return fail(GH_ENOMEM, "attention decode: workspace");
+    a.o_part = o;
+    a.ml_part = ml;
+    const dim3 grid(a.splits, a.KV, S);
+    switch (hd) {
+        case 16: hipLaunchKernelGGL((k_attn_decode<16, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 32: hipLaunchKernelGGL((k_attn_decode<32, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 64: hipLaunchKernelGGL((k_attn_decode<64, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 128: hipLaunchKernelGGL((k_attn_decode<128, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        default: return fail(GH_EUNSUPPORTED, "attention decode: head_dim %d (supported: 16, 32, 64, 128)", hd);
+    }
+    GH_LAUNCHED("k_attn_decode");
+    return GH_OK;
 }
 
 template <bool PAGED>
@@ -474,6 +516,22 @@ int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, f
     a.q = q; a.k = kc; a.v = vc; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
     a.cache_max = cache_max; a.ctl = ctl; a.j0 = 0;
     return launch_decode<false>(a, hd, 1, cache_max, out);
+}
+
+// Partials of the ring-cache decode (device control block), for a merge in
+// the consumer: o_part [KV][splits][G][hd], ml [KV][splits][G][2].
+int attn_decode_partials_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, int H, int KV, int hd,
+                                int cache_max, const int32_t* ctl, float scale, const float** o_part,
+                                const float** ml, int* splits) {
+    DecodeArgs a{};
+    a.q = q; a.k = kc; a.v = vc; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
+    a.cache_max = cache_max; a.ctl = ctl; a.j0 = 0;
+    const int rc = launch_decode_partials<false>(a, hd, 1, cache_max);
+    if (rc) return rc;
+    *o_part = a.o_part;
+    *ml = a.ml_part;
+    *splits = a.splits;
+    return GH_OK;
 }
 
 int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,

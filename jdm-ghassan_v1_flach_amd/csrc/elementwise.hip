@@ -68,7 +68,10 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
 
 // core/math_cpu.cpp:710-723: the first finite maximum (strict '>', lowest
 // index on ties); if no value is finite, the reference's serial fallback.
-__global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ l, int V, int32_t* __restrict__ out) {
+// With `step` set, the winner is also appended to ids[*step] (if *step <
+// cap) and *step advances: the greedy-decode record of one token.
+__global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ l, int V, int32_t* __restrict__ out,
+                                                 int32_t* __restrict__ step, int32_t* __restrict__ ids, int cap) {
     float bv = 0.f;
     int bi = -1;
     for (int i = threadIdx.x; i < V; i += 1024) {
@@ -96,6 +99,11 @@ __global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ l, in
             for (int i = 1; i < V; ++i) if (l[i] > l[bi]) bi = i;
         }
         *out = bi;
+        if (step) {
+            const int s = *step;
+            if (s < cap) ids[s] = bi;
+            *step = s + 1;
+        }
     }
 }
 
@@ -106,7 +114,13 @@ int launch_f32_to_f16(const float* s, uint16_t* d, int64_t n) {
 }
 
 int launch_argmax(const float* l, int V, int32_t* out_dev) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream(), l, V, out_dev);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream(), l, V, out_dev, nullptr, nullptr, 0);
+    GH_LAUNCHED("k_argmax");
+    return GH_OK;
+}
+
+int launch_argmax_record(const float* l, int V, int32_t* out_dev, int32_t* step, int32_t* ids, int cap) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream(), l, V, out_dev, step, ids, cap);
     GH_LAUNCHED("k_argmax");
     return GH_OK;
 }

@@ -42,7 +42,7 @@
 // tile's as soon as the current one's bytes are consumed).
 #include <stdlib.h>
 
-#include "gh_common.h"
+#include "gemv_fuse.h"
 
 namespace gh {
 
@@ -150,6 +150,237 @@ __device__ __forceinline__ void gm_kinv(int kk, int& r8, int& g, int& el) {
     }
 }
 
+// ---------------------------------------------------------- fusion hooks
+// Block-wide sum of a double (all threads get the total).
+__device__ __forceinline__ double gm_block_sum(double v, double* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int nw = blockDim.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+// Writes activation k of token t (M tokens) into the MFMA A-operand layout:
+// its fp16 hi and lo parts at the code-order position of its super-block.
+template <int KIND>
+__device__ __forceinline__ void gm_put_a(uint16_t* a16, int M, int t, int k, float v) {
+    int r8, gg, el;
+    gm_kinv<KIND>(k & 255, r8, gg, el);
+    const _Float16 hi = (_Float16)v;
+    const _Float16 lo = (_Float16)(v - (float)hi);
+    const int base = (((((k >> 8) * 8 + r8) * M + t) * 4 + gg) * 2) * 8 + el;
+    a16[base] = __builtin_bit_cast(uint16_t, hi);
+    a16[base + 8] = __builtin_bit_cast(uint16_t, lo);
+}
+
+// The activations of ONE token formed by a prologue go straight into the A
+// layout: element i = tid + j*nth is held by consecutive lanes, so 32 lanes
+// hold a 32-value group and reduce its sum with shuffles.
+template <int KIND>
+__device__ __forceinline__ void gm_put_one(uint16_t* a16, float* xsum, int i, float v) {
+    gm_put_a<KIND>(a16, 1, 0, i, v);
+    float sum = v;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    if ((i & 31) == 0) xsum[i >> 5] = sum;
+}
+
+// Forms the activation vector of ONE token (K values) directly into the
+// MFMA layout + group sums; every block computes the same values. Every
+// operand is requested before the first one is used (one memory round trip
+// instead of one per dependent load): a thread keeps up to GM_PR elements
+// of each input in registers; xf [K floats] is scratch for the rest.
+constexpr int GM_PR = 8;
+constexpr int GM_SPR = 4;  // attention splits whose partials are held in registers
+
+template <int KIND>
+__device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f, float* xf, uint16_t* a16,
+                            float* xsum) {
+    __shared__ double red[16];
+    const int tid = threadIdx.x, nth = blockDim.x;
+    if (f.pro == GM_PRO_RMSNORM || f.pro == GM_PRO_GATED) {
+        const bool gated = f.pro == GM_PRO_GATED;
+        float xr[GM_PR], wr[GM_PR], zr[GM_PR];
+#pragma unroll
+        for (int j = 0; j < GM_PR; ++j) {
+            const int i = tid + j * nth;
+            if (i < K) {
+                xr[j] = x[i];
+                wr[j] = f.pw[i];
+                zr[j] = gated ? f.pz[i] : 0.f;
+            }
+        }
+        // elementwise.hip k_rmsnorm: double sum of squares, x * inv * w;
+        // mamba.hip k_gated_norm: v = y * silu(z), double variance, float rsqrt
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < GM_PR; ++j) {
+            const int i = tid + j * nth;
+            if (i < K) {
+                float v = xr[j];
+                if (gated) v = v * (zr[j] / (1.0f + expf(-zr[j])));
+                xr[j] = v;
+                ss += (double)v * v;
+            }
+        }
+        for (int i = tid + GM_PR * nth; i < K; i += nth) {  // elements beyond the registers
+            float v = x[i];
+            if (gated) v = v * (f.pz[i] / (1.0f + expf(-f.pz[i])));
+            xf[i] = v;
+            ss += (double)v * v;
+        }
+        const double tot = gm_block_sum(ss, red);
+        float inv;
+        if (gated) {
+            inv = 1.0f / sqrtf((float)(tot / (double)K) + f.eps);
+        } else {
+            const double invd = 1.0 / sqrt(tot / (double)K + (double)f.eps);
+            inv = isfinite(invd) ? (float)invd : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < GM_PR; ++j) {
+            const int i = tid + j * nth;
+            if (i < K) gm_put_one<KIND>(a16, xsum, i, xr[j] * inv * wr[j]);
+        }
+        for (int i = tid + GM_PR * nth; i < K; i += nth) gm_put_one<KIND>(a16, xsum, i, xf[i] * inv * f.pw[i]);
+    } else {
+        // attention.hip k_attn_combine for all H heads at once. Output
+        // i = h*hd + c. (A) every (m, l) pair goes to LDS and every thread
+        // requests the partial outputs of its elements; (B) thread h turns
+        // its head's pairs into split weights; (C) ordered weighted sums.
+        const int H = f.H, S = f.splits, hd = f.hd;
+        float* sm = xf;              // [H][S] running max, then split weight
+        float* sl = xf + H * S;      // [H][S] sums
+        float* sinv = sl + H * S;    // [H]
+        for (int q = tid; q < H * S; q += nth) {
+            const int h = q / S, sp = q - h * S;
+            const float* p = f.ml + (((size_t)(h / f.G) * S + sp) * f.G + h % f.G) * 2;
+            sm[q] = p[0];
+            sl[q] = p[1];
+        }
+        float ov[GM_PR][GM_SPR];
+#pragma unroll
+        for (int j = 0; j < GM_PR; ++j) {
+            const int i = tid + j * nth;
+            if (i < K) {
+                const int h = i / hd, c = i - h * hd;
+                const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + c;
+#pragma unroll
+                for (int sp = 0; sp < GM_SPR; ++sp)
+                    if (sp < S) ov[j][sp] = op[(size_t)sp * f.G * hd];
+            }
+        }
+        __syncthreads();
+        if (tid < H) {
+            float Mx = -INFINITY;
+            for (int sp = 0; sp < S; ++sp)
+                if (sl[tid * S + sp] > 0.f) Mx = fmaxf(Mx, sm[tid * S + sp]);
+            float L = 0.f;
+            for (int sp = 0; sp < S; ++sp) {
+                const float l = sl[tid * S + sp];
+                const float w = l > 0.f ? expf(sm[tid * S + sp] - Mx) : 0.f;
+                sm[tid * S + sp] = w;
+                L += w * l;
+            }
+            sinv[tid] = L > 0.f ? 1.0f / L : 0.0f;
+        }
+        __syncthreads();
+        auto merge = [&](int i, const float* o4) {
+            const int h = i / hd, c = i - h * hd;
+            const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + c;
+            float acc = 0.f;
+            for (int sp = 0; sp < S; ++sp) {
+                const float w = sm[h * S + sp];
+                const float o = (o4 && sp < GM_SPR) ? o4[sp] : op[(size_t)sp * f.G * hd];
+                if (w != 0.f) acc += w * o;
+            }
+            return acc * sinv[h];
+        };
+#pragma unroll
+        for (int j = 0; j < GM_PR; ++j) {
+            const int i = tid + j * nth;
+            if (i < K) gm_put_one<KIND>(a16, xsum, i, merge(i, ov[j]));
+        }
+        for (int i = tid + GM_PR * nth; i < K; i += nth) gm_put_one<KIND>(a16, xsum, i, merge(i, nullptr));
+    }
+    __syncthreads();
+}
+
+// Epilogue operands of one output row, requested at kernel start.
+struct GmEpiPre {
+    float v[16];  // ADD: v[0] = y[n]; CONV: taps [0,ck), bias ck, window ck+1..
+    int slot;
+};
+
+__device__ __forceinline__ void gm_epi_prefetch(const float* __restrict__ y, int n, const GmFuse& f, GmEpiPre& e) {
+    if (f.epi == GM_EPI_ADD) {
+        e.v[0] = y[n];
+    } else if (f.epi == GM_EPI_QKV) {
+        e.slot = *f.slot;
+    } else if (f.epi == GM_EPI_CONV) {
+        const int c = n - f.c0;
+        if (c >= 0 && c < f.cdim && f.ck <= 8) {
+            const int k = f.ck, wl = k > 1 ? k - 1 : 1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (j < k) e.v[j] = f.conv_w[(size_t)c * k + j];
+            e.v[8] = f.conv_b ? f.conv_b[c] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 7; ++j)
+                if (j < wl) e.v[9 + j] = f.conv_win[(size_t)c * wl + j];
+        }
+    }
+}
+
+// Output n (value v) of a fused GEMV, ONE token; `pre` holds the operands
+// fetched at kernel start (use_pre) or, if not, loads them now.
+__device__ __forceinline__ void gm_epilogue(float* __restrict__ y, int yi, int n, float v, const GmFuse& f,
+                                            const GmEpiPre& e, bool use_pre) {
+    const GmEpiPre* pre = use_pre ? &e : nullptr;
+    if (f.epi == GM_EPI_ADD) {
+        y[yi] = (pre ? pre->v[0] : y[yi]) + v;
+    } else if (f.epi == GM_EPI_QKV) {
+        if (n < f.n0) {
+            y[yi] = v;
+        } else {
+            const int r = n - f.n0;
+            const size_t base = (size_t)(pre ? pre->slot : *f.slot) * f.kvd;
+            if (r < f.kvd) f.kc[base + r] = f32_to_f16(v);
+            else f.vc[base + r - f.kvd] = f32_to_f16(v);
+        }
+    } else {  // GM_EPI_CONV: mamba.hip k_step_conv on channel n - c0
+#pragma clang fp contract(off)
+        const int c = n - f.c0;
+        if (c >= 0 && c < f.cdim) {
+            const int k = f.ck, wl = k > 1 ? k - 1 : 1;
+            float* wc = f.conv_win + (size_t)c * wl;
+            if (pre && k <= 8) {
+                float acc = pre->v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j < k) acc += pre->v[j] * ((j == k - 1) ? v : pre->v[9 + j]);
+                y[yi] = acc / (1.0f + expf(-acc));
+#pragma unroll
+                for (int j = 0; j < 7; ++j)
+                    if (j + 1 < wl) wc[j] = pre->v[10 + j];
+                wc[wl - 1] = v;
+            } else {
+                float acc = f.conv_b ? f.conv_b[c] : 0.0f;
+                for (int j = 0; j < k; ++j) acc += f.conv_w[(size_t)c * k + j] * ((j == k - 1) ? v : wc[j]);
+                y[yi] = acc / (1.0f + expf(-acc));
+                for (int j = 0; j + 1 < wl; ++j) wc[j] = wc[j + 1];
+                wc[wl - 1] = v;
+            }
+        } else {
+            y[yi] = v;
+        }
+    }
+}
+
 // Weight bytes move in "steps": SS consecutive super-blocks of the 16 rows
 // of a tile. A wave reads a step with contiguous 16-byte pieces (each row's
 // SS*SB_BYTES bytes are contiguous, so a load instruction touches few
@@ -168,10 +399,10 @@ struct GmStep {
 //                     [red: 2*WB*16*M f32][weight slices: WB x GmStep::BYTES]
 // Blocks of up to 16 waves for one token pair, up to 8 (twice the
 // registers per lane) for more.
-template <int KIND, int TP, int SS>
+template <int KIND, int TP, int SS, bool FUSED>
 __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                     float* __restrict__ y, int M, int K, int N, size_t rowb,
-                                                    int WB, int tpb, int spw) {
+                                                    int WB, int tpb, int spw, GmFuse f) {
     constexpr int DW = GmCfg<KIND>::DW;
     using St = GmStep<KIND, SS>;
     extern __shared__ __align__(16) unsigned char gm_smem[];
@@ -183,6 +414,7 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
     float* xsum = (float*)(achunk + nchunks);
     float* red = xsum + NSB * 8 * M;
     unsigned char* slices = (unsigned char*)(red + 2 * WB * 16 * M);
+    float* xf = (float*)(slices + WB * St::BYTES);  // prologue output [K] (M = 1)
     const int tid = threadIdx.x, nth = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -202,6 +434,10 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
     const int tile0 = blockIdx.x * tpb;
     const int tile1 = min(ntiles, tile0 + tpb);
     const int items = ns > 0 ? (tile1 - tile0) * ns : 0;
+    // epilogue operands of the first tile's outputs (one token)
+    GmEpiPre epre;
+    if (FUSED && f.epi != GM_EPI_STORE && tid < 16 && tile0 < tile1 && tile0 * 16 + tid < N)
+        gm_epi_prefetch(y, tile0 * 16 + tid, f, epre);
 
     uint4 P[St::PPL];
     auto load_item = [&](int it) {
@@ -214,7 +450,13 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
                 const int r = q / St::PPR, j = q - r * St::PPR;
                 int n = tile * 16 + r;
                 n = n < N ? n : N - 1;
-                P[i] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const gm_u4*)(base + (size_t)n * rowb + 16 * j)));
+                const uint8_t* src = base;
+                if (FUSED && f.w1 && n >= f.n0) {  // weight segments (tile-aligned)
+                    const bool second = n < f.n0 + f.n1;
+                    src = (const uint8_t*)(second ? f.w1 : f.w2) + (base - W);
+                    n -= second ? f.n0 : f.n0 + f.n1;
+                }
+                P[i] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const gm_u4*)(src + (size_t)n * rowb + 16 * j)));
             }
         }
     };
@@ -232,48 +474,42 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
     // 32-value sums. Coalesced float4 reads; each group of 8 lanes covers
     // one 32-value group and reduces its sum with shuffles. (K is a
     // multiple of 256, so every wave runs the loop the same number of times.)
-    // The first activation reads are issued before the first step's weight
-    // reads (which would otherwise queue ahead of them), the conversion runs
-    // while the weight bytes are in flight.
+    // The conversion runs while the first step's weight bytes are in flight.
     if (tid == 0) *zero = make_uint4(0, 0, 0, 0);
     const int K4 = K >> 2, xtotal = M * K4;
-    auto xload = [&](int idx) {
-        const int t = idx / K4, k = (idx - t * K4) * 4;
-        return *(const float4*)(x + (size_t)t * K + k);
-    };
-    uint16_t* a16 = (uint16_t*)achunk;
-    auto stage = [&](int idx, float4 v4) {
-        const int t = idx / K4, k = (idx - t * K4) * 4;
-        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-        const int sb = k >> 8;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int kk = (k + j) & 255;
-            int r8, gg, el;
-            gm_kinv<KIND>(kk, r8, gg, el);
-            const _Float16 hi = (_Float16)vv[j];
-            const _Float16 lo = (_Float16)(vv[j] - (float)hi);
-            const int base = ((((sb * 8 + r8) * M + t) * 4 + gg) * 2) * 8 + el;
-            a16[base] = __builtin_bit_cast(uint16_t, hi);
-            a16[base + 8] = __builtin_bit_cast(uint16_t, lo);
-        }
-        float sum = (vv[0] + vv[1]) + (vv[2] + vv[3]);
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        if ((idx & 7) == 0) xsum[(k >> 5) * M + t] = sum;
-    };
-    constexpr int XP = 4;
-    float4 xpre[XP];
-#pragma unroll
-    for (int i = 0; i < XP; ++i)
-        if (tid + i * nth < xtotal) xpre[i] = xload(tid + i * nth);
+    // the first step's weight bytes are requested before anything else
     if (items > 0) load_item(0);
+    uint16_t* a16 = (uint16_t*)achunk;
+    if (FUSED && f.pro != GM_PRO_NONE) {
+        // one token formed by the prologue straight into the A layout
+        gm_prologue<KIND>(x, K, f, xf, a16, xsum);
+    } else {
+        auto xload = [&](int idx) {
+            const int t = idx / K4, k = (idx - t * K4) * 4;
+            return *(const float4*)(x + (size_t)t * K + k);
+        };
+        auto stage = [&](int idx, float4 v4) {
+            const int t = idx / K4, k = (idx - t * K4) * 4;
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-    for (int i = 0; i < XP; ++i)
-        if (tid + i * nth < xtotal) stage(tid + i * nth, xpre[i]);
-    for (int idx = tid + XP * nth; idx < xtotal; idx += nth) stage(idx, xload(idx));
-    __syncthreads();
+            for (int j = 0; j < 4; ++j) gm_put_a<KIND>(a16, M, t, k + j, vv[j]);
+            float sum = (vv[0] + vv[1]) + (vv[2] + vv[3]);
+            sum += __shfl_xor(sum, 1, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            sum += __shfl_xor(sum, 4, 64);
+            if ((idx & 7) == 0) xsum[(k >> 5) * M + t] = sum;
+        };
+        constexpr int XP = 4;
+        float4 xpre[XP];
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+            if (tid + i * nth < xtotal) xpre[i] = xload(tid + i * nth);
+#pragma unroll
+        for (int i = 0; i < XP; ++i)
+            if (tid + i * nth < xtotal) stage(tid + i * nth, xpre[i]);
+        for (int idx = tid + XP * nth; idx < xtotal; idx += nth) stage(idx, xload(idx));
+        __syncthreads();
+    }
 
     int buf = 0;
     for (int tile = tile0; tile < tile1; ++tile) {
@@ -374,7 +610,10 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
             float v = 0.f;
             for (int wv = 0; wv < WB; ++wv) v += rb[(wv * M + t) * 16 + nn];
             const int n = tile * 16 + nn;
-            if (n < N) y[(size_t)t * N + n] = v;
+            if (n < N) {
+                if (!FUSED || f.epi == GM_EPI_STORE) y[(size_t)t * N + n] = v;
+                else gm_epilogue(y, t * N + n, n, v, f, epre, tile == tile0 && i == tid && tid < 16);
+            }
         }
         buf ^= 1;
     }
@@ -385,19 +624,21 @@ static int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
-constexpr size_t GM_LDS_MAX = 160 * 1024;
+// dynamic LDS budget: 160 KB per workgroup less a reserve for the static
+// arrays of the fusion prologue
+constexpr size_t GM_LDS_MAX = 160 * 1024 - 512;
 
 template <int KIND, int SS>
-static size_t gm_lds_bytes(int K, int M, int WB) {
+static size_t gm_lds_bytes(int K, int M, int WB, bool pro) {
     const size_t nsb = K / 256;
     return 16 + nsb * 8 * M * 8 * 16 + nsb * 8 * M * 4 + 2 * (size_t)WB * 16 * M * 4 +
-           (size_t)WB * GmStep<KIND, SS>::BYTES;
+           (size_t)WB * GmStep<KIND, SS>::BYTES + (pro ? (size_t)K * 4 : 0);
 }
 
 // Waves per block and steps per wave: as many waves as there are steps (up
 // to 16), fewer if the block's LDS would not fit. 0 if nothing fits.
 template <int KIND, int SS>
-static int gm_split(int K, int M, int& WB, int& spw) {
+static int gm_split(int K, int M, bool pro, int& WB, int& spw) {
     const int nsteps = K / 256 / SS;
     const int wcap = M <= 2 ? 16 : 8;
     int wmax = env_int("GH_GEMVM_WB", wcap);
@@ -405,17 +646,19 @@ static int gm_split(int K, int M, int& WB, int& spw) {
     for (int wb = nsteps < wmax ? nsteps : wmax; wb >= 1; --wb) {
         spw = (nsteps + wb - 1) / wb;
         WB = (nsteps + spw - 1) / spw;
-        if (gm_lds_bytes<KIND, SS>(K, M, WB) <= GM_LDS_MAX) return 1;
+        if (gm_lds_bytes<KIND, SS>(K, M, WB, pro) <= GM_LDS_MAX) return 1;
     }
     return 0;
 }
 
-template <int KIND, int TP, int SS>
-static int gm_launch(const float* x, const void* w, float* y, int M, int K, int N) {
-    auto kern = k_gemv_mfma<KIND, TP, SS>;
+template <int KIND, int TP, int SS, bool FUSED>
+static int gm_launch(const float* x, const void* w, float* y, int M, int K, int N, const GmFuse& f) {
+    auto kern = k_gemv_mfma<KIND, TP, SS, FUSED>;
+    const bool pro = f.pro != GM_PRO_NONE;
     int WB, spw;
-    if (!gm_split<KIND, SS>(K, M, WB, spw)) return fail(GH_EINVAL, "gemv_mfma: K=%d M=%d does not fit LDS", K, M);
-    const size_t lds = gm_lds_bytes<KIND, SS>(K, M, WB);
+    if (!gm_split<KIND, SS>(K, M, pro, WB, spw))
+        return fail(GH_EINVAL, "gemv_mfma: K=%d M=%d does not fit LDS", K, M);
+    const size_t lds = gm_lds_bytes<KIND, SS>(K, M, WB, pro);
     static bool attr_set = false;
     if (!attr_set) {
         GH_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GM_LDS_MAX));
@@ -432,27 +675,27 @@ static int gm_launch(const float* x, const void* w, float* y, int M, int K, int 
     const int tpb = (ntiles + blocks - 1) / blocks;
     blocks = (ntiles + tpb - 1) / tpb;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * WB), lds, stream(), x, (const uint8_t*)w, y, M, K, N,
-                       row_bytes(KIND, K), WB, tpb, spw);
+                       row_bytes(KIND, K), WB, tpb, spw, f);
     GH_LAUNCHED("k_gemv_mfma");
     return GH_OK;
 }
 
 // Q4_K moves two super-blocks per step when K allows, Q8_0 one
 template <int KIND>
-static bool gm_fits(int K, int M) {
+static bool gm_fits(int K, int M, bool pro) {
     int WB, spw;
     if constexpr (KIND == 3) {
-        if ((K / 256) % 2 == 0) return gm_split<KIND, 2>(K, M, WB, spw);
+        if ((K / 256) % 2 == 0) return gm_split<KIND, 2>(K, M, pro, WB, spw);
     }
-    return gm_split<KIND, 1>(K, M, WB, spw);
+    return gm_split<KIND, 1>(K, M, pro, WB, spw);
 }
 
-template <int KIND, int TP>
-static int gm_ss(const float* x, const void* w, float* y, int M, int K, int N) {
+template <int KIND, int TP, bool FUSED = false>
+static int gm_ss(const float* x, const void* w, float* y, int M, int K, int N, const GmFuse& f = GmFuse()) {
     if constexpr (KIND == 3) {
-        if ((K / 256) % 2 == 0) return gm_launch<KIND, TP, 2>(x, w, y, M, K, N);
+        if ((K / 256) % 2 == 0) return gm_launch<KIND, TP, 2, FUSED>(x, w, y, M, K, N, f);
     }
-    return gm_launch<KIND, TP, 1>(x, w, y, M, K, N);
+    return gm_launch<KIND, TP, 1, FUSED>(x, w, y, M, K, N, f);
 }
 
 template <int KIND>
@@ -473,7 +716,7 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
     if (!enabled || (kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
     if (kind == 2 && M == 1 && !q8_m1) return 0;
     int mc = M;
-    while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc) : gm_fits<2>(K, mc))) --mc;
+    while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc, false) : gm_fits<2>(K, mc, false))) --mc;
     if (mc < 1) return 0;
     // y is [M][N]; a token group [t0, t0+mc) is a contiguous slice of x and y
     for (int t0 = 0; t0 < M; t0 += mc) {
@@ -484,6 +727,16 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
         if (*rc) return 1;
     }
     return 1;
+}
+
+int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, const GmFuse& f) {
+    if ((kind != 2 && kind != 3) || K % 256 != 0) return fail(GH_EUNSUPPORTED, "gemv_fused: kind %d K=%d", kind, K);
+    if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
+    if (f.pro == GM_PRO_ATTN && (f.splits > 64 || f.H * f.hd != K))
+        return fail(GH_EUNSUPPORTED, "gemv_fused: attention merge of %d splits", f.splits);
+    if (!(kind == 3 ? gm_fits<3>(K, 1, f.pro != GM_PRO_NONE) : gm_fits<2>(K, 1, f.pro != GM_PRO_NONE)))
+        return fail(GH_EUNSUPPORTED, "gemv_fused: K=%d does not fit LDS", K);
+    return kind == 3 ? gm_ss<3, 1, true>(x, w, y, 1, K, N, f) : gm_ss<2, 1, true>(x, w, y, 1, K, N, f);
 }
 
 }  // namespace gh

@@ -12,13 +12,25 @@
 #include <string>
 #include <vector>
 
-#include "gh_common.h"
+#include "gemv_fuse.h"
 
 namespace gh {
 
 int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
 int launch_f32_to_f16(const float* s, uint16_t* d, int64_t n);
 int launch_argmax(const float* l, int V, int32_t* out_dev);
+int launch_argmax_record(const float* l, int V, int32_t* out_dev, int32_t* step, int32_t* ids, int cap);
+int attn_decode_partials_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, int H, int KV, int hd,
+                                int cache_max, const int32_t* ctl, float scale, const float** o_part,
+                                const float** ml, int* splits);
+int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void* w_in, const float* conv_w,
+                     const float* conv_b, const float* dt_bias, const float* a_log, const float* D,
+                     const float* norm_w, const void* w_out, float* conv_state, float* ssm_state, float* out,
+                     bool add, int d, int d_inner, int conv_dim, int n_heads, int d_head, int d_state, int k,
+                     float eps, int kind);
+int moe_decode_fused(float* xres, const float* nw, float eps, const float* rw, const float* bias, const void* gates,
+                     const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, int N,
+                     int d, int E, int ne, int K, int SH, int qkind);
 int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,
                       float scale, int window);
 int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV, int hd,
@@ -63,6 +75,30 @@ __global__ void k_record_token(int32_t* ctl, int32_t* ids, int cap) {
     const int s = ctl[CTL_STEP];
     if (s < cap) ids[s] = ctl[CTL_TOKEN];
     ctl[CTL_STEP] = s + 1;
+}
+
+// Start of a decode step: the cache slot of the new token (k_alloc_slot)
+// and its embedding row (elementwise.hip k_embed_half) in one launch.
+__global__ void k_step_begin(int32_t* ctl, const uint16_t* __restrict__ tab, float* __restrict__ x, int dim,
+                             int vocab) {
+    if (threadIdx.x == 0) {
+        const int cap = ctl[CTL_CAP], pin = ctl[CTL_PINNED];
+        int len = ctl[CTL_LEN], start = ctl[CTL_START], slot;
+        if (len < cap) {
+            slot = len;
+            if (len >= pin) slot = pin + ((start + (len - pin)) % (cap - pin));
+            ++len;
+        } else {
+            slot = pin + (start % (cap - pin));
+            start = (start + 1) % (cap - pin);
+        }
+        ctl[CTL_LEN] = len;
+        ctl[CTL_START] = start;
+        ctl[CTL_SLOT] = slot;
+    }
+    const int id = ctl[CTL_TOKEN];
+    for (int i = threadIdx.x; i < dim; i += blockDim.x)
+        x[i] = (id < 0 || id >= vocab) ? 0.f : f16_to_f32(tab[(size_t)id * dim + i]);
 }
 
 }  // namespace gh
@@ -198,6 +234,83 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
     }
     GH_LAUNCHED("decode_step");
     return GH_OK;
+}
+
+// The same step with every sub-layer fused into few launches: per Mamba
+// layer 3 ([norm+in_proj+conv], scan, [gated norm+out_proj+residual]), per
+// attention layer 3 ([norm+q/k/v+cache store], split-K partials,
+// [merge+wo+residual]), per MoE 3 ([norm+route], gate/up, [down+combine+
+// residual]); begin, lm head and argmax+record around them. Returns
+// GH_EUNSUPPORTED before launching anything if a shape does not fit.
+static bool fused_supported(const gh_granite* g) {
+    const int k = g->qkind;
+    if (k != 2 && k != 3) return false;
+    if (g->d % 256 || g->di % 256 || g->qd % 256 || g->qd % 16 || g->kvd % 16) return false;
+    if (g->mds != 64 && g->mds != 128) return false;
+    const int chunk_min = 128;
+    if ((g->max_ctx + chunk_min - 1) / chunk_min > 64) return false;  // attention merge in the wo prologue
+    return true;
+}
+
+static int decode_step_fused(gh_granite* g, bool argmax) {
+    const int d = g->d;
+    hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(256), 0, stream(), g->ctl, (const uint16_t*)g->W("tok_embeddings"),
+                       g->x, d, g->V);
+    GH_LAUNCHED("k_step_begin");
+    for (int l = 0; l < g->L; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        if (g->lt[l] == 0) {
+            const std::string mp = pre + "mamba.";
+            GHC(mamba_step_fused(g->x, g->F(pre + "attn_norm"), g->eps, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
+                                 g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"), g->F(mp + "D"),
+                                 g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->conv[l], g->ssm[l], g->x, true, d,
+                                 g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck, g->eps, g->qkind));
+        } else {
+            GmFuse f1;
+            f1.pro = GM_PRO_RMSNORM;
+            f1.pw = g->F(pre + "attn_norm");
+            f1.eps = g->eps;
+            f1.w1 = g->W(pre + "wk");
+            f1.w2 = g->W(pre + "wv");
+            f1.n0 = g->qd;
+            f1.n1 = g->kvd;
+            f1.epi = GM_EPI_QKV;
+            f1.kc = g->kc[l];
+            f1.vc = g->vc[l];
+            f1.slot = g->ctl + CTL_SLOT;
+            f1.kvd = g->kvd;
+            GHC(gemv_fused(g->x, g->W(pre + "wq"), g->q, d, g->qd + 2 * g->kvd, g->qkind, f1));
+            GmFuse f3;
+            GHC(attn_decode_partials_devctl(g->q, g->kc[l], g->vc[l], g->H, g->KV, g->hd, g->max_ctx, g->ctl, g->scale,
+                                            &f3.o_part, &f3.ml, &f3.splits));
+            f3.pro = GM_PRO_ATTN;
+            f3.H = g->H;
+            f3.KV = g->KV;
+            f3.G = g->H / g->KV;
+            f3.hd = g->hd;
+            f3.epi = GM_EPI_ADD;
+            GHC(gemv_fused(g->q, g->W(pre + "wo"), g->x, g->qd, d, g->qkind, f3));
+        }
+        GHC(moe_decode_fused(g->x, g->F(pre + "ffn_norm"), g->eps, g->F(pre + "moe_router"), nullptr,
+                             g->W(pre + "moe_gate"), g->W(pre + "moe_up"), g->W(pre + "moe_down"),
+                             g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"), g->W(pre + "moe_sh_down"), 1, d, g->E,
+                             g->ne, g->K, g->SH, g->qkind));
+    }
+    GHC(gh_rmsnorm_forward(g->x, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
+    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    if (argmax)
+        GHC(launch_argmax_record(g->logits, g->V, g->ctl + CTL_TOKEN, g->ctl + CTL_STEP, g->gen_ids, g->max_ctx));
+    GH_LAUNCHED("decode_step");
+    return GH_OK;
+}
+
+static int decode_step(gh_granite* g, bool argmax) {
+    static const int fused = [] {
+        const char* e = getenv("GH_DECODE_FUSED");
+        return e ? atoi(e) : 1;
+    }();
+    if (fused && fused_supported(g)) return decode_step_fused(g, argmax);
+    return decode_step_dev(g, argmax);
 }
 
 extern "C" {
@@ -432,7 +545,7 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
 int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host) {
     GH_REQUIRE(g != nullptr, "granite_decode: null model");
     GH_HIP(hipMemcpyAsync(g->ctl + CTL_TOKEN, &token, 4, hipMemcpyHostToDevice, stream()));
-    GHC(decode_step_dev(g, false));
+    GHC(decode_step(g, false));
     g->host_len = g->host_len < g->max_ctx ? g->host_len + 1 : g->host_len;
     if (logits_host) GH_HIP(hipMemcpyAsync(logits_host, g->logits, (size_t)g->V * 4, hipMemcpyDeviceToHost, stream()));
     GH_HIP(hipStreamSynchronize(stream()));
@@ -452,7 +565,7 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
     int done = 1;
     if (n_new > 1) {
         // one plain step (also sizes every workspace before a capture)
-        GHC(decode_step_dev(g, true));
+        GHC(decode_step(g, true));
         ++done;
     }
     if (use_graph && done < n_new) {
@@ -466,7 +579,7 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
                 gh_set_stream((void*)s);
             }
             GH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-            int rc = decode_step_dev(g, true);
+            int rc = decode_step(g, true);
             hipGraph_t graph = nullptr;
             hipError_t e = hipStreamEndCapture(s, &graph);
             if (own) {
@@ -483,7 +596,7 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
         }
         for (; done < n_new; ++done) GH_HIP(hipGraphLaunch(g->graph_exec, stream()));
     } else {
-        for (; done < n_new; ++done) GHC(decode_step_dev(g, true));
+        for (; done < n_new; ++done) GHC(decode_step(g, true));
     }
     GH_HIP(hipMemcpyAsync(ids_host, g->gen_ids, (size_t)n_new * 4, hipMemcpyDeviceToHost, stream()));
     GH_HIP(hipStreamSynchronize(stream()));

@@ -14,7 +14,7 @@
 // state across chunks, and the chunk outputs (intra-chunk M X and the
 // C S_in correction on the matrix cores). Decode is one fused conv+update
 // kernel between the two projections.
-#include "gh_common.h"
+#include "gemv_fuse.h"
 
 namespace gh {
 
@@ -465,6 +465,52 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
     return linear_any(normed, w_out, out, T, d_inner, d, kind);
 }
 
+// Single-token Mamba-2 layer as three launches: (1) [RMSNorm] + in_proj
+// with the conv step + SiLU + window shift in its epilogue, (2) the state
+// update, (3) gated norm + out_proj [+ residual add into `out`]. Returns
+// GH_EUNSUPPORTED (launching nothing) if the shapes do not fit the fused GEMV.
+int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void* w_in, const float* conv_w,
+                     const float* conv_b, const float* dt_bias, const float* a_log, const float* D,
+                     const float* norm_w, const void* w_out, float* conv_state, float* ssm_state, float* out,
+                     bool add, int d, int d_inner, int conv_dim, int n_heads, int d_head, int d_state, int k,
+                     float eps, int kind) {
+    if ((kind != 2 && kind != 3) || d % 256 || d_inner % 256 || (d_state != 64 && d_state != 128))
+        return GH_EUNSUPPORTED;
+    const int proj = d_inner + conv_dim + n_heads;
+    float* pr = (float*)workspace(WS_MAMBA_PROJ, (size_t)proj * 4);
+    float* yb = (float*)workspace(WS_MAMBA_Y, (size_t)d_inner * 4 * 2);
+    if (!pr || !yb) return fail(GH_ENOMEM, "mamba: workspace");
+    GmFuse f1;
+    f1.pro = nw ? GM_PRO_RMSNORM : GM_PRO_NONE;
+    f1.pw = nw;
+    f1.eps = norm_eps;
+    f1.epi = GM_EPI_CONV;
+    f1.conv_w = conv_w;
+    f1.conv_b = conv_b;
+    f1.conv_win = conv_state;
+    f1.c0 = d_inner;
+    f1.cdim = conv_dim;
+    f1.ck = k;
+    int rc = gemv_fused(x, w_in, pr, d, proj, kind, f1);
+    if (rc) return rc;
+    const float* xbc = pr + d_inner;  // conv output, in place of the raw xBC
+    const int rows_per_block = 256 / (d_state / 8);
+    if (d_state == 128)
+        hipLaunchKernelGGL(k_step_scan<128>, dim3(cdiv(d_head, rows_per_block), n_heads), dim3(256), 0, stream(), xbc,
+                           pr + d_inner + conv_dim, dt_bias, a_log, D, ssm_state, yb, d_inner, d_head);
+    else
+        hipLaunchKernelGGL(k_step_scan<64>, dim3(cdiv(d_head, rows_per_block), n_heads), dim3(256), 0, stream(), xbc,
+                           pr + d_inner + conv_dim, dt_bias, a_log, D, ssm_state, yb, d_inner, d_head);
+    GH_LAUNCHED("k_step_scan");
+    GmFuse f3;
+    f3.pro = GM_PRO_GATED;
+    f3.pz = pr;  // z = in_proj rows [0, d_inner)
+    f3.pw = norm_w;
+    f3.eps = eps;
+    f3.epi = add ? GM_EPI_ADD : GM_EPI_STORE;
+    return gemv_fused(yb, w_out, out, d_inner, d, kind, f3);
+}
+
 }  // namespace gh
 
 using namespace gh;
@@ -509,6 +555,12 @@ int gh_mamba2_step_half(const float* x, const void* w_in, const float* conv_w, c
     GH_REQUIRE(d_state == 64 || d_state == 128, "mamba2_step: d_state %d (64 or 128)", d_state);
     GH_REQUIRE(qkind >= -1 && qkind <= 3, "mamba: unknown qkind %d", qkind);
     const int kind = qkind < 0 ? 4 : qkind;
+    {
+        const int rc = mamba_step_fused(x, nullptr, 0.f, w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w, w_out,
+                                        conv_state, ssm_state, out, false, d, d_inner, conv_dim, n_heads, d_head,
+                                        d_state, k, eps, kind);
+        if (rc != GH_EUNSUPPORTED) return rc;
+    }
     const int proj = d_inner + conv_dim + n_heads;
     float* pr = (float*)workspace(WS_MAMBA_PROJ, (size_t)proj * 4);
     float* xbc = (float*)workspace(WS_MAMBA_XBC, (size_t)conv_dim * 4);

@@ -17,46 +17,108 @@ namespace gh {
 // core/moe_cpu.cpp:218-256, one block per token, same arithmetic order:
 // logit_e = dot_row: s += ((p0 + p1) + p2) + p3 over groups of 4, left to
 // right, no fused multiply-add. The group terms are independent, so the
-// block computes them in parallel for 64 groups at a time into LDS and lane e
-// then adds its 64 terms in order -- the sequential sum stays exact while
-// the weight loads are spread over the block. softmax_row
-// (core/math_cpu.cpp:546-558: sequential sum, exp rounded once from double
-// = correctly rounded), selection on p + bias by K rounds of strict '>'
-// argmax with the lowest index winning ties, weights from the unbiased p
-// renormalised (uniform if their sum <= 1e-8).
-constexpr int ROUTE_G = 64;  // groups of 4 per pass
+// block computes all of them in parallel into LDS and lane e then adds its
+// terms in order -- the sequential sum stays exact while the weight loads
+// are spread over the block (the first batch is requested together with the
+// activations). softmax_row (core/math_cpu.cpp:546-558: sequential sum, exp
+// rounded once from double = correctly rounded), selection on p + bias by K
+// rounds of strict '>' argmax with the lowest index winning ties, weights
+// from the unbiased p renormalised (uniform if their sum <= 1e-8).
+// LDS: x [d] | terms [ne][gw + 1] for a window of gw groups (all groups
+// when they fit; the lane sums run on across windows, still in order).
+constexpr int ROUTE_RB = 8;  // float4 weight loads per thread per batch
+// With `nw` set, the token is first RMS-normalised (elementwise.hip
+// k_rmsnorm arithmetic) and the normalised row is also written to xn.
 __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, const float* __restrict__ rw,
                                                const float* __restrict__ bias, float* __restrict__ probs,
                                                int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
-                                               int K) {
+                                               int K, const float* __restrict__ nw, float eps,
+                                               float* __restrict__ xn, int GW) {
 #pragma clang fp contract(off)
-    extern __shared__ float sx[];
-    __shared__ float term[64][ROUTE_G + 1];
+    extern __shared__ float route_sm[];
+    float* sx = route_sm;
+    float* term = route_sm + d;
+    const int ngroups = d / 4, ts = GW + 1;
     __shared__ float sp[64];
+    __shared__ double dred[4];
     const int t = blockIdx.x, tid = threadIdx.x;
-    const float* xt = x + (size_t)t * d;
-    for (int i = tid; i < d; i += 256) sx[i] = xt[i];
+    const float4* xt = (const float4*)(x + (size_t)t * d);
+    const float4* rw4 = (const float4*)rw;
+    auto widx = [&](int q, int g0, int gw) {  // pair q of a window -> float4 index in rw
+        const int e = q / gw;
+        return e * ngroups + g0 + (q - e * gw);
+    };
+    // first batch of router weights, requested with the activations
+    float4 wreg[ROUTE_RB];
+    {
+        const int gw = min(GW, ngroups);
+#pragma unroll
+        for (int b = 0; b < ROUTE_RB; ++b) {
+            const int q = tid + b * 256;
+            if (q < ne * gw) wreg[b] = rw4[widx(q, 0, gw)];
+        }
+    }
+    double ss = 0.0;
+    for (int g = tid; g < ngroups; g += 256) {
+        const float4 v = xt[g];
+        *(float4*)(sx + 4 * g) = v;
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+    if (nw) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) dred[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = dred[0] + dred[1] + dred[2] + dred[3];
+        const double invd = 1.0 / sqrt(tot / (double)d + (double)eps);
+        const float inv = isfinite(invd) ? (float)invd : 0.0f;
+        for (int i = tid; i < d; i += 256) {
+            const float v = sx[i] * inv * nw[i];
+            sx[i] = v;
+            xn[(size_t)t * d + i] = v;
+        }
+    }
     __syncthreads();
-    const int ngroups = d / 4;
-    float s = 0.0f;  // lane e < ne of wave 0 owns logit e
-    for (int g0 = 0; g0 < ngroups; g0 += ROUTE_G) {
-        const int gn = min(ROUTE_G, ngroups - g0);
-        for (int j = tid; j < ne * gn; j += 256) {
-            const int e = j / gn, g = j % gn;
-            const int i = 4 * (g0 + g);
-            const float4 w = *(const float4*)(rw + (size_t)e * d + i);
-            const float p0 = sx[i] * w.x, p1 = sx[i + 1] * w.y, p2 = sx[i + 2] * w.z, p3 = sx[i + 3] * w.w;
-            term[e][g] = ((p0 + p1) + p2) + p3;
+    float s = 0.0f;  // lane e < ne owns logit e
+    for (int g0 = 0; g0 < ngroups; g0 += GW) {
+        const int gw = min(GW, ngroups - g0), np = ne * gw;
+        for (int q0 = 0; q0 < np; q0 += ROUTE_RB * 256) {
+            if (g0 > 0 || q0 > 0) {
+#pragma unroll
+                for (int b = 0; b < ROUTE_RB; ++b) {
+                    const int q = q0 + tid + b * 256;
+                    if (q < np) wreg[b] = rw4[widx(q, g0, gw)];
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < ROUTE_RB; ++b) {
+                const int q = q0 + tid + b * 256;
+                if (q < np) {
+                    const int e = q / gw, gl = q - e * gw;
+                    const int i = 4 * (g0 + gl);
+                    const float4 w = wreg[b];
+                    const float p0 = sx[i] * w.x, p1 = sx[i + 1] * w.y, p2 = sx[i + 2] * w.z, p3 = sx[i + 3] * w.w;
+                    term[e * ts + gl] = ((p0 + p1) + p2) + p3;
+                }
+            }
         }
         __syncthreads();
-        if (tid < ne)
-            for (int g = 0; g < gn; ++g) s += term[tid][g];
+        if (tid < ne) {
+            // in order; the LDS reads are batched so only the adds are serial
+            const float* tr = term + tid * ts;
+            int g = 0;
+            for (; g + 16 <= gw; g += 16) {
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = tr[g + j];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s += v[j];
+            }
+            for (; g < gw; ++g) s += tr[g];
+        }
         __syncthreads();
     }
-    if (tid < ne) {
-        for (int i = 4 * ngroups; i < d; ++i) s += sx[i] * rw[(size_t)tid * d + i];
-        sp[tid] = s;
-    }
+    if (tid < ne) sp[tid] = s;
     __syncthreads();
     if (tid < 64) {
         const int lane = tid;
@@ -116,6 +178,15 @@ __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, cons
         if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
     }
 }
+
+// window of router groups whose terms fit 60 KB of LDS next to the token
+static int route_window(int d, int ne) {
+    const int budget = 60 * 1024 / 4 - d;  // floats, leaving room for the static arrays
+    int gw = budget / ne - 1;
+    if (gw > d / 4) gw = d / 4;
+    return gw < 1 ? 1 : gw;
+}
+static size_t route_lds(int d, int ne) { return ((size_t)d + (size_t)ne * (route_window(d, ne) + 1)) * 4; }
 
 // ========================================================== permutation
 // Stable counting sort of slot ids s = t*K+k by expert, in three
@@ -297,6 +368,108 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
         if (shared) J.out_s[(size_t)(job - J.S) * rows + row] = v;
         else J.out_r[(size_t)job * rows + row] = v;
     }
+}
+
+// Down projections of all K routed experts and the shared expert of token
+// blockIdx.y, merged in the combine order (shared first, then k = 0..K-1,
+// core/moe_cpu.cpp:265-287) and added to the residual row:
+// xres[t][row] += shared + sum_k w[t,k] * down_k (or = without `accumulate`).
+// One wave owns RP rows for every job, so the merge happens in registers
+// (no per-expert outputs). Latency: the token's activation rows are staged
+// in LDS while the routing is read, and the next job's weight bytes are
+// requested while the current job is multiplied.
+constexpr int DC_TPJ = 4;  // tasks per lane per job held in registers
+template <int KIND>
+__global__ void __launch_bounds__(256) k_moe_down_combine(GemvJobs J, const float* __restrict__ wroute,
+                                                          float* __restrict__ xres, int LPR, int accumulate) {
+    constexpr int DW = Task<KIND>::DW;
+    extern __shared__ float dc_act[];  // shared [kin_s] | routed k [kin_r] each
+    const int tok = blockIdx.y, K = J.K;
+    const bool has_sh = J.N > 0;
+    const int RP = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rp = lane / LPR;
+    const int rows = J.rows_r;  // = d for both routed and shared down matrices
+    const int row = (blockIdx.x * 4 + wave) * RP + rp;
+    const int rr = row < rows ? row : rows - 1;
+    const bool active = (blockIdx.x * 4 + wave) * RP < rows;
+    int ek[8];
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        if (k < K) {
+            ek[k] = J.idx[tok * K + k];
+            wk[k] = wroute[tok * K + k];
+        }
+    const int sh_len = has_sh ? J.kin_s : 0;
+    {
+        const float4* src_s = (const float4*)(J.in_s + (size_t)tok * J.kin_s);
+        const float4* src_r = (const float4*)(J.x + (size_t)tok * K * J.kin_r);
+        const int n4s = sh_len / 4, n4 = n4s + K * J.kin_r / 4;
+        for (int i = threadIdx.x; i < n4; i += 256)
+            ((float4*)dc_act)[i] = i < n4s ? src_s[i] : src_r[i - n4s];
+    }
+    auto load_job = [&](int j, uint32_t (*w)[DW]) {
+        const bool shared = j < 0;
+        const int T = (shared ? J.kin_s : J.kin_r) / 64;
+        const size_t rowb = shared ? J.rowb_s : J.rowb_r;
+        const uint8_t* base = (shared ? J.sa : J.wa + (size_t)ek[j] * J.estride) + (size_t)rr * rowb;
+#pragma unroll
+        for (int q = 0; q < DC_TPJ; ++q) {
+            const int t = sub + q * LPR;
+            if (t < T) load_task<KIND>(base, t, w[q]);
+        }
+    };
+    uint32_t wa[DC_TPJ][DW], wb[DC_TPJ][DW];
+    const int first = has_sh ? -1 : 0;
+    if (active) load_job(first, wa);
+    __syncthreads();
+    if (!active) return;
+    float acc = 0.f;
+    for (int j = first; j < K; ++j) {
+        if (j + 1 < K) load_job(j + 1, wb);
+        const bool shared = j < 0;
+        const int T = (shared ? J.kin_s : J.kin_r) / 64;
+        const float* xin = shared ? dc_act : dc_act + sh_len + (size_t)j * J.kin_r;
+        float ga = 0.f;
+#pragma unroll
+        for (int q = 0; q < DC_TPJ; ++q) {
+            const int t = sub + q * LPR;
+            if (t < T) {
+                float xv[64];
+                const float4* xp = (const float4*)(xin + (size_t)t * 64);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float4 v = xp[i];
+                    xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+                }
+                float xs[2];
+                task_xsum<KIND>(xv, xs);
+                ga += task_dot<KIND>(wa[q], xv, xs, t);
+            }
+        }
+        for (int o = LPR >> 1; o > 0; o >>= 1) ga += __shfl_xor(ga, o, 64);
+        if (shared) acc = ga;
+        else acc += wk[j] * ga;
+#pragma unroll
+        for (int q = 0; q < DC_TPJ; ++q)
+#pragma unroll
+            for (int i = 0; i < DW; ++i) wa[q][i] = wb[q][i];
+    }
+    if (sub == 0 && row < rows) {
+        float* o = xres + (size_t)tok * rows + row;
+        *o = accumulate ? *o + acc : acc;
+    }
+}
+
+// lanes per row of the fused down kernel: the smallest job's task count
+// (capped at 64), raised until every job fits DC_TPJ tasks per lane
+static int down_lpr(int E, int SH, bool has_sh) {
+    const int Tmin = (has_sh && SH < E ? SH : E) / 64, Tmax = (has_sh && SH > E ? SH : E) / 64;
+    int LPR = 64;
+    while (LPR > 1 && LPR > Tmin) LPR >>= 1;
+    while (LPR < 64 && (Tmax + LPR - 1) / LPR > DC_TPJ) LPR <<= 1;
+    return LPR;
 }
 
 // out[t] = shared[t] + sum_k w[t,k] * y[slot(t,k)], k in order
@@ -497,14 +670,24 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
         D.wa = (const uint8_t*)downs; D.estride = (size_t)d * rowb_E; D.sa = (const uint8_t*)sh_d;
         D.rows_r = d; D.rows_s = d; D.kin_r = E; D.kin_s = SH; D.rowb_r = rowb_E; D.rowb_s = rowb_SH;
-        D.out_r = yr; D.out_s = sh_y; D.in_s = sh_act;
-        const int rpb = rows_per_block(E) < rows_per_block(SH) ? rows_per_block(E) : rows_per_block(SH);
-        dim3 g2(cdiv(d, rpb), S + D.N);
-        hipLaunchKernelGGL((k_moe_gemv<KIND, false>), g2, dim3(256), 0, stream(), D);
-        GH_LAUNCHED("k_moe_gemv(down)");
-        hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, nullptr,
-                           w_route, out, N, K, d);
-        GH_LAUNCHED("k_moe_combine");
+        D.in_s = sh_act;
+        // down projections + ordered combine in one launch
+        const int LPR = down_lpr(E, SH, has_sh);
+        const int rpb = 4 * (64 / LPR);
+        const size_t lds = ((has_sh ? (size_t)SH : 0) + (size_t)K * E) * 4;
+        if (lds > 60 * 1024) {  // activations do not fit LDS: per-expert outputs + ordered combine
+            D.out_r = yr; D.out_s = sh_y;
+            const int rpb2 = rows_per_block(E) < rows_per_block(SH) ? rows_per_block(E) : rows_per_block(SH);
+            hipLaunchKernelGGL((k_moe_gemv<KIND, false>), dim3(cdiv(d, rpb2), S + D.N), dim3(256), 0, stream(), D);
+            GH_LAUNCHED("k_moe_gemv(down)");
+            hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, nullptr,
+                               w_route, out, N, K, d);
+            GH_LAUNCHED("k_moe_combine");
+            return GH_OK;
+        }
+        hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w_route,
+                           out, LPR, 0);
+        GH_LAUNCHED("k_moe_down_combine");
         return GH_OK;
     }
     // prefill: permutation, grouped gate/up GEMM, grouped down GEMM, combine
@@ -553,9 +736,77 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
     return GH_OK;
 }
 
+// Decode MoE FFN of N <= 8 tokens as three launches, fused with the block
+// around it: xres += MoE(rmsnorm(xres) * nw). (1) norm + route, (2) grouped
+// gate/up GEMV with SwiGLU, (3) grouped down GEMV + combine + residual.
+template <int KIND>
+static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const float* rw, const float* bias,
+                                 const void* gates, const void* ups, const void* downs, const void* sh_g,
+                                 const void* sh_u, const void* sh_d, int N, int d, int E, int ne, int K, int SH) {
+    const int S = N * K;
+    const bool has_sh = sh_g && sh_u && sh_d;
+    const size_t rowb_d = KIND == 4 ? (size_t)d * 2 : row_bytes(KIND, d);
+    const size_t rowb_E = KIND == 4 ? (size_t)E * 2 : row_bytes(KIND, E);
+    const size_t rowb_SH = KIND == 4 ? (size_t)SH * 2 : row_bytes(KIND, SH);
+    char* r = (char*)workspace(WS_MOE_ROUTE, (size_t)S * 8);
+    float* xn = (float*)workspace(WS_MOE_XG, (size_t)N * d * 4);
+    float* act = (float*)workspace(WS_MOE_ACT, (size_t)S * E * 4);
+    float* sh_act = (float*)workspace(WS_MOE_SHARED, (size_t)N * ((size_t)SH + d) * 4);
+    if (!r || !xn || !act || !sh_act) return fail(GH_ENOMEM, "moe: workspace");
+    int32_t* idx = (int32_t*)r;
+    float* w = (float*)(r + (size_t)S * 4);
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne), stream(), xres, rw, bias, nullptr, idx, w, d,
+                       ne, K, nw, eps, xn, route_window(d, ne));
+    GH_LAUNCHED("k_route(norm)");
+    GemvJobs J{};
+    J.x = xn; J.idx = idx; J.S = S; J.N = has_sh ? N : 0; J.K = K; J.d = d;
+    J.wa = (const uint8_t*)gates; J.wb = (const uint8_t*)ups; J.estride = (size_t)E * rowb_d;
+    J.sa = (const uint8_t*)sh_g; J.sb = (const uint8_t*)sh_u;
+    J.rows_r = E; J.rows_s = SH; J.kin_r = d; J.kin_s = d; J.rowb_r = rowb_d; J.rowb_s = rowb_d;
+    J.out_r = act; J.out_s = sh_act;
+    auto rows_per_block = [&](int kin) {
+        int T = kin / 64, LPR = 64;
+        while (LPR > 1 && LPR > T) LPR >>= 1;
+        return 4 * (64 / LPR);
+    };
+    const int maxrows = has_sh ? (E > SH ? E : SH) : E;
+    hipLaunchKernelGGL((k_moe_gemv<KIND, true>), dim3(cdiv(maxrows, rows_per_block(d)), S + J.N), dim3(256), 0,
+                       stream(), J);
+    GH_LAUNCHED("k_moe_gemv(gate/up)");
+    GemvJobs D{};
+    D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
+    D.wa = (const uint8_t*)downs; D.estride = (size_t)d * rowb_E; D.sa = (const uint8_t*)sh_d;
+    D.rows_r = d; D.rows_s = d; D.kin_r = E; D.kin_s = SH; D.rowb_r = rowb_E; D.rowb_s = rowb_SH;
+    D.in_s = sh_act;
+    const int LPR = down_lpr(E, SH, has_sh);
+    const int rpb = 4 * (64 / LPR);
+    const size_t lds = ((has_sh ? (size_t)SH : 0) + (size_t)K * E) * 4;
+    hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w, xres, LPR,
+                       1);
+    GH_LAUNCHED("k_moe_down_combine");
+    return GH_OK;
+}
+
+int moe_decode_fused(float* xres, const float* nw, float eps, const float* rw, const float* bias, const void* gates,
+                     const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, int N,
+                     int d, int E, int ne, int K, int SH, int qkind) {
+    GH_REQUIRE(N >= 1 && N <= 8 && K >= 1 && K <= 8 && ne > 0 && ne <= 64, "moe decode: bad arguments");
+    const int bv = qkind == 3 ? 256 : 64;
+    GH_REQUIRE(d % bv == 0 && E % bv == 0 && SH % bv == 0, "moe decode: dims must be multiples of %d", bv);
+    GH_REQUIRE((size_t)K * E + SH <= 15 * 1024, "moe decode: K*E + SH = %d activations exceed LDS", K * E + SH);
+    switch (qkind) {
+        case -1: return moe_decode_fused_kind<4>(xres, nw, eps, rw, bias, gates, ups, downs, sh_g, sh_u, sh_d, N, d, E, ne, K, SH);
+        case 0: return moe_decode_fused_kind<0>(xres, nw, eps, rw, bias, gates, ups, downs, sh_g, sh_u, sh_d, N, d, E, ne, K, SH);
+        case 1: return moe_decode_fused_kind<1>(xres, nw, eps, rw, bias, gates, ups, downs, sh_g, sh_u, sh_d, N, d, E, ne, K, SH);
+        case 2: return moe_decode_fused_kind<2>(xres, nw, eps, rw, bias, gates, ups, downs, sh_g, sh_u, sh_d, N, d, E, ne, K, SH);
+        default: return moe_decode_fused_kind<3>(xres, nw, eps, rw, bias, gates, ups, downs, sh_g, sh_u, sh_d, N, d, E, ne, K, SH);
+    }
+}
+
 int moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int N, int d,
               int ne, int K) {
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), (size_t)d * 4, stream(), x, rw, bias, probs, idx, w, d, ne, K);
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne), stream(), x, rw, bias, probs, idx, w, d, ne,
+                       K, nullptr, 0.f, nullptr, route_window(d, ne));
     GH_LAUNCHED("k_route");
     return GH_OK;
 }
