@@ -16,6 +16,8 @@
 // wave 32 queries; per 64-key tile S^T = K Q^T (v_mfma_f32_32x32x16_f16),
 // online softmax in registers, O += P V with P taken straight from the S^T
 // accumulator layout (no LDS round trip) and V staged transposed in LDS.
+#include <stdlib.h>
+
 #include "gh_common.h"
 
 namespace gh {
@@ -325,6 +327,7 @@ static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
 
 // ============================================================== prefill
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t gh_u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -474,6 +477,218 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mfma(const float* __restri
     }
 }
 
+// ---- fp16 K / V^T staging for the prefill: K16 [B][KV][Tp][HD] and
+// Vt16 [B][KV][HD][Tp] (Tp = T rounded up to 64, zero-filled), written once
+// so every (query tile, head) block copies its key tiles with 16-byte loads.
+template <int HD>
+__global__ void __launch_bounds__(256) k_kv_f16(const float* __restrict__ k, const float* __restrict__ v,
+                                                _Float16* __restrict__ K16, _Float16* __restrict__ Vt16, int T,
+                                                int KV, int Tp) {
+    __shared__ float sv[PF_BK][HD + 1];
+    const int t0 = blockIdx.x * PF_BK, kvh = blockIdx.y, b = blockIdx.z;
+    const size_t kvs = (size_t)T * KV * HD;
+    _Float16* kd = K16 + (((size_t)b * KV + kvh) * Tp + t0) * HD;
+    for (int e = threadIdx.x; e < PF_BK * HD / 4; e += 256) {
+        const int r = e / (HD / 4), c4 = (e % (HD / 4)) * 4;
+        const int key = t0 + r;
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+        if (key < T) {
+            kv = *(const float4*)(k + b * kvs + ((size_t)key * KV + kvh) * HD + c4);
+            vv = *(const float4*)(v + b * kvs + ((size_t)key * KV + kvh) * HD + c4);
+        }
+        f16x4 h4;
+        h4[0] = (_Float16)kv.x; h4[1] = (_Float16)kv.y; h4[2] = (_Float16)kv.z; h4[3] = (_Float16)kv.w;
+        *(f16x4*)(kd + (size_t)r * HD + c4) = h4;
+        sv[r][c4] = vv.x; sv[r][c4 + 1] = vv.y; sv[r][c4 + 2] = vv.z; sv[r][c4 + 3] = vv.w;
+    }
+    __syncthreads();
+    _Float16* vd = Vt16 + ((size_t)b * KV + kvh) * HD * Tp + t0;
+    for (int e = threadIdx.x; e < HD * (PF_BK / 8); e += 256) {
+        const int c = e / (PF_BK / 8), r8 = (e % (PF_BK / 8)) * 8;
+        f16x8 h8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h8[i] = (_Float16)sv[r8 + i][c];
+        *(f16x8*)(vd + (size_t)c * Tp + r8) = h8;
+    }
+}
+
+// Causal flash attention over the fp16 K / V^T tiles. Block = 128 queries
+// (4 waves x 32) of one head; key tiles of 64 are double-buffered in LDS:
+// the next tile's 16-byte pieces are loaded into registers while the
+// current tile is multiplied. MFMA layout as k_attn_prefill_mfma. Softmax
+// in the log2 domain (scores pre-multiplied by scale*log2(e), one v_exp_f32
+// per score); masks only on the tiles that cross the diagonal or the
+// window; the running output is rescaled only when a row maximum moved.
+template <int HD>
+__global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __restrict__ q, const _Float16* __restrict__ K16,
+                                                          const _Float16* __restrict__ Vt16, float* __restrict__ out,
+                                                          int T, int Tp, int H, int KV, float scale, int window) {
+    constexpr int KS = HD + 8;
+    constexpr int VS = PF_BK + 8;
+    constexpr int KPT = PF_BK * HD / 8 / 256;  // 16-byte pieces per thread (K), same for V^T
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][PF_BK * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * VS];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int nqt = cdiv(T, PF_BQ);
+    const int qt = nqt - 1 - (int)blockIdx.x;  // heavy (late) tiles first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int G = H / KV, kvh = h / G;
+    const int q0 = qt * PF_BQ + wave * 32;
+    const size_t qs = (size_t)T * H * HD;
+    const float* qb = q + b * qs;
+    const _Float16* kbase = K16 + ((size_t)b * KV + kvh) * Tp * HD;
+    const _Float16* vbase = Vt16 + ((size_t)b * KV + kvh) * HD * Tp;
+
+    const int kend = min(T, qt * PF_BQ + PF_BQ);
+    int kbeg = 0;
+    if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
+    // per-thread piece coordinates (fixed): K row kr, dims kc; V^T dim vc, keys vr
+    int kr[KPT], kc[KPT], vc[KPT], vr[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+        const int e = tid + 256 * i;
+        kr[i] = e / (HD / 8); kc[i] = (e % (HD / 8)) * 8;
+        vc[i] = e / (PF_BK / 8); vr[i] = (e % (PF_BK / 8)) * 8;
+    }
+    gh_u32x4 pk[KPT], pv[KPT];  // (ext-vector: an array of uint4 structs stays in scratch)
+    if (kbeg < kend) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kbeg + kr[i]) * HD + kc[i]);
+            pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kbeg + vr[i]);
+        }
+    }
+
+    const int qj = q0 + (lane & 31), hf = lane >> 5;
+    f16x8 qreg[HD / 16];
+#pragma unroll
+    for (int s = 0; s < HD / 16; ++s) {
+        if (qj < T) {
+            const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
+            const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
+            qreg[s][0] = (_Float16)a0.x; qreg[s][1] = (_Float16)a0.y; qreg[s][2] = (_Float16)a0.z; qreg[s][3] = (_Float16)a0.w;
+            qreg[s][4] = (_Float16)a1.x; qreg[s][5] = (_Float16)a1.y; qreg[s][6] = (_Float16)a1.z; qreg[s][7] = (_Float16)a1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
+        }
+    }
+    f32x16 oacc[HD / 32];
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+    const float sl2 = scale * 1.4426950408889634f;  // scores in log2 units
+    float m_run = -INFINITY, l_run = 0.f;
+
+    int buf = 0;
+    for (int k0 = kbeg; k0 < kend; k0 += PF_BK, buf ^= 1) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            *(gh_u32x4*)(sK[buf] + kr[i] * KS + kc[i]) = pk[i];
+            *(gh_u32x4*)(sVt[buf] + vc[i] * VS + vr[i]) = pv[i];
+        }
+        __syncthreads();
+        if (k0 + PF_BK < kend) {
+            const int kn = k0 + PF_BK;
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kn + kr[i]) * HD + kc[i]);
+                pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kn + vr[i]);
+            }
+        }
+        if (k0 > q0 + 31) continue;  // whole tile in this wave's future (uniform per wave)
+        const _Float16* cK = sK[buf];
+        const _Float16* cV = sVt[buf];
+        f32x16 st[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
+#pragma unroll
+            for (int s = 0; s < HD / 16; ++s) {
+                const f16x8 ka = *(const f16x8*)(cK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
+                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[s], st[t], 0, 0, 0);
+            }
+        }
+        // masks only where the tile crosses the diagonal, the sequence end or the window
+        const bool edge = (k0 + PF_BK > q0) || (k0 + PF_BK > T) || (window > 0 && k0 <= q0 + 31 - window + 1);
+        float tmax = -INFINITY;
+        if (edge) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
+                    const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
+                    const float sv = vis ? st[t][e] * sl2 : -INFINITY;
+                    st[t][e] = sv;
+                    tmax = fmaxf(tmax, sv);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float sv = st[t][e] * sl2;
+                    st[t][e] = sv;
+                    tmax = fmaxf(tmax, sv);
+                }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float msub = (m_new == -INFINITY) ? 0.f : m_new;  // fully masked row: exp2(-inf) = 0
+        const float alpha = __builtin_amdgcn_exp2f(m_run - msub);
+        float psum = 0.f;
+        f16x8 pa[4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = __builtin_amdgcn_exp2f(st[t][e] - msub);
+                psum += p;
+                pa[2 * t + (e >> 3)][e & 7] = (_Float16)p;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * alpha + psum;
+        const bool moved = m_new != m_run;
+        m_run = m_new;
+        if (__ballot(moved)) {  // some row maximum moved: rescale (alpha = 1 for the others)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * hf + (e & 3), 64);
+#pragma unroll
+                for (int c = 0; c < HD / 32; ++c) oacc[c][e] *= ar;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kb = 32 * (u >> 1) + 16 * (u & 1) + 4 * hf;
+#pragma unroll
+            for (int c = 0; c < HD / 32; ++c) {
+                const _Float16* vrow = cV + (32 * c + (lane & 31)) * VS;
+                f16x8 vb8;
+                const f16x4 lo = *(const f16x4*)(vrow + kb), hi = *(const f16x4*)(vrow + kb + 8);
+                vb8[0] = lo[0]; vb8[1] = lo[1]; vb8[2] = lo[2]; vb8[3] = lo[3];
+                vb8[4] = hi[0]; vb8[5] = hi[1]; vb8[6] = hi[2]; vb8[7] = hi[3];
+                oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
+            }
+        }
+    }
+    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int r = 8 * (e >> 2) + 4 * hf + (e & 3);
+        const float inv = __shfl(linv, r, 64);
+        const int qi = q0 + r;
+        if (qi >= T) continue;
+        float* dst = out + b * qs + ((size_t)qi * H + h) * HD;
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) dst[32 * c + (lane & 31)] = oacc[c][e] * inv;
+    }
+}
+
 // Any head_dim (<= 256, multiple of 4): one wave per (query, head), online
 // softmax over keys, fp32 throughout. Used for shapes the MFMA kernel does
 // not cover.
@@ -536,6 +751,25 @@ int attn_decode_partials_devctl(const float* q, const uint16_t* kc, const uint16
 
 int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,
                       float scale, int window) {
+    if ((hd == 64 || hd == 128) && !getenv("GH_ATTN_PF_OLD")) {
+        const int Tp = cdiv(T, PF_BK) * PF_BK;
+        _Float16* kv16 = (_Float16*)workspace(WS_ATTN_KV16, (size_t)B * KV * Tp * hd * 2 * 2);
+        if (!kv16) return fail(GH_ENOMEM, "attention prefill: workspace");
+        _Float16* K16 = kv16;
+        _Float16* Vt16 = kv16 + (size_t)B * KV * Tp * hd;
+        const dim3 gs(Tp / PF_BK, KV, B), grid(cdiv(T, PF_BQ), H, B);
+        if (hd == 64) {
+            hipLaunchKernelGGL(k_kv_f16<64>, gs, dim3(256), 0, stream(), k, v, K16, Vt16, T, KV, Tp);
+            hipLaunchKernelGGL(k_attn_prefill_f16<64>, grid, dim3(256), 0, stream(), q, K16, Vt16, out, T, Tp, H, KV,
+                               scale, window);
+        } else {
+            hipLaunchKernelGGL(k_kv_f16<128>, gs, dim3(256), 0, stream(), k, v, K16, Vt16, T, KV, Tp);
+            hipLaunchKernelGGL(k_attn_prefill_f16<128>, grid, dim3(256), 0, stream(), q, K16, Vt16, out, T, Tp, H, KV,
+                               scale, window);
+        }
+        GH_LAUNCHED("k_attn_prefill_f16");
+        return GH_OK;
+    }
     if (hd == 64 || hd == 128) {
         const dim3 grid(cdiv(T, PF_BQ), H, B);
         if (hd == 64) hipLaunchKernelGGL(k_attn_prefill_mfma<64>, grid, dim3(256), 0, stream(), q, k, v, out, T, H, KV, scale, window);

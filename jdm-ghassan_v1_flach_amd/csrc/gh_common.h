@@ -157,6 +157,7 @@ enum WsSlot {
     WS_MAMBA_CHUNK = 11,
     WS_MAMBA_XF = 12,
     WS_GEMM_X = 13,
+    WS_ATTN_KV16 = 14,  // prefill: K and V^T as fp16, per kv head
     WS_QUANT0 = 16,     // 16 quant_materialize slots: 16..31
     WS_MOE_XG = 32,     // gathered rows for the grouped prefill GEMM
     WS_MOE_H = 33,
