@@ -12,6 +12,10 @@
 // step every thread converts 32 activations (fp32 -> fp16) and dequantises
 // 32 weights of one row (its half of a 64-value task) into LDS; the next
 // K step's global loads are issued before the MFMAs of the current one.
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "gemm_tile.h"
 
 namespace gh {
@@ -113,10 +117,215 @@ __global__ void __launch_bounds__(256) k_gemm_q(const float* __restrict__ X, con
         }
 }
 
+// ---------------------------------------------------------------- v2
+// Activations converted to fp16 ONCE (k_to_f16) instead of once per N tile;
+// the A tile then moves with 16-byte copies. LDS is double-buffered (one
+// barrier per K step): the next step's activation pieces and weight bytes
+// are requested right after the barrier and land in registers while the
+// MFMAs of the current step run. Weight decode for Q4_K / Q8_0 builds fp16
+// integer codes with one v_and_or_b32 per pair (code | 0x6400 = 1024 + q)
+// and scales them with one v_fma_mix_f32 each.
+__global__ void k_to_f16(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n4) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+        const float4 v = ((const float4*)x)[i];
+        f16x4v h;
+        h[0] = (_Float16)v.x; h[1] = (_Float16)v.y; h[2] = (_Float16)v.z; h[3] = (_Float16)v.w;
+        ((f16x4v*)y)[i] = h;
+    }
+}
+
+__device__ __forceinline__ uint32_t gq_and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float gq_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF)); }
+__device__ __forceinline__ float gq_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
+
+// 32 weights of a row-task half as fp16 into dst (LDS)
+template <int KIND>
+__device__ __forceinline__ void decode16(const WLoad<KIND>& wl, uint16_t* dst, uint32_t magic) {
+    float v[32];
+    if constexpr (KIND == 3) {
+        const uint32_t sc4[3] = {wl.hd.y, wl.hd.z, wl.hd.w};
+        auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+        const int s = 2 * wl.p + wl.h;
+        int scv, mv;
+        if (s < 4) {
+            scv = scb(s) & 63;
+            mv = scb(s + 4) & 63;
+        } else {
+            scv = (scb(s + 4) & 0xF) | ((scb(s - 4) >> 6) << 4);
+            mv = (scb(s + 4) >> 4) | ((scb(s) >> 6) << 4);
+        }
+        const float d1 = f16_to_f32((uint16_t)(wl.hd.x & 0xFFFF)) * (float)scv;
+        const float m1 = f16_to_f32((uint16_t)(wl.hd.x >> 16)) * (float)mv;
+        const float nb = -fmaf(1024.f, d1, m1);  // (1024 + q) * d1 + nb = q * d1 - m1
+        const uint32_t q[8] = {wl.a.x, wl.a.y, wl.a.z, wl.a.w, wl.b.x, wl.b.y, wl.b.z, wl.b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w = q[i] >> (4 * wl.h);
+            const uint32_t c0 = gq_and_or(w, 0x000F000Fu, magic);       // values 4i, 4i+2
+            const uint32_t c1 = gq_and_or(w >> 8, 0x000F000Fu, magic);  // values 4i+1, 4i+3
+            v[4 * i] = fmaf(gq_lo(c0), d1, nb);
+            v[4 * i + 1] = fmaf(gq_lo(c1), d1, nb);
+            v[4 * i + 2] = fmaf(gq_hi(c0), d1, nb);
+            v[4 * i + 3] = fmaf(gq_hi(c1), d1, nb);
+        }
+    } else if constexpr (KIND == 2) {
+        // block bytes: d at shift+0..1, quants at shift+2..33 (shift 0 or 2)
+        const int sh = wl.shift;
+        const uint32_t dbits = (sh == 0) ? (wl.w[0] & 0xFFFF) : (wl.w[0] >> 16);
+        const float d = f16_to_f32((uint16_t)dbits);
+        const float nb = -1152.f * d;  // (1152 + q) * d + nb = q * d
+        // quant j = stream byte sh + 2 + j; with sh == 2 quants start at dword 1
+        const int w0 = sh == 0 ? 0 : 1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // 4 quants 4i..4i+3 from the (possibly 2-byte shifted) stream
+            const uint32_t lo = wl.w[w0 + i], hi = wl.w[w0 + i + 1];
+            const uint32_t u = (sh == 0 ? __builtin_amdgcn_alignbyte(hi, lo, 2) : lo) ^ 0x80808080u;
+            const uint32_t c0 = gq_and_or(u, 0x00FF00FFu, magic);
+            const uint32_t c1 = gq_and_or(u >> 8, 0x00FF00FFu, magic);
+            v[4 * i] = fmaf(gq_lo(c0), d, nb);
+            v[4 * i + 1] = fmaf(gq_lo(c1), d, nb);
+            v[4 * i + 2] = fmaf(gq_hi(c0), d, nb);
+            v[4 * i + 3] = fmaf(gq_hi(c1), d, nb);
+        }
+    } else {
+        wl.decode(v);
+    }
+    store_f16x32(dst, v);
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
+                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDS_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tilesN = cdiv(N, BN), tilesM = cdiv(M, BM);
+    const int nblk = tilesN * tilesM;
+    int bid = blockIdx.x;
+    if (nblk % 8 == 0) bid = (bid % 8) * (nblk / 8) + bid / 8;  // XCD-aware: an XCD keeps a run of N tiles
+    const int tm = bid % tilesM, tn = bid / tilesM;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // A pieces: thread -> rows ar + 32i (i < 4), 8 halves at ac
+    const int ar = tid >> 3, ac = (tid & 7) * 8;
+    // B: thread -> (row lr = tid/2, half lh = tid%2)
+    const int lr = tid >> 1, lh = tid & 1;
+    const int bn = n0 + lr;
+    const uint8_t* wrow = W + (size_t)(bn < N ? bn : N - 1) * rowb;
+    const uint16_t* xrows[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int am = m0 + ar + 32 * i;
+        xrows[i] = X16 + (size_t)(am < M ? am : M - 1) * K;
+    }
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int T = K / BK;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+
+    gh_u32x4v xa[4];
+    WLoad<KIND> wl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + ac);
+    wl.load(wrow, 0, lh);
+    int buf = 0;
+    for (int t = 0; t < T; ++t, buf ^= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gh_u32x4v v = xa[i];
+            if (m0 + ar + 32 * i >= M) v = gh_u32x4v{0u, 0u, 0u, 0u};
+            *(gh_u32x4v*)(sA[buf] + (ar + 32 * i) * LDS_STRIDE + ac) = v;
+        }
+        {
+            uint16_t* dst = sB[buf] + lr * LDS_STRIDE + lh * 32;
+            if (bn < N) {
+                decode16<KIND>(wl, dst, magic);
+            } else {
+                float z[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) z[i] = 0.f;
+                store_f16x32(dst, z);
+            }
+        }
+        __syncthreads();
+        if (t + 1 < T) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + (size_t)(t + 1) * BK + ac);
+            wl.load(wrow, t + 1, lh);
+        }
+        const uint16_t* cA = sA[buf];
+        const uint16_t* cB = sB[buf];
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int kofs = ks * 16 + (lane >> 5) * 8;
+            f16x8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = *(const f16x8*)(cA + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+                b[i] = *(const f16x8*)(cB + (wn + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn + j * 32 + (lane & 31);
+            if (col >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row < M) Y[(size_t)row * N + col] = acc[i][j][e];
+            }
+        }
+}
+
+template <int KIND>
+static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {
+    uint16_t* x16 = (uint16_t*)workspace(WS_GEMM_X, (size_t)M * K * 2);
+    if (!x16) return fail(GH_ENOMEM, "gemm: workspace");
+    const int64_t n4 = (int64_t)M * K / 4;
+    hipLaunchKernelGGL(k_to_f16, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 8192)), dim3(256), 0, stream(), x,
+                       x16, n4);
+    const int blocks = cdiv(M, BM) * cdiv(N, BN);
+    hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, (const uint8_t*)w, y, M, K, N,
+                       rowb);
+    GH_LAUNCHED("k_gemm_q2");
+    return GH_OK;
+}
+
 int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
     const int blocks = cdiv(M, BM) * cdiv(N, BN);
     size_t rowb = kind == 4 ? (size_t)K * 2 : kind == 5 ? (size_t)K * 4 : row_bytes(kind, K);
     const dim3 g(blocks), b(256);
+    static const int v2 = [] {
+        const char* e = getenv("GH_GEMM_V2");
+        return e ? atoi(e) : 1;
+    }();
+    if (v2 && (kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
+        switch (kind) {
+            case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb);
+            case 3: return gemm2_launch<3>(x, w, y, M, K, N, rowb);
+            default: return gemm2_launch<4>(x, w, y, M, K, N, rowb);
+        }
+    }
     switch (kind) {
         case 0: hipLaunchKernelGGL(k_gemm_q<0>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
         case 1: hipLaunchKernelGGL(k_gemm_q<1>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;

@@ -8,6 +8,10 @@ namespace gh {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t gh_u32x4v __attribute__((ext_vector_type(4)));
+
+inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 constexpr int BM = 128, BN = 128, BK = 64, LDS_STRIDE = BK + 8;  // in fp16 elements
 
