@@ -137,7 +137,7 @@ def kernel_suite(gh):
             if M <= 8:
                 res[tag] = entry("k_gemv_mfma", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
-                res[tag] = entry("k_gemm_q", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
+                res[tag] = entry("k_to_f16+k_gemm_q2", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
                                  bound="mfma")
             del dw, dx, y
     # ---------------- c3: SSD scan T=4096 + decode state update
@@ -210,7 +210,7 @@ def kernel_suite(gh):
     of = gh.Buf.zeros(Tp * Hq * hd, np.float32)
     ms = time_launches(gh, lambda: gh.call("gh_attention_forward_ex", qf.p, kf.p, vf.p, of.p, None, 1, Tp, Hq, KVh, hd,
                                            gh.fl(0.0884), 0, None), 10)
-    res["c4_prefill_T4096"] = entry("k_attn_prefill_mfma", ms, flops=4.0 * Hq * hd * Tp * (Tp + 1) / 2, bound="mfma")
+    res["c4_prefill_T4096"] = entry("k_kv_f16+k_attn_prefill_f16", ms, flops=4.0 * Hq * hd * Tp * (Tp + 1) / 2, bound="mfma")
     del qf, kf, vf, of
     # ---------------- c5: MoE FFN decode / prefill, skewed routing
     d5, E5, ne5, K5, SH5 = 1536, 512, 64, 6, 1024

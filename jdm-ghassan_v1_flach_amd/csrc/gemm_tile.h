@@ -166,4 +166,75 @@ __device__ __forceinline__ void store_f16x32(uint16_t* dst, const float* v) {
 }
 
 
+// ---- fp16 weight decode of the MFMA GEMMs (32 values of a row-task half
+// into LDS): fp16 integer codes by one v_and_or_b32 per pair (code | 0x6400
+// is the fp16 number 1024 + code), scaled by one v_fma_mix_f32 each.
+__device__ __forceinline__ uint32_t gq_and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm volatile("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float gq_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF)); }
+__device__ __forceinline__ float gq_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
+
+// 32 weights of a row-task half as fp16 into dst (LDS)
+template <int KIND>
+__device__ __forceinline__ void decode16(const WLoad<KIND>& wl, uint16_t* dst, uint32_t magic) {
+    float v[32];
+    if constexpr (KIND == 3) {
+        const uint32_t sc4[3] = {wl.hd.y, wl.hd.z, wl.hd.w};
+        auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+        const int s = 2 * wl.p + wl.h;
+        int scv, mv;
+        if (s < 4) {
+            scv = scb(s) & 63;
+            mv = scb(s + 4) & 63;
+        } else {
+            scv = (scb(s + 4) & 0xF) | ((scb(s - 4) >> 6) << 4);
+            mv = (scb(s + 4) >> 4) | ((scb(s) >> 6) << 4);
+        }
+        const float d1 = f16_to_f32((uint16_t)(wl.hd.x & 0xFFFF)) * (float)scv;
+        const float m1 = f16_to_f32((uint16_t)(wl.hd.x >> 16)) * (float)mv;
+        const float nb = -fmaf(1024.f, d1, m1);  // (1024 + q) * d1 + nb = q * d1 - m1
+        const uint32_t q[8] = {wl.a.x, wl.a.y, wl.a.z, wl.a.w, wl.b.x, wl.b.y, wl.b.z, wl.b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w = q[i] >> (4 * wl.h);
+            const uint32_t c0 = gq_and_or(w, 0x000F000Fu, magic);       // values 4i, 4i+2
+            const uint32_t c1 = gq_and_or(w >> 8, 0x000F000Fu, magic);  // values 4i+1, 4i+3
+            v[4 * i] = fmaf(gq_lo(c0), d1, nb);
+            v[4 * i + 1] = fmaf(gq_lo(c1), d1, nb);
+            v[4 * i + 2] = fmaf(gq_hi(c0), d1, nb);
+            v[4 * i + 3] = fmaf(gq_hi(c1), d1, nb);
+        }
+    } else if constexpr (KIND == 2) {
+        // block bytes: d at shift+0..1, quants at shift+2..33 (shift 0 or 2)
+        const int sh = wl.shift;
+        const uint32_t dbits = (sh == 0) ? (wl.w[0] & 0xFFFF) : (wl.w[0] >> 16);
+        const float d = f16_to_f32((uint16_t)dbits);
+        const float nb = -1152.f * d;  // (1152 + q) * d + nb = q * d
+        // quant j = stream byte sh + 2 + j; with sh == 2 quants start at dword 1
+        const int w0 = sh == 0 ? 0 : 1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // 4 quants 4i..4i+3 from the (possibly 2-byte shifted) stream
+            const uint32_t lo = wl.w[w0 + i], hi = wl.w[w0 + i + 1];
+            const uint32_t u = (sh == 0 ? __builtin_amdgcn_alignbyte(hi, lo, 2) : lo) ^ 0x80808080u;
+            const uint32_t c0 = gq_and_or(u, 0x00FF00FFu, magic);
+            const uint32_t c1 = gq_and_or(u >> 8, 0x00FF00FFu, magic);
+            v[4 * i] = fmaf(gq_lo(c0), d, nb);
+            v[4 * i + 1] = fmaf(gq_lo(c1), d, nb);
+            v[4 * i + 2] = fmaf(gq_hi(c0), d, nb);
+            v[4 * i + 3] = fmaf(gq_hi(c1), d, nb);
+        }
+    } else {
+        wl.decode(v);
+    }
+    store_f16x32(dst, v);
+}
+
+
+// fp32 -> fp16 copy of n values (n a multiple of 4), on the backend stream
+int launch_to_f16(const float* x, uint16_t* y, int64_t n);
+
 }  // namespace gh

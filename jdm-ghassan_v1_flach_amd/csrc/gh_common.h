@@ -158,6 +158,7 @@ enum WsSlot {
     WS_MAMBA_XF = 12,
     WS_GEMM_X = 13,
     WS_ATTN_KV16 = 14,  // prefill: K and V^T as fp16, per kv head
+    WS_MOE_X16 = 15,    // prefill: fp16 copy of the MoE input rows
     WS_QUANT0 = 16,     // 16 quant_materialize slots: 16..31
     WS_MOE_XG = 32,     // gathered rows for the grouped prefill GEMM
     WS_MOE_H = 33,

@@ -179,14 +179,18 @@ __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, cons
     }
 }
 
-// window of router groups whose terms fit 60 KB of LDS next to the token
-static int route_window(int d, int ne) {
+// window of router groups whose terms fit 60 KB of LDS next to the token;
+// for many tokens (one block each) a 64-group window keeps blocks small
+static int route_window(int d, int ne, int N) {
     const int budget = 60 * 1024 / 4 - d;  // floats, leaving room for the static arrays
     int gw = budget / ne - 1;
+    if (N > 8 && gw > 64) gw = 64;
     if (gw > d / 4) gw = d / 4;
     return gw < 1 ? 1 : gw;
 }
-static size_t route_lds(int d, int ne) { return ((size_t)d + (size_t)ne * (route_window(d, ne) + 1)) * 4; }
+static size_t route_lds(int d, int ne, int N) {
+    return ((size_t)d + (size_t)ne * (route_window(d, ne, N) + 1)) * 4;
+}
 
 // ========================================================== permutation
 // Stable counting sort of slot ids s = t*K+k by expert, in three
@@ -506,6 +510,8 @@ struct GroupGemm {
     size_t gstride, rowb;
     int K, N;                  // K = input length, N = output rows per group
     float* out;                // [rows][N], row = grouped position
+    const uint16_t* A16;       // v2: fp16 activations (instead of A)
+    uint16_t* out16;           // v2 DUAL: fp16 SwiGLU output (instead of out)
 };
 
 template <int KIND, bool DUAL>
@@ -619,6 +625,129 @@ __global__ void __launch_bounds__(256) k_moe_group_gemm(GroupGemm P) {
     }
 }
 
+// v2 of the grouped GEMM (kinds 2, 3, 4): fp16 activations converted once
+// (gathered rows are read with 16-byte loads), double-buffered LDS with one
+// barrier per K step, and_or/fma_mix weight decode (gemm.hip), the DUAL
+// (gate/up) epilogue writes the SwiGLU output as fp16 for the down GEMM.
+template <int KIND, bool DUAL>
+__global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDS_STRIDE];
+    const int tile = blockIdx.x;
+    if (tile >= P.tiles[0]) return;
+    const int g = P.tiles[1 + 2 * tile], m0 = P.tiles[2 + 2 * tile];
+    const int mend = P.offsets[g + 1];
+    const int NT = DUAL ? 64 : BN;  // output columns per block
+    const int n0 = blockIdx.y * NT;
+    if (n0 >= P.N) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ar = tid >> 3, ac = (tid & 7) * 8;
+    const uint16_t* xrows[4];
+    bool aok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int am = m0 + ar + 32 * i;
+        aok[i] = am < mend;
+        int arow = aok[i] ? am : m0;
+        if (P.gather) arow = P.gather[arow] / P.topk;
+        xrows[i] = P.A16 + (size_t)arow * P.lda;
+    }
+    const int lr = tid >> 1, lh = tid & 1;
+    int brow;
+    const uint8_t* Wm;
+    if (DUAL) {
+        const int wn = lr >> 6, r = lr & 63;
+        brow = n0 + 32 * wn + (r & 31);
+        Wm = (r < 32 ? P.W0 : P.W1) + (size_t)g * P.gstride;
+    } else {
+        brow = n0 + lr;
+        Wm = P.W0 + (size_t)g * P.gstride;
+    }
+    const bool brow_ok = brow < P.N;
+    const uint8_t* wrow = Wm + (size_t)(brow_ok ? brow : 0) * P.rowb;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int T = P.K / BK;
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    gh_u32x4v xa[4];
+    WLoad<KIND> wl;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + ac);
+    wl.load(wrow, 0, lh);
+    int buf = 0;
+    for (int t = 0; t < T; ++t, buf ^= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            gh_u32x4v v = xa[i];
+            if (!aok[i]) v = gh_u32x4v{0u, 0u, 0u, 0u};
+            *(gh_u32x4v*)(sA[buf] + (ar + 32 * i) * LDS_STRIDE + ac) = v;
+        }
+        {
+            uint16_t* dst = sB[buf] + lr * LDS_STRIDE + lh * 32;
+            if (brow_ok) {
+                decode16<KIND>(wl, dst, magic);
+            } else {
+                float z[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) z[i] = 0.f;
+                store_f16x32(dst, z);
+            }
+        }
+        __syncthreads();
+        if (t + 1 < T) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + (size_t)(t + 1) * BK + ac);
+            wl.load(wrow, t + 1, lh);
+        }
+        const uint16_t* cA = sA[buf];
+        const uint16_t* cB = sB[buf];
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int kofs = ks * 16 + (lane >> 5) * 8;
+            f16x8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = *(const f16x8*)(cA + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+                b[i] = *(const f16x8*)(cB + (wn + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (row >= mend) continue;
+            if (DUAL) {
+                const int col = n0 + 32 * (wave & 1) + (lane & 31);
+                if (col < P.N) {
+                    const float gv = acc[i][0][e], uv = acc[i][1][e];
+                    P.out16[(size_t)row * P.N + col] = f32_to_f16(gv / (1.0f + expf(-gv)) * uv);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + j * 32 + (lane & 31);
+                    if (col < P.N) P.out[(size_t)row * P.N + col] = acc[i][j][e];
+                }
+            }
+        }
+    }
+}
+
 // tile table of one group covering rows [0, N)
 __global__ void k_single_group_tiles(int32_t* tiles, int32_t* offs, int N, int bm) {
     const int nt = (N + bm - 1) / bm;
@@ -700,6 +829,48 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
     const int max_tiles = S / BM + ne + 1;
     int rc = permute(idx, S, ne, grouped, offsets, pos, tiles, BM);
     if (rc) return rc;
+    if constexpr (KIND == 2 || KIND == 3 || KIND == 4) {
+        // v2: fp16 activations converted once; gate/up write fp16 SwiGLU rows
+        uint16_t* x16 = (uint16_t*)workspace(WS_MOE_X16, (size_t)N * d * 2);
+        if (!x16) return fail(GH_ENOMEM, "moe: workspace");
+        uint16_t* act16 = (uint16_t*)act;         // [S][E] fp16 in the fp32 buffer
+        uint16_t* sh_act16 = (uint16_t*)sh_act;   // [N][SH] fp16
+        rc = launch_to_f16(x, x16, (int64_t)N * d);
+        if (rc) return rc;
+        GroupGemm P{};
+        P.A16 = x16; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
+        P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
+        P.K = d; P.N = E; P.out16 = act16;
+        hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
+        GH_LAUNCHED("k_moe_group_gemm2(gate/up)");
+        GroupGemm Q{};
+        Q.A16 = act16; Q.lda = E; Q.gather = nullptr; Q.topk = 1; Q.tiles = tiles; Q.offsets = offsets;
+        Q.W0 = (const uint8_t*)downs; Q.gstride = (size_t)d * rowb_E; Q.rowb = rowb_E; Q.K = E; Q.N = d; Q.out = yr;
+        hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
+        GH_LAUNCHED("k_moe_group_gemm2(down)");
+        if (has_sh) {
+            int32_t* sh_tiles = (int32_t*)workspace(WS_MOE_H, ((size_t)2 * (N / BM + 2) + 1 + 2) * 4);
+            if (!sh_tiles) return fail(GH_ENOMEM, "moe: workspace");
+            int32_t* sh_off = sh_tiles + 2 * (N / BM + 2) + 1;
+            const int nt = cdiv(N, BM);
+            hipLaunchKernelGGL(k_single_group_tiles, dim3(1), dim3(64), 0, stream(), sh_tiles, sh_off, N, BM);
+            GH_LAUNCHED("k_single_group_tiles");
+            GroupGemm R{};
+            R.A16 = x16; R.lda = d; R.gather = nullptr; R.topk = 1; R.tiles = sh_tiles; R.offsets = sh_off;
+            R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.gstride = 0; R.rowb = rowb_d;
+            R.K = d; R.N = SH; R.out16 = sh_act16;
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
+            GroupGemm U{};
+            U.A16 = sh_act16; U.lda = SH; U.gather = nullptr; U.topk = 1; U.tiles = sh_tiles; U.offsets = sh_off;
+            U.W0 = (const uint8_t*)sh_d; U.gstride = 0; U.rowb = rowb_SH; U.K = SH; U.N = d; U.out = sh_y;
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
+            GH_LAUNCHED("k_moe_group_gemm2(shared)");
+        }
+        hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
+                           out, N, K, d);
+        GH_LAUNCHED("k_moe_combine");
+        return GH_OK;
+    }
     GroupGemm P{};
     P.A = x; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
     P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
@@ -755,8 +926,8 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     if (!r || !xn || !act || !sh_act) return fail(GH_ENOMEM, "moe: workspace");
     int32_t* idx = (int32_t*)r;
     float* w = (float*)(r + (size_t)S * 4);
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne), stream(), xres, rw, bias, nullptr, idx, w, d,
-                       ne, K, nw, eps, xn, route_window(d, ne));
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), xres, rw, bias, nullptr, idx, w, d,
+                       ne, K, nw, eps, xn, route_window(d, ne, N));
     GH_LAUNCHED("k_route(norm)");
     GemvJobs J{};
     J.x = xn; J.idx = idx; J.S = S; J.N = has_sh ? N : 0; J.K = K; J.d = d;
@@ -805,8 +976,8 @@ int moe_decode_fused(float* xres, const float* nw, float eps, const float* rw, c
 
 int moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int N, int d,
               int ne, int K) {
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne), stream(), x, rw, bias, probs, idx, w, d, ne,
-                       K, nullptr, 0.f, nullptr, route_window(d, ne));
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), x, rw, bias, probs, idx, w, d, ne,
+                       K, nullptr, 0.f, nullptr, route_window(d, ne, N));
     GH_LAUNCHED("k_route");
     return GH_OK;
 }
