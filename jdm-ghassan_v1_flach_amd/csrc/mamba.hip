@@ -19,6 +19,7 @@
 namespace gh {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
@@ -114,6 +115,31 @@ __global__ void __launch_bounds__(256) k_ssd_cb(const float* __restrict__ Bm, co
 
 // dS[c][h][p][n] = sum_tau e^(cum_end - cum_tau) dt_tau x_tau[p] B_tau[n]
 // (P = 64 rows, N cols in 32-wide MFMA tiles), fp16 operands, fp32 acc.
+// Stages a [64 rows][W] fp32 tile (row stride ld, rows >= nvalid read as
+// 0, optionally scaled per row by sw) into LDS as fp16 TRANSPOSED [W][S]:
+// thread = (column c, group of 64*W/256 consecutive rows); the global loads
+// coalesce across columns and each thread writes its rows as 16-byte pieces.
+template <int W, int S, bool SCALE>
+__device__ __forceinline__ void stage_t64(const float* __restrict__ src, int ld, int nvalid, const float* sw,
+                                          _Float16* dst) {
+    constexpr int G = 256 / W, R = 64 / G;
+    const int c = threadIdx.x % W, g = threadIdx.x / W;
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int r = g * R + i;
+        v[i] = r < nvalid ? src[(size_t)r * ld + c] : 0.f;
+        if (SCALE) v[i] *= sw[r];
+    }
+#pragma unroll
+    for (int j = 0; j < R / 8; ++j) {
+        f16x8 hv;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) hv[k] = (_Float16)v[8 * j + k];
+        *(f16x8*)(dst + c * S + g * R + 8 * j) = hv;
+    }
+}
+
 template <int N>
 __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict__ xs, int ldx,
                                                          const float* __restrict__ Bm, int ldb,
@@ -143,16 +169,8 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict
                                         : 0.f;
         }
         __syncthreads();
-        for (int e = threadIdx.x; e < TK * P; e += 256) {
-            const int tau = e / P, p = e % P;
-            const float v = (k0 + tau < len) ? xs[(size_t)(t0 + k0 + tau) * ldx + h * P + p] * sw[tau] : 0.f;
-            sX[p * S + tau] = (_Float16)v;
-        }
-        for (int e = threadIdx.x; e < TK * N; e += 256) {
-            const int tau = e / N, n = e % N;
-            const float v = (k0 + tau < len) ? Bm[(size_t)(t0 + k0 + tau) * ldb + n] : 0.f;
-            sB[n * S + tau] = (_Float16)v;
-        }
+        stage_t64<P, S, true>(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0, sw, sX);
+        stage_t64<N, S, false>(Bm + (size_t)(t0 + k0) * ldb, ldb, len - k0, nullptr, sB);
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ++ks) {
@@ -222,13 +240,20 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
     const int trow = tt + wt + (lane & 31);                  // A-operand row of this lane
     const bool trow_ok = trow < len;
     const float cum_t = trow_ok ? cum[(size_t)(t0 + trow) * H + h] : 0.f;
+    const float cum_t2 = cum_t * 1.4426950408889634f;
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 
     // ---- inter-chunk term: e^(cum_t) C_t S_in^T
     const float* Sc = Sin + ((size_t)c * H + h) * P * N;
-    for (int e = threadIdx.x; e < P * N; e += 256) sS[(e / N) * SN + (e % N)] = (_Float16)Sc[e];
+    for (int e = threadIdx.x; e < P * N / 4; e += 256) {
+        const float4 v = ((const float4*)Sc)[e];
+        const int r = (4 * e) / N, cc = (4 * e) % N;
+        f16x4 hv;
+        hv[0] = (_Float16)v.x; hv[1] = (_Float16)v.y; hv[2] = (_Float16)v.z; hv[3] = (_Float16)v.w;
+        *(f16x4*)(sS + r * SN + cc) = hv;
+    }
     __syncthreads();
     {
         const float sc = trow_ok ? expf(cum_t) : 0.f;
@@ -250,13 +275,10 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
         __syncthreads();
         if (threadIdx.x < TK) {
             const int tau = k0 + threadIdx.x;
-            scum[threadIdx.x] = tau < len ? cum[(size_t)(t0 + tau) * H + h] : 0.f;
+            scum[threadIdx.x] = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
             sdt[threadIdx.x] = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
         }
-        for (int e = threadIdx.x; e < TK * P; e += 256) {
-            const int tau = e / P, p = e % P;
-            sXt[p * S + tau] = (_Float16)((k0 + tau < len) ? xs[(size_t)(t0 + k0 + tau) * ldx + h * P + p] : 0.f);
-        }
+        stage_t64<P, S, false>(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0, nullptr, sXt);
         __syncthreads();
         if (k0 > tt + wt + 31) continue;  // wave-uniform: tile entirely in this wave's future
         const float* grow = G + ((size_t)c * L + (trow_ok ? trow : 0)) * L + k0;
@@ -270,7 +292,7 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
             for (int i = 0; i < 8; ++i) {
                 const int tau = k0 + ko + i;
                 const bool vis = trow_ok && tau <= trow && tau < len;
-                const float m = vis ? gv[i] * expf(cum_t - scum[ko + i]) * sdt[ko + i] : 0.f;
+                const float m = vis ? gv[i] * __builtin_amdgcn_exp2f(cum_t2 - scum[ko + i]) * sdt[ko + i] : 0.f;
                 a[i] = (_Float16)m;
             }
             const f16x8 b = *(const f16x8*)(sXt + (wp + (lane & 31)) * S + ko);
