@@ -162,5 +162,6 @@ enum WsSlot {
     WS_QUANT0 = 16,     // 16 quant_materialize slots: 16..31
     WS_MOE_XG = 32,     // gathered rows for the grouped prefill GEMM
     WS_MOE_H = 33,
+    WS_MOE_TERMS = 34,  // router group terms (large routers, few tokens)
 };
 }  // namespace gh

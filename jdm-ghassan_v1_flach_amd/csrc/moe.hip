@@ -26,6 +26,68 @@ namespace gh {
 // from the unbiased p renormalised (uniform if their sum <= 1e-8).
 // LDS: x [d] | terms [ne][gw + 1] for a window of gw groups (all groups
 // when they fit; the lane sums run on across windows, still in order).
+// Softmax + top-k of one token's logits sp[0..ne) (LDS, overwritten with
+// the exponentials), run by the 64 lanes of one wave (see k_route).
+__device__ void route_finish(float* sp, const float* __restrict__ bias, int ne, int K, int t,
+                             int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    float mx = sp[0];
+    if (lane == 0)
+        for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
+    mx = __shfl(mx, 0, 64);
+    const float ev = lane < ne ? (float)exp((double)(sp[lane] - mx)) : 0.f;
+    if (lane < ne) sp[lane] = ev;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float sum = 0.f;
+    if (lane == 0)
+        for (int e = 0; e < ne; ++e) sum += sp[e];
+    sum = __shfl(sum, 0, 64);
+    const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
+    const float p = ev * inv;
+    const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
+    // K rounds of argmax: larger value wins, equal values -> lower index
+    bool taken = false;
+    int sel_idx[8];
+    for (int k = 0; k < K; ++k) {
+        float bv = (!taken && lane < ne && sel > -1e30f) ? sel : -INFINITY;
+        int bi = (!taken && lane < ne && sel > -1e30f) ? lane : 64;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi >= 64) bi = 0;  // nothing selectable: the reference falls back to expert 0
+        sel_idx[k] = bi;
+        if (lane == bi) taken = true;
+    }
+    // weights from the unbiased probabilities, renormalised in order
+    float wv[8], sw = 0.f;
+    for (int k = 0; k < K; ++k) {
+        wv[k] = __shfl(p, sel_idx[k], 64);
+        sw += wv[k];
+    }
+    if (lane == 0) {
+        if (sw > 1e-8f) {
+            const float iw = 1.0f / sw;
+            for (int k = 0; k < K; ++k) wv[k] *= iw;
+        } else {
+            for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
+        }
+        for (int k = 0; k < K; ++k) {
+            idx[(size_t)t * K + k] = sel_idx[k];
+            wout[(size_t)t * K + k] = wv[k];
+        }
+    }
+    if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
+}
+
 constexpr int ROUTE_RB = 8;  // float4 weight loads per thread per batch
 // With `nw` set, the token is first RMS-normalised (elementwise.hip
 // k_rmsnorm arithmetic) and the normalised row is also written to xn.
@@ -120,63 +182,7 @@ __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, cons
     }
     if (tid < ne) sp[tid] = s;
     __syncthreads();
-    if (tid < 64) {
-        const int lane = tid;
-        float mx = sp[0];
-        if (lane == 0)
-            for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
-        mx = __shfl(mx, 0, 64);
-        const float ev = lane < ne ? (float)exp((double)(sp[lane] - mx)) : 0.f;
-        if (lane < ne) sp[lane] = ev;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float sum = 0.f;
-        if (lane == 0)
-            for (int e = 0; e < ne; ++e) sum += sp[e];
-        sum = __shfl(sum, 0, 64);
-        const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
-        const float p = ev * inv;
-        const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
-        // K rounds of argmax: larger value wins, equal values -> lower index
-        bool taken = false;
-        int sel_idx[8];
-        for (int k = 0; k < K; ++k) {
-            float bv = (!taken && lane < ne && sel > -1e30f) ? sel : -INFINITY;
-            int bi = (!taken && lane < ne && sel > -1e30f) ? lane : 64;
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if (bi >= 64) bi = 0;  // nothing selectable: the reference falls back to expert 0
-            sel_idx[k] = bi;
-            if (lane == bi) taken = true;
-        }
-        // weights from the unbiased probabilities, renormalised in order
-        float wv[8], sw = 0.f;
-        for (int k = 0; k < K; ++k) {
-            wv[k] = __shfl(p, sel_idx[k], 64);
-            sw += wv[k];
-        }
-        if (lane == 0) {
-            if (sw > 1e-8f) {
-                const float iw = 1.0f / sw;
-                for (int k = 0; k < K; ++k) wv[k] *= iw;
-            } else {
-                for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
-            }
-            for (int k = 0; k < K; ++k) {
-                idx[(size_t)t * K + k] = sel_idx[k];
-                wout[(size_t)t * K + k] = wv[k];
-            }
-        }
-        if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
-    }
+    if (tid < 64) route_finish(sp, bias, ne, K, t, idx, wout, probs);
 }
 
 // window of router groups whose terms fit 60 KB of LDS next to the token;
@@ -190,6 +196,125 @@ static int route_window(int d, int ne, int N) {
 }
 static size_t route_lds(int d, int ne, int N) {
     return ((size_t)d + (size_t)ne * (route_window(d, ne, N) + 1)) * 4;
+}
+
+// Router of a large expert set for few tokens, over many blocks: block
+// (x, t) computes the group terms of groups [64x, 64x+64) of token t for
+// every expert (same arithmetic as k_route) into terms [t][group][expert];
+// k_route_select then adds each expert's terms in group order and finishes.
+constexpr int RT_G = 64;
+__global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x, const float* __restrict__ rw,
+                                                     float* __restrict__ terms, int d, int ne,
+                                                     const float* __restrict__ nw, float eps,
+                                                     float* __restrict__ xn) {
+#pragma clang fp contract(off)
+    extern __shared__ float rt_sx[];  // [d]
+    __shared__ double dred[4];
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int ngroups = d / 4, g0 = blockIdx.x * RT_G, gw = min(RT_G, ngroups - g0);
+    const float4* xt = (const float4*)(x + (size_t)t * d);
+    const float4* rw4 = (const float4*)rw;
+    float4 wreg[ROUTE_RB];
+#pragma unroll
+    for (int b = 0; b < ROUTE_RB; ++b) {
+        const int q = tid + b * 256;
+        if (q < ne * gw) {
+            const int e = q / gw;
+            wreg[b] = rw4[(size_t)e * ngroups + g0 + (q - e * gw)];
+        }
+    }
+    double ss = 0.0;
+    for (int g = tid; g < ngroups; g += 256) {
+        const float4 v = xt[g];
+        *(float4*)(rt_sx + 4 * g) = v;
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+    if (nw) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) dred[tid >> 6] = ss;
+        __syncthreads();
+        const double tot = dred[0] + dred[1] + dred[2] + dred[3];
+        const double invd = 1.0 / sqrt(tot / (double)d + (double)eps);
+        const float inv = isfinite(invd) ? (float)invd : 0.0f;
+        for (int i = tid; i < d; i += 256) {
+            const float v = rt_sx[i] * inv * nw[i];
+            rt_sx[i] = v;
+            if (blockIdx.x == 0) xn[(size_t)t * d + i] = v;
+        }
+    }
+    __syncthreads();
+    float* tt = terms + ((size_t)t * ngroups + g0) * ne;
+    for (int q0 = 0; q0 < ne * gw; q0 += ROUTE_RB * 256) {
+        if (q0 > 0) {
+#pragma unroll
+            for (int b = 0; b < ROUTE_RB; ++b) {
+                const int q = q0 + tid + b * 256;
+                if (q < ne * gw) {
+                    const int e = q / gw;
+                    wreg[b] = rw4[(size_t)e * ngroups + g0 + (q - e * gw)];
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < ROUTE_RB; ++b) {
+            const int q = q0 + tid + b * 256;
+            if (q < ne * gw) {
+                const int e = q / gw, gl = q - e * gw;
+                const int i = 4 * (g0 + gl);
+                const float4 w = wreg[b];
+                const float p0 = rt_sx[i] * w.x, p1 = rt_sx[i + 1] * w.y, p2 = rt_sx[i + 2] * w.z,
+                            p3 = rt_sx[i + 3] * w.w;
+                tt[(size_t)gl * ne + e] = ((p0 + p1) + p2) + p3;
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(64) k_route_select(const float* __restrict__ terms, int ngroups, int ne, int K,
+                                                     const float* __restrict__ bias, int32_t* __restrict__ idx,
+                                                     float* __restrict__ wout, float* __restrict__ probs) {
+#pragma clang fp contract(off)
+    __shared__ float sp[64];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float* tt = terms + (size_t)t * ngroups * ne + lane;
+    float s = 0.0f;
+    if (lane < ne) {
+        int g = 0;
+        for (; g + 16 <= ngroups; g += 16) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = tt[(size_t)(g + j) * ne];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s += v[j];
+        }
+        for (; g < ngroups; ++g) s += tt[(size_t)g * ne];
+        sp[lane] = s;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    route_finish(sp, bias, ne, K, t, idx, wout, probs);
+}
+
+// router launch: one block per token, or the two-kernel form for a large
+// router matrix and few tokens
+static int launch_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w,
+                        int N, int d, int ne, int K, const float* nw, float eps, float* xn) {
+    if (N <= 8 && (size_t)ne * d > 16384) {
+        const int ngroups = d / 4;
+        float* terms = (float*)workspace(WS_MOE_TERMS, (size_t)N * ngroups * ne * 4);
+        if (!terms) return fail(GH_ENOMEM, "moe route: workspace");
+        hipLaunchKernelGGL(k_route_terms, dim3(cdiv(ngroups, RT_G), N), dim3(256), (size_t)d * 4, stream(), x, rw,
+                           terms, d, ne, nw, eps, xn);
+        hipLaunchKernelGGL(k_route_select, dim3(N), dim3(64), 0, stream(), terms, ngroups, ne, K, bias, idx, w,
+                           probs);
+        GH_LAUNCHED("k_route_terms/select");
+        return GH_OK;
+    }
+    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), x, rw, bias, probs, idx, w, d, ne,
+                       K, nw, eps, xn, route_window(d, ne, N));
+    GH_LAUNCHED("k_route");
+    return GH_OK;
 }
 
 // ========================================================== permutation
@@ -926,9 +1051,10 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     if (!r || !xn || !act || !sh_act) return fail(GH_ENOMEM, "moe: workspace");
     int32_t* idx = (int32_t*)r;
     float* w = (float*)(r + (size_t)S * 4);
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), xres, rw, bias, nullptr, idx, w, d,
-                       ne, K, nw, eps, xn, route_window(d, ne, N));
-    GH_LAUNCHED("k_route(norm)");
+    {
+        const int rc = launch_route(xres, rw, bias, nullptr, idx, w, N, d, ne, K, nw, eps, xn);
+        if (rc) return rc;
+    }
     GemvJobs J{};
     J.x = xn; J.idx = idx; J.S = S; J.N = has_sh ? N : 0; J.K = K; J.d = d;
     J.wa = (const uint8_t*)gates; J.wb = (const uint8_t*)ups; J.estride = (size_t)E * rowb_d;
@@ -976,10 +1102,7 @@ int moe_decode_fused(float* xres, const float* nw, float eps, const float* rw, c
 
 int moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int N, int d,
               int ne, int K) {
-    hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), x, rw, bias, probs, idx, w, d, ne,
-                       K, nullptr, 0.f, nullptr, route_window(d, ne, N));
-    GH_LAUNCHED("k_route");
-    return GH_OK;
+    return launch_route(x, rw, bias, probs, idx, w, N, d, ne, K, nullptr, 0.f, nullptr);
 }
 
 }  // namespace gh
