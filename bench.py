@@ -266,7 +266,7 @@ def roofline_gemv(gh):
     return run, bufs, nbytes
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv1_q4k_c2_traffic.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_c2_traffic.txt")
 COPY_FLOATS = 16 << 20  # 64 MiB per side
 
 
