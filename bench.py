@@ -135,7 +135,8 @@ def kernel_suite(gh):
                                10 if M > 8 else 200)
             tag = f"c2_{kname}_M{M}_{N}x{K}"
             if M <= 8:
-                res[tag] = entry("k_gemv_mfma", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
+                kern = "k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else "k_gemv_mfma"
+                res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
                 res[tag] = entry("k_to_f16+k_gemm_q2", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
                                  bound="mfma")
@@ -368,7 +369,7 @@ def main():
         kernels = kernel_suite(gh)
     kernels["c1_decode_moe_layer"] = entry("moe route+gemv x2+combine (c1)", moe_ms,
                                            bytes_=(2 * 3 * 256 * 512 + 3 * 512 * 512) * 144 // 256)
-    kernels["c1_decode_inproj_gemv"] = entry("k_gemv_mfma (c1 mamba in_proj 2192x512)", inproj_ms,
+    kernels["c1_decode_inproj_gemv"] = entry("k_gemv_q4k_i8 (c1 mamba in_proj 2192x512)", inproj_ms,
                                              bytes_=w.nbytes + 512 * 4 + proj * 4)
 
     cpu = None
@@ -399,7 +400,7 @@ def main():
         "decode_tok_s_q8_0": round(N_NEW * args.steps / (sum(d8) * 1e-3), 2),
         "prefill_tok_s_q8_0": round(PROMPT * args.steps / (sum(p8) * 1e-3), 1),
         "decode_ms_per_token": round(sum(dec_ms) / args.steps / N_NEW, 4),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_mfma<Q4_K,1,2> (BASELINE c2: 14336x4096, M=1)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_q4k_i8 (BASELINE c2: 14336x4096, M=1)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "avg_launch_us": round(gemv_ms * 1e3, 3), "algorithmic_bytes": int(gemv_bytes)},

@@ -619,6 +619,268 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
     }
 }
 
+// ---------------------------------------------------------------------------
+// Single-token Q4_K GEMV on int8 MFMA, weights streamed straight into LDS.
+//
+// Codes: the low nibbles of a Q4_K byte quad become four int8 codes with one
+// AND (u & 0x0F0F0F0F); the high nibbles become 16 c - 128 with one
+// three-input XOR (u ^ lo ^ 0x80808080), the -128 being undone by starting
+// their accumulator at 128 * (sum of the activation parts).
+// Activations: each 32-value sub-block j of x is split exactly into three
+// int8 parts, x = s_j (p0 + p1 / 128 + p2 / 16384) + O(s_j 2^-15), s_j =
+// max|x| / 127, so every product and sum is an exact integer and the result
+// keeps about 22 bits of every activation (the reference accumulates in fp32).
+// MFMA (v_mfma_i32_16x16x64_i8, block-diagonal A): lane (n = l % 16, g = l / 16)
+// holds 16 codes of row n (chunk g of a super-block) as B; A row m = 4g + e is
+// non-zero only in the lanes of group g and carries part e, so lane (n, g)
+// receives D[4g + e][n] = part-e dot of its own 16 codes for e = 0, 1, 2 at
+// once. A and the per-sub-block scales are the same for every tile a wave
+// processes, so they live in registers.
+// Streaming: one persistent block per CU slot walks tiles b, b+G, ... (16
+// rows each); wave w owns super-blocks SBW*w .. SBW*w+SBW-1 of every tile and
+// keeps NB tiles in flight in its ring of LDS slices, filled by
+// global_load_lds_dwordx4 (SGPR base + per-lane offset) from inline assembly
+// with explicit in-order vmcnt waits: the compiler's own tracking of LDS DMA
+// would drain every transfer before each LDS read, and __syncthreads would
+// drain them too (gd_barrier waits for LDS only). Waves never wait for each
+// other per tile: each leaves its row sums in LDS and the last wave to arrive
+// (LDS counter) adds them up and stores y.
+// K a multiple of 256 SBW, K <= 4096.
+constexpr int GD_S = 4;  // reduction slots (tiles a wave may run ahead between barriers)
+typedef int gd_i4 __attribute__((ext_vector_type(4)));
+
+template <int SBW>
+struct GdCfg {
+    static constexpr int PR = 9 * SBW;          // 16-byte pieces per row of a wave's column
+    static constexpr int NP = 16 * PR;          // pieces per column (16 rows)
+    static constexpr int PPL = (NP + 63) / 64;  // transfers per wave and tile (the last one partial)
+};
+
+// 16 bytes per lane from base + voff into LDS at lds_base + 16 * lane
+__device__ __forceinline__ void gd_dma16s(const void* base, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ uint32_t gd_lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+__device__ __forceinline__ void gd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// wait until at most `ahead` tiles of PPL transfers are outstanding (vmcnt takes an immediate)
+template <int PPL>
+__device__ __forceinline__ void gd_wait(int ahead) {
+    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PPL) : "memory");
+    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PPL) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPL) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ gd_i4 gd_lo_codes(uint4 u) {
+    return gd_i4{(int)(u.x & 0x0F0F0F0Fu), (int)(u.y & 0x0F0F0F0Fu), (int)(u.z & 0x0F0F0F0Fu), (int)(u.w & 0x0F0F0F0Fu)};
+}
+__device__ __forceinline__ gd_i4 gd_hi_codes(uint4 u, gd_i4 lo) {
+    return gd_i4{(int)(u.x ^ (uint32_t)lo.x ^ 0x80808080u), (int)(u.y ^ (uint32_t)lo.y ^ 0x80808080u),
+                 (int)(u.z ^ (uint32_t)lo.z ^ 0x80808080u), (int)(u.w ^ (uint32_t)lo.w ^ 0x80808080u)};
+}
+__device__ __forceinline__ uint32_t gd_pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+// dynamic LDS of k_gemv_q4k_i8: ring, x, parts, part sums, scales, x sums, reduction slots, counters
+static size_t gd_lds_bytes(int K, int SBW, int NB) {
+    const size_t WB = K / (256 * SBW);
+    return (size_t)NB * WB * 144 * SBW * 16 + (size_t)K * 4 + 3 * (size_t)K + (size_t)K / 32 * 12 + (size_t)K / 32 * 8 +
+           GD_S * WB * 16 * 4 + GD_S * 4;
+}
+
+template <int SBW, int NB>
+__global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                           float* __restrict__ y, int K, int N, size_t rowb) {
+    using C = GdCfg<SBW>;
+    constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL;
+    extern __shared__ __attribute__((aligned(16))) uint4 gd_lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int WB = blockDim.x >> 6;  // = K / (256 SBW); K / 4 = SBW * blockDim.x float4 pieces of x
+    const int K4 = K >> 2;
+    const int ntiles = (N + 15) >> 4, G = gridDim.x, t0 = blockIdx.x;
+    uint4* ring = gd_lds;                                   // [NB][WB][NP]
+    float4* sx = (float4*)(ring + (size_t)NB * WB * NP);    // [K / 4]
+    uint32_t* apart = (uint32_t*)(sx + K4);                 // [3][K / 4] four int8 parts each
+    int* shs = (int*)(apart + 3 * K4);                      // [K / 32][3] sums of the three parts
+    float* ssc = (float*)(shs + 3 * (K >> 5));              // [K / 32] part scales s_j
+    float* sxs = ssc + (K >> 5);                            // [K / 32] sums of x
+    float* sred = sxs + (K >> 5);                           // [GD_S][WB][16]
+    int* scnt = (int*)(sred + GD_S * WB * 16);              // [GD_S]
+    // x: piece tid + j * blockDim.x (contiguous per wave instruction)
+#pragma unroll
+    for (int j = 0; j < SBW; ++j)
+        gd_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, gd_lds_addr(&sx[wave * 64 + j * blockDim.x]));
+    // column `wave` of a tile -> ring slice; piece q = PR r + j of row r
+    uint32_t voff[PPL];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+        const int q = lane + 64 * i, r = q / PR, j = q - r * PR;
+        voff[i] = (uint32_t)(r * rowb) + wave * (144 * SBW) + 16 * j;
+    }
+    auto dma = [&](int tile, int b) {
+        uint4* dst = ring + ((size_t)b * WB + wave) * NP;
+        const uint8_t* base = W + (size_t)tile * 16 * rowb;
+        if (tile * 16 + 16 <= N) {
+#pragma unroll
+            for (int i = 0; i < PPL; ++i)
+                if (NP % 64 == 0 || i + 1 < PPL || lane + 64 * i < NP) gd_dma16s(base, voff[i], gd_lds_addr(dst + 64 * i));
+        } else {  // ragged last tile: rows past N re-read row N-1
+#pragma unroll
+            for (int i = 0; i < PPL; ++i) {
+                const int q = lane + 64 * i;
+                if (q < NP) {
+                    const int r = q / PR, j = q - r * PR, rc = tile * 16 + r < N ? r : N - 1 - tile * 16;
+                    gd_dma16s(base, (uint32_t)(rc * rowb) + wave * (144 * SBW) + 16 * j, gd_lds_addr(dst + 64 * i));
+                }
+            }
+        }
+    };
+    // the first NB tiles are always issued (a missing tile re-reads the last one), so every wait is exact
+#pragma unroll
+    for (int b = 0; b < NB; ++b) dma(t0 + b * G < ntiles ? t0 + b * G : ntiles - 1, b);
+    // ---- x -> three int8 parts per value; scale, x sum and part sums per 32 values (8 threads each)
+    gd_wait<PPL>(NB);  // x landed (weights in flight)
+    gd_barrier();
+#pragma unroll
+    for (int jj = 0; jj < SBW; ++jj) {
+        const int idx = tid + jj * blockDim.x;
+        const float4 v4 = sx[idx];
+        float m = fmaxf(fmaxf(fabsf(v4.x), fabsf(v4.y)), fmaxf(fabsf(v4.z), fabsf(v4.w)));
+        float sum = (v4.x + v4.y) + (v4.z + v4.w);
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            m = fmaxf(m, __shfl_xor(m, o, 64));
+            sum += __shfl_xor(sum, o, 64);
+        }
+        const float inv = m > 0.f ? 127.f / m : 0.f;
+        int p[3][4];
+        const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float t = vv[q] * inv;
+            const float a0 = rintf(t);
+            const float r1 = (t - a0) * 128.f;
+            const float a1 = rintf(r1);
+            const float a2 = rintf((r1 - a1) * 128.f);
+            p[0][q] = (int)a0; p[1][q] = (int)a1; p[2][q] = (int)a2;
+        }
+        int ps[3];
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {
+            apart[e * K4 + idx] = gd_pack4(p[e][0], p[e][1], p[e][2], p[e][3]);
+            ps[e] = p[e][0] + p[e][1] + p[e][2] + p[e][3];
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) ps[e] += __shfl_xor(ps[e], o, 64);
+        }
+        if ((idx & 7) == 0) {
+            const int sbk = idx >> 3;
+            ssc[sbk] = m * (1.f / 127.f);
+            sxs[sbk] = sum;
+            shs[3 * sbk] = ps[0];
+            shs[3 * sbk + 1] = ps[1];
+            shs[3 * sbk + 2] = ps[2];
+        }
+    }
+    if (tid < GD_S) scnt[tid] = 0;
+    gd_barrier();
+    // A operands of this wave's super-blocks (rows m = 4g + e of group g), scales, high-nibble offsets
+    gd_i4 A[SBW][2][2], hinit[SBW];
+    float s_lo[SBW], s_hi[SBW], xs_lo[SBW], xs_hi[SBW];
+    {
+        const int e = n16 & 3;
+        const bool on = (n16 >> 2) == g && e < 3;
+#pragma unroll
+        for (int sbl = 0; sbl < SBW; ++sbl) {
+            const int sb = wave * SBW + sbl;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+                    A[sbl][h][r] = on ? *(const gd_i4*)&apart[e * K4 + ((sb * 256 + 64 * g + 32 * h + 16 * r) >> 2)]
+                                      : gd_i4{0, 0, 0, 0};
+            const int jl = sb * 8 + 2 * g, jh = jl + 1;
+            // parts combine as 16384 p0 + 128 p1 + p2 (exact in int32), hence the 2^-14
+            s_lo[sbl] = ssc[jl] * (1.f / 16384.f);
+            s_hi[sbl] = ssc[jh] * (1.f / 16384.f);
+            xs_lo[sbl] = sxs[jl];
+            xs_hi[sbl] = sxs[jh];
+            // high-nibble codes are 16 c - 128: their accumulator starts at 128 * (part sums)
+            hinit[sbl] = gd_i4{128 * shs[3 * jh], 128 * shs[3 * jh + 1], 128 * shs[3 * jh + 2], 0};
+        }
+    }
+    int b = 0;
+    for (int it = 0;; ++it) {
+        const int tile = t0 + it * G;
+        if (tile >= ntiles) break;
+        // tiles issued after this one: it+1 .. it+NB-1, each issued if among the first NB or real
+        int ahead = 0;
+#pragma unroll
+        for (int j = 1; j < NB; ++j) ahead += (it + j < NB || tile + j * G < ntiles) ? 1 : 0;
+        gd_wait<PPL>(ahead);
+        const unsigned char* rowp = (const unsigned char*)(ring + ((size_t)b * WB + wave) * NP) + n16 * (144 * SBW);
+        uint4 hd[SBW], qa[SBW], qb[SBW];
+#pragma unroll
+        for (int sbl = 0; sbl < SBW; ++sbl) {
+            hd[sbl] = *(const uint4*)(rowp + 144 * sbl);
+            qa[sbl] = *(const uint4*)(rowp + 144 * sbl + 16 + 32 * g);
+            qb[sbl] = *(const uint4*)(rowp + 144 * sbl + 32 + 32 * g);
+        }
+        if (tile + NB * G < ntiles) {  // slice read: refill it
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            dma(tile + NB * G, b);
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int sbl = 0; sbl < SBW; ++sbl) {
+            const gd_i4 la = gd_lo_codes(qa[sbl]), lb = gd_lo_codes(qb[sbl]);
+            gd_i4 Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][0][0], la, gd_i4{0, 0, 0, 0}, 0, 0, 0);
+            gd_i4 Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][1][0], gd_hi_codes(qa[sbl], la), hinit[sbl], 0, 0, 0);
+            Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][0][1], lb, Dl, 0, 0, 0);
+            Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][1][1], gd_hi_codes(qb[sbl], lb), Dh, 0, 0, 0);
+            // scales of sub-blocks 2g (low nibbles) and 2g+1 (high nibbles)
+            const uint4 h4 = hd[sbl];
+            const float d = gm_lo16(h4.x), dmin = gm_hi16(h4.x);
+            const int j0 = 2 * (g & 1);
+            const uint32_t A2 = (h4.y >> (8 * j0)) & 0xFFFFu, B2 = (h4.z >> (8 * j0)) & 0xFFFFu,
+                           C2 = (h4.w >> (8 * j0)) & 0xFFFFu;
+            const uint32_t scp = g < 2 ? (A2 & 0x3F3Fu) : ((C2 & 0x0F0Fu) | ((A2 >> 2) & 0x3030u));
+            const uint32_t mp = g < 2 ? (B2 & 0x3F3Fu) : (((C2 >> 4) & 0x0F0Fu) | ((B2 >> 2) & 0x3030u));
+            // |D0| <= 32 * 15 * 127, |D1|, |D2| <= 32 * 15 * 64: 16384 D0 + 128 D1 + D2 fits in int32;
+            // the high-nibble sums are 16x (exact), so their weights are 1024, 8 and 1/16
+            const int il = Dl[0] * 16384 + Dl[1] * 128 + Dl[2];
+            const int ih = Dh[0] * 1024 + Dh[1] * 8 + (Dh[2] >> 4);
+            acc += d * ((float)(scp & 0xFFu) * s_lo[sbl] * (float)il + (float)(scp >> 8) * s_hi[sbl] * (float)ih) -
+                   dmin * ((float)(mp & 0xFFu) * xs_lo[sbl] + (float)(mp >> 8) * xs_hi[sbl]);
+        }
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        // row sums of this column -> slot; the last column to arrive stores y
+        const int slot = it & (GD_S - 1);
+        float* red = sred + slot * WB * 16;
+        if (lane < 16) red[wave * 16 + lane] = acc;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        int old = 0;
+        if (lane == 0) old = atomicAdd(&scnt[slot], 1);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old == WB - 1) {
+            if (lane < 16) {
+                float v = 0.f;
+                for (int wv = 0; wv < WB; ++wv) v += red[wv * 16 + lane];
+                const int n = tile * 16 + lane;
+                if (n < N) y[n] = v;
+            }
+            if (lane == 0) scnt[slot] = 0;
+        }
+        // a slot is reused GD_S tiles later: keep every wave within GD_S tiles of the others
+        if (slot == GD_S - 1) gd_barrier();
+        b = b + 1 == NB ? 0 : b + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no transfer into LDS outlives the block
+}
+
 static int env_int(const char* name, int dflt) {
     const char* e = getenv(name);
     return e ? atoi(e) : dflt;
@@ -707,11 +969,49 @@ static int gm_kind(const float* x, const void* w, float* y, int M, int K, int N)
     return gm_ss<KIND, 4>(x, w, y, M, K, N);
 }
 
+template <int SBW, int NB>
+static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N) {
+    static int configured = 0;
+    static int per_cu[17];  // resident blocks per CU by K / (256 SBW)
+    const size_t lds = gd_lds_bytes(K, SBW, NB);
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)gd_lds_bytes(4096, SBW, NB));
+        if (e != hipSuccess) return fail(GH_EHIP, "k_gemv_q4k_i8 LDS attribute: %s", hipGetErrorString(e));
+        configured = 1;
+    }
+    const int wb = K / (256 * SBW);
+    if (!per_cu[wb]) {
+        int nb = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB>, 64 * wb, lds);
+        per_cu[wb] = e == hipSuccess && nb > 0 ? nb : 1;
+    }
+    const int ntiles = (N + 15) / 16;
+    const int slots = per_cu[wb] * num_cus();
+    const int blocks = ntiles < slots ? ntiles : slots;
+    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K, N,
+                       row_bytes(3, K));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
+}
+
+// variant: tens digit = ring depth NB (2, 3), units = super-blocks per wave (1, 2; 2 needs K % 512 == 0)
+static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N, int variant) {
+    const int nb = variant / 10, sbw = (variant % 10 == 2 && K % 512 == 0) ? 2 : 1;
+    if (sbw == 2) return nb == 3 ? gd_launch<2, 3>(x, w, y, K, N) : gd_launch<2, 2>(x, w, y, K, N);
+    return nb == 3 ? gd_launch<1, 3>(x, w, y, K, N) : gd_launch<1, 2>(x, w, y, K, N);
+}
+
 // Returns 1 if handled (Q4_K / Q8_0, 1 <= M <= 8, K a multiple of 256).
 // Token groups whose activations do not fit LDS together are run as
 // separate launches over the same weights.
 int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
     static const int enabled = env_int("GH_GEMV_MFMA", 1);
+    static const int dma = env_int("GH_GEMV_DMA", 21);  // 0 off, else the variant of gemv_q4k_i8
+    if (enabled && dma && M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
+        *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, dma);
+        return 1;
+    }
     static const int q8_m1 = env_int("GH_GEMV_MFMA_Q8M1", 1);
     if (!enabled || (kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
     if (kind == 2 && M == 1 && !q8_m1) return 0;
