@@ -638,15 +638,17 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
 // processes, so they live in registers.
 // Streaming: one persistent block per CU slot walks tiles b, b+G, ... (16
 // rows each); wave w owns super-blocks SBW*w .. SBW*w+SBW-1 of every tile and
-// keeps NB tiles in flight in its ring of LDS slices, filled by
+// keeps NB (= 2) tiles in flight in its ring of LDS slices, filled by
 // global_load_lds_dwordx4 (SGPR base + per-lane offset) from inline assembly
 // with explicit in-order vmcnt waits: the compiler's own tracking of LDS DMA
 // would drain every transfer before each LDS read, and __syncthreads would
-// drain them too (gd_barrier waits for LDS only). Waves never wait for each
-// other per tile: each leaves its row sums in LDS and the last wave to arrive
-// (LDS counter) adds them up and stores y.
+// drain them too (gd_barrier waits for LDS only). Waves do not synchronise
+// per tile: every lane leaves its partial sum in LDS, and after each group
+// of GD_S tiles (one barrier) the block adds the partials of the group and
+// stores its rows of y; groups alternate between two LDS areas, so the next
+// group's partials never overwrite ones still being added.
 // K a multiple of 256 SBW, K <= 4096.
-constexpr int GD_S = 4;  // reduction slots (tiles a wave may run ahead between barriers)
+constexpr int GD_S = 4;  // tiles per reduction group
 typedef int gd_i4 __attribute__((ext_vector_type(4)));
 
 template <int SBW>
@@ -683,11 +685,11 @@ __device__ __forceinline__ uint32_t gd_pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
 }
 
-// dynamic LDS of k_gemv_q4k_i8: ring, x, parts, part sums, scales, x sums, reduction slots, counters
+// dynamic LDS of k_gemv_q4k_i8: ring, x, parts, part sums, scales, x sums, partial sums
 static size_t gd_lds_bytes(int K, int SBW, int NB) {
     const size_t WB = K / (256 * SBW);
     return (size_t)NB * WB * 144 * SBW * 16 + (size_t)K * 4 + 3 * (size_t)K + (size_t)K / 32 * 12 + (size_t)K / 32 * 8 +
-           GD_S * WB * 16 * 4 + GD_S * 4;
+           2 * GD_S * WB * 64 * 4;
 }
 
 template <int SBW, int NB>
@@ -707,8 +709,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     int* shs = (int*)(apart + 3 * K4);                      // [K / 32][3] sums of the three parts
     float* ssc = (float*)(shs + 3 * (K >> 5));              // [K / 32] part scales s_j
     float* sxs = ssc + (K >> 5);                            // [K / 32] sums of x
-    float* sred = sxs + (K >> 5);                           // [GD_S][WB][16]
-    int* scnt = (int*)(sred + GD_S * WB * 16);              // [GD_S]
+    float4* sred = (float4*)(sxs + (K >> 5));               // [2][GD_S][WB][16] (4 lane groups each)
     // x: piece tid + j * blockDim.x (contiguous per wave instruction)
 #pragma unroll
     for (int j = 0; j < SBW; ++j)
@@ -784,7 +785,6 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             shs[3 * sbk + 2] = ps[2];
         }
     }
-    if (tid < GD_S) scnt[tid] = 0;
     gd_barrier();
     // A operands of this wave's super-blocks (rows m = 4g + e of group g), scales, high-nibble offsets
     gd_i4 A[SBW][2][2], hinit[SBW];
@@ -855,27 +855,29 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             acc += d * ((float)(scp & 0xFFu) * s_lo[sbl] * (float)il + (float)(scp >> 8) * s_hi[sbl] * (float)ih) -
                    dmin * ((float)(mp & 0xFFu) * xs_lo[sbl] + (float)(mp >> 8) * xs_hi[sbl]);
         }
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
-        // row sums of this column -> slot; the last column to arrive stores y
-        const int slot = it & (GD_S - 1);
-        float* red = sred + slot * WB * 16;
-        if (lane < 16) red[wave * 16 + lane] = acc;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        int old = 0;
-        if (lane == 0) old = atomicAdd(&scnt[slot], 1);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (old == WB - 1) {
-            if (lane < 16) {
+        // partial of (row n16, lane group g) -> slot; a group of GD_S tiles is added up at once
+        const int slot = it & (GD_S - 1), grp = (it / GD_S) & 1;
+        float4* red = sred + (size_t)(grp * GD_S + slot) * WB * 16;
+        ((float*)&red[wave * 16 + n16])[g] = acc;
+        if (slot == GD_S - 1 || tile + G >= ntiles) {
+            gd_barrier();
+            // thread (output o, wave w = tid % 16) adds w's four lane groups; 16 lanes add the waves
+            const int w = tid & 15;
+            for (int o = tid >> 4; o < 16 * (slot + 1); o += blockDim.x >> 4) {  // uniform per 16 lanes
+                const int tl = o >> 4, row = o & 15;
                 float v = 0.f;
-                for (int wv = 0; wv < WB; ++wv) v += red[wv * 16 + lane];
-                const int n = tile * 16 + lane;
-                if (n < N) y[n] = v;
+                if (w < WB) {
+                    const float4 p4 = sred[(size_t)(grp * GD_S + tl) * WB * 16 + w * 16 + row];
+                    v = (p4.x + p4.y) + (p4.z + p4.w);
+                }
+                v += __shfl_xor(v, 1, 64);
+                v += __shfl_xor(v, 2, 64);
+                v += __shfl_xor(v, 4, 64);
+                v += __shfl_xor(v, 8, 64);
+                const int n = (tile - (slot - tl) * G) * 16 + row;
+                if (w == 0 && n < N) y[n] = v;
             }
-            if (lane == 0) scnt[slot] = 0;
         }
-        // a slot is reused GD_S tiles later: keep every wave within GD_S tiles of the others
-        if (slot == GD_S - 1) gd_barrier();
         b = b + 1 == NB ? 0 : b + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no transfer into LDS outlives the block
@@ -995,11 +997,10 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N) {
     return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
 }
 
-// variant: tens digit = ring depth NB (2, 3), units = super-blocks per wave (1, 2; 2 needs K % 512 == 0)
+// variant 1: one super-block per wave; 2: two (needs K % 512 == 0)
 static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N, int variant) {
-    const int nb = variant / 10, sbw = (variant % 10 == 2 && K % 512 == 0) ? 2 : 1;
-    if (sbw == 2) return nb == 3 ? gd_launch<2, 3>(x, w, y, K, N) : gd_launch<2, 2>(x, w, y, K, N);
-    return nb == 3 ? gd_launch<1, 3>(x, w, y, K, N) : gd_launch<1, 2>(x, w, y, K, N);
+    if (variant == 2 && K % 512 == 0) return gd_launch<2, 2>(x, w, y, K, N);
+    return gd_launch<1, 2>(x, w, y, K, N);
 }
 
 // Returns 1 if handled (Q4_K / Q8_0, 1 <= M <= 8, K a multiple of 256).
@@ -1007,7 +1008,7 @@ static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N,
 // separate launches over the same weights.
 int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
     static const int enabled = env_int("GH_GEMV_MFMA", 1);
-    static const int dma = env_int("GH_GEMV_DMA", 21);  // 0 off, else the variant of gemv_q4k_i8
+    static const int dma = env_int("GH_GEMV_DMA", 1);  // 0 off, else the variant of gemv_q4k_i8
     if (enabled && dma && M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
         *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, dma);
         return 1;
