@@ -638,7 +638,7 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
 // processes, so they live in registers.
 // Streaming: one persistent block per CU slot walks tiles b, b+G, ... (16
 // rows each); wave w owns super-blocks SBW*w .. SBW*w+SBW-1 of every tile and
-// keeps NB (= 2) tiles in flight in its ring of LDS slices, filled by
+// keeps NB tiles in flight in its ring of LDS slices, filled by
 // global_load_lds_dwordx4 (SGPR base + per-lane offset) from inline assembly
 // with explicit in-order vmcnt waits: the compiler's own tracking of LDS DMA
 // would drain every transfer before each LDS read, and __syncthreads would
@@ -740,10 +740,11 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         }
     };
     // the first NB tiles are always issued (a missing tile re-reads the last one), so every wait is exact
-#pragma unroll
-    for (int b = 0; b < NB; ++b) dma(t0 + b * G < ntiles ? t0 + b * G : ntiles - 1, b);
+    // only the first tile now: the memory system returns it sooner when the other tiles of the
+    // ring are requested after the conversion of x (the ring is always filled, so every wait is exact)
+    dma(t0 < ntiles ? t0 : ntiles - 1, 0);
     // ---- x -> three int8 parts per value; scale, x sum and part sums per 32 values (8 threads each)
-    gd_wait<PPL>(NB);  // x landed (weights in flight)
+    gd_wait<PPL>(1);  // x landed (the first tile in flight)
     gd_barrier();
 #pragma unroll
     for (int jj = 0; jj < SBW; ++jj) {
@@ -785,6 +786,9 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             shs[3 * sbk + 2] = ps[2];
         }
     }
+    // the rest of the ring (a missing tile re-reads the last one)
+#pragma unroll
+    for (int b = 1; b < NB; ++b) dma(t0 + b * G < ntiles ? t0 + b * G : ntiles - 1, b);
     gd_barrier();
     // A operands of this wave's super-blocks (rows m = 4g + e of group g), scales, high-nibble offsets
     gd_i4 A[SBW][2][2], hinit[SBW];
@@ -997,7 +1001,7 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N) {
     return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
 }
 
-// variant 1: one super-block per wave; 2: two (needs K % 512 == 0)
+// variant 1: one super-block per wave; 2: two super-blocks per wave (needs K % 512 == 0)
 static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N, int variant) {
     if (variant == 2 && K % 512 == 0) return gd_launch<2, 2>(x, w, y, K, N);
     return gd_launch<1, 2>(x, w, y, K, N);
