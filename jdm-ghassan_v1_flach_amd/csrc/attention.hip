@@ -19,6 +19,7 @@
 #include <stdlib.h>
 
 #include "gh_common.h"
+#include "lds_dma.h"
 
 namespace gh {
 
@@ -222,6 +223,276 @@ __global__ void __launch_bounds__(256) k_attn_decode(DecodeArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------- decode v2
+// head_dim 64 / 128: the same split-K partials as k_attn_decode, in one pass
+// over the run with an online softmax per wave:
+//  - K and V rows of a group of 16 positions are moved together by LDS DMA
+//    into a wave-private ring of DEC2_NST stages, requested DEC2_NST groups
+//    ahead; K's 16-byte pieces are stored with an XOR swizzle so the 16 rows
+//    of an MFMA operand read hit distinct LDS banks;
+//  - scores on the matrix cores: S = K q^T by v_mfma_f32_16x16x32_{bf16,f16}
+//    (A = the 16 K rows, B = the G query heads as columns), q split into two
+//    parts of the cache's type (hi + lo) so the products keep fp32-level
+//    accuracy; no per-position lane reductions;
+//  - running max / sum per head, P handed to the P V layout through a small
+//    wave-private LDS area; P V on the vector units (a lane owns 8 channels
+//    of a few rows per group), accumulators rescaled when the max grows;
+//  - the 4 waves' (max, sum, o) merged in LDS into the block's partial.
+// Wave w processes the groups w, w+4, ... of the block's run.
+constexpr int DEC2_NST = 2;
+
+template <bool BF>
+struct Dec2Op;
+template <>
+struct Dec2Op<true> {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+    typedef __bf16 s;
+    __device__ static float4 mfma(v8 a, v8 b, float4 c) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 r = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, __builtin_bit_cast(f4, c), 0, 0, 0);
+        return __builtin_bit_cast(float4, r);
+    }
+};
+template <>
+struct Dec2Op<false> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 s;
+    __device__ static float4 mfma(v8 a, v8 b, float4 c) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 r = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, __builtin_bit_cast(f4, c), 0, 0, 0);
+        return __builtin_bit_cast(float4, r);
+    }
+};
+
+constexpr int DEC2_CHUNK_MAX = 2048;  // positions per block (no score buffer bounds it)
+
+template <int HD, bool PAGED, int GMAX>
+__global__ void __launch_bounds__(256) k_attn_decode2(DecodeArgs a) {
+    using Op = Dec2Op<PAGED>;  // the paged cache is bf16, the ring cache fp16
+    constexpr int PPR = HD / 8;        // 16-byte pieces per row
+    constexpr int RPI = 64 / PPR;      // rows per transfer instruction
+    constexpr int IPS = 16 / RPI;      // transfer instructions per 16 rows
+    constexpr int KS = HD / 32;        // MFMA k-steps
+    constexpr int NST = DEC2_NST;
+    constexpr int SH = PPR == 16 ? 0 : 1;         // K piece m of row r sits at m ^ ((r >> SH) & (PPR - 1))
+    constexpr int QI = (GMAX * HD / 4 + 63) / 64;  // transfers of the query block (fp32, G <= GMAX)
+    static_assert(QI * 64 <= 2 * 16 * PPR, "query block fits a ring stage");
+    __shared__ __attribute__((aligned(16))) uint4 ring[4][NST][2][16 * PPR];  // [wave][stage][K, V][rows]
+    __shared__ __attribute__((aligned(16))) float pex[4][GMAX][20];  // per wave: P [head][position], [16] = rescale
+    __shared__ int spage[PAGED ? DEC2_CHUNK_MAX + 1 : 1];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.G;
+    if (!PAGED && a.ctl) {  // decode control block: token, len, start, pinned
+        a.cur_len = a.ctl[1];
+        a.ring_start = a.ctl[2];
+        a.pinned = min(a.ctl[3], a.cur_len);
+    }
+    int jb, je;  // logical positions [jb, je) of this block
+    if (PAGED) {
+        const int L = a.seq_lens[seq];
+        jb = split * a.chunk;
+        je = min(L, jb + a.chunk);
+    } else {
+        jb = a.j0 + split * a.chunk;
+        je = min(a.cur_len, jb + a.chunk);
+    }
+    const int n = je - jb;
+    const size_t part = ((size_t)seq * a.KV + kvh) * a.splits + split;
+    if (n <= 0) {
+        if (tid < G) {
+            a.ml_part[(part * G + tid) * 2] = -INFINITY;
+            a.ml_part[(part * G + tid) * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    int pg0 = 0;
+    if (PAGED) {  // the run's page numbers, staged before any transfer is in flight
+        pg0 = jb / a.page_size;
+        const int npg = (je - 1) / a.page_size - pg0 + 1;
+        for (int i = tid; i < npg; i += 256) spage[i] = a.page_table[(size_t)seq * a.max_pages + pg0 + i];
+        __syncthreads();
+    }
+    const int ring_cap = a.cache_max - a.pinned;
+    auto row_of = [&](int j) -> size_t {  // element offset of row (position j, kvh)
+        size_t slot;
+        if (PAGED) {
+            slot = (size_t)spage[j / a.page_size - pg0] * a.page_size + j % a.page_size;
+        } else {
+            slot = j < a.pinned ? (size_t)j
+                                : (size_t)a.pinned + (size_t)((a.ring_start + (j - a.pinned)) % (ring_cap > 0 ? ring_cap : 1));
+        }
+        return (slot * a.KV + kvh) * HD;
+    };
+    const int ngroups = (n + 15) >> 4;
+    const int ngw = wave < ngroups ? (ngroups - wave + 3) >> 2 : 0;  // this wave's groups: wave, wave+4, ...
+    // K and V rows of group k of this wave -> ring stage st (rows past the run re-read its last row)
+    auto dma = [&](int k, int st) {
+        const int gi = wave + 4 * (k < ngw ? k : ngw - 1);
+#pragma unroll
+        for (int i = 0; i < IPS; ++i) {
+            const int slot = i * 64 + lane, r = slot / PPR, t = slot % PPR;
+            const size_t row = row_of(jb + min(gi * 16 + r, n - 1));
+            lds_dma16(a.k + row + (t ^ ((r >> SH) & (PPR - 1))) * 8, lds_addr(&ring[wave][st][0][i * 64]));
+            lds_dma16(a.v + row + t * 8, lds_addr(&ring[wave][st][1][i * 64]));
+        }
+    };
+    // ---- query block -> the wave's last ring stage (read before that stage is first filled)
+    {
+        const float* qb = a.q + ((size_t)seq * a.H + (size_t)kvh * G) * HD;
+        float* qs = (float*)&ring[wave][NST - 1][0][0];
+#pragma unroll
+        for (int i = 0; i < QI; ++i) {
+            const int piece = min(i * 64 + lane, G * HD / 4 - 1);
+            lds_dma16(qb + 4 * piece, lds_addr(qs + i * 256));
+        }
+    }
+    if (ngw > 0)
+#pragma unroll
+        for (int st = 0; st < NST - 1; ++st) dma(st, st);
+    lds_dma_wait<2 * IPS>(ngw > 0 ? NST - 1 : 0);  // the query block landed
+    const int n16 = lane & 15, kg = lane >> 4;
+    typename Op::v8 bh[KS], bl[KS];  // B: column n16 = head n16 (zero past G), channels 32 s + 8 kg + i
+    {
+        const float* qs = (const float*)&ring[wave][NST - 1][0][0] + n16 * HD;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float qv = n16 < G ? qs[32 * s + 8 * kg + i] : 0.f;
+                const typename Op::s h = (typename Op::s)qv;
+                bh[s][i] = h;
+                bl[s][i] = (typename Op::s)(qv - (float)h);
+            }
+    }
+    lds_wait_lgkm();
+    if (ngw > 0) dma(NST - 1, NST - 1);
+    const int sub = lane / PPR, cg = lane % PPR;  // P V: channels 8 cg .. 8 cg + 7 of rows sub + RPI r
+    float acc[GMAX][8];
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    float run_m = -INFINITY, run_l = 0.f;  // of head n16 (lanes n16 < G)
+    for (int k = 0; k < ngw; ++k) {
+        lds_dma_wait<2 * IPS>((k + 1 < NST || k + 1 < ngw) ? 1 : 0);
+        const int st = k % NST;
+        uint4 ar[KS], vr[16 / RPI];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) ar[s] = ring[wave][st][0][n16 * PPR + ((4 * s + kg) ^ ((n16 >> SH) & (PPR - 1)))];
+#pragma unroll
+        for (int r = 0; r < 16 / RPI; ++r) vr[r] = ring[wave][st][1][(sub + RPI * r) * PPR + cg];
+        if (k + NST < ngw) {
+            lds_wait_lgkm();
+            dma(k + NST, st);
+        }
+        float4 d = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const typename Op::v8 av = __builtin_bit_cast(typename Op::v8, ar[s]);
+            d = Op::mfma(av, bh[s], d);
+            d = Op::mfma(av, bl[s], d);
+        }
+        // lane (head n16, row group kg) holds positions p0 + e of the group
+        const int gp0 = (wave + 4 * k) * 16, p0 = gp0 + 4 * kg;
+        float sv[4] = {d.x * a.scale, d.y * a.scale, d.z * a.scale, d.w * a.scale};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (p0 + e >= n) sv[e] = -INFINITY;
+        float gm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        gm = fmaxf(gm, __shfl_xor(gm, 16, 64));
+        gm = fmaxf(gm, __shfl_xor(gm, 32, 64));
+        const float nm = fmaxf(run_m, gm);  // finite: the group has at least one position
+        const float f = expf(run_m - nm);
+        float pv[4], ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            pv[e] = expf(sv[e] - nm);
+            ps += pv[e];
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        run_l = run_l * f + ps;
+        run_m = nm;
+        if (n16 < G) {
+            *(float4*)&pex[wave][n16][4 * kg] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            if (kg == 0) pex[wave][n16][16] = f;
+        }
+        lds_wait_lgkm();  // the wave's own P (no other wave touches pex[wave])
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= G) break;
+            const float fg = pex[wave][g][16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] *= fg;
+        }
+#pragma unroll
+        for (int r = 0; r < 16 / RPI; ++r) {
+            float vf[8];
+            widen8<PAGED>(vr[r], vf);
+#pragma unroll
+            for (int g = 0; g < GMAX; ++g) {
+                if (g >= G) break;
+                const float w = pex[wave][g][sub + RPI * r];  // 0 past the run
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(w, vf[i], acc[g][i]);
+            }
+        }
+        lds_wait_lgkm();  // pex is rewritten by the next group
+    }
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+        if (g >= G) break;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+#pragma unroll
+            for (int o = PPR; o < 64; o <<= 1) acc[g][i] += __shfl_xor(acc[g][i], o, 64);
+        }
+    }
+    // ---- merge the 4 waves: (m_w, l_w, o_w) -> (M, sum l_w e^(m_w - M), sum o_w e^(m_w - M))
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // re-read stages of a short run
+    lds_barrier();  // every wave is done with its ring: it becomes the merge area
+    float* red = (float*)&ring[0][0][0][0];  // [4][GMAX][HD]
+    float* wml = red + 4 * GMAX * HD;    // [4][GMAX][2]
+    if (sub == 0)
+#pragma unroll
+        for (int g = 0; g < GMAX; ++g) {
+            if (g >= G) break;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red[(wave * GMAX + g) * HD + cg * 8 + i] = acc[g][i];
+        }
+    if (kg == 0 && n16 < G) {
+        wml[(wave * GMAX + n16) * 2] = run_m;
+        wml[(wave * GMAX + n16) * 2 + 1] = run_l;
+    }
+    lds_barrier();
+    for (int e = tid; e < G * HD; e += 256) {
+        const int g = e / HD, c = e % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * GMAX + g) * 2]);
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mw = wml[(w * GMAX + g) * 2];
+            if (mw > -INFINITY) o += red[(w * GMAX + g) * HD + c] * expf(mw - M);
+        }
+        a.o_part[(part * G + g) * HD + c] = o;
+    }
+    if (tid < G) {
+        float M = -INFINITY, L = 0.f;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wml[(w * GMAX + tid) * 2]);
+        for (int w = 0; w < 4; ++w) {
+            const float mw = wml[(w * GMAX + tid) * 2];
+            if (mw > -INFINITY) L += wml[(w * GMAX + tid) * 2 + 1] * expf(mw - M);
+        }
+        a.ml_part[(part * G + tid) * 2] = M;
+        a.ml_part[(part * G + tid) * 2 + 1] = L;
+    }
+}
+
 // Merge the split partials: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
 // One block per (head, sequence): the split weights are computed once into
 // LDS, then every thread reduces one channel over the splits (coalesced).
@@ -257,53 +528,67 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
     __syncthreads();
     L = red[0] + red[1] + red[2] + red[3];
     const float inv = L > 0.f ? 1.0f / L : 0.0f;
-    for (int c = threadIdx.x; c < hd; c += 256) {
-        float acc = 0.f;
-        for (int s = 0; s < splits; ++s) {
-            const float w = sw[s];
-            if (w != 0.f) acc += w * o_part[((base + s) * G + g) * hd + c];
+    // thread (part, channel): the splits part, part + np, ... of one channel, COMB_U loads in
+    // flight at a time (an empty split's o is never written: it is selected away, not multiplied)
+    constexpr int COMB_U = 8;
+    __shared__ float cred[256];
+    const int np = hd <= 256 ? 256 / hd : 1;
+    const int c = threadIdx.x % hd, pt = threadIdx.x / hd;
+    float acc = 0.f;
+    if (pt < np && c < hd) {
+        for (int s0 = pt; s0 < splits; s0 += COMB_U * np) {
+            float ov[COMB_U], wv[COMB_U];
+#pragma unroll
+            for (int u = 0; u < COMB_U; ++u) {
+                const int s = s0 + u * np;
+                wv[u] = s < splits ? sw[s] : 0.f;
+                ov[u] = s < splits ? o_part[((base + s) * G + g) * hd + c] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < COMB_U; ++u) acc += wv[u] != 0.f ? wv[u] * ov[u] : 0.f;
         }
-        out[((size_t)seq * H + h) * hd + c] = acc * inv;
+    }
+    cred[threadIdx.x] = acc;
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < hd; cc += 256) {
+        float v = 0.f;
+        for (int q = 0; q < np; ++q) v += cred[q * hd + cc];
+        out[((size_t)seq * H + h) * hd + cc] = v * inv;
     }
 }
 
-static int pick_chunk(int len, int blocks_other) {
+// the MFMA decode kernel (head_dim 64 / 128) unless GH_ATTN_DEC_OLD is set
+static bool dec_v2() {
+    static const bool v2 = getenv("GH_ATTN_DEC_OLD") == nullptr;
+    return v2;
+}
+
+static int pick_chunk(int len, int blocks_other, int cap = DEC_CHUNK_MAX) {
     // enough blocks to fill the chip, runs of 64..512 positions
     const int target = 2 * num_cus();
     int per = cdiv(target, blocks_other > 0 ? blocks_other : 1);
     int chunk = cdiv(len > 0 ? len : 1, per > 0 ? per : 1);
     chunk = (chunk + 63) / 64 * 64;
     if (chunk < 128) chunk = 128;
-    if (chunk > DEC_CHUNK_MAX) chunk = DEC_CHUNK_MAX;
+    if (chunk > cap) chunk = cap;
     return chunk;
 }
 
-// Split-K partials only (no merge): the merge is left to the consumer
-// (the fused output projection merges them in its prologue).
-template <bool PAGED>
-static int launch_decode_partials(DecodeArgs& a, int hd, int S, int span) {
-    a.chunk = pick_chunk(span, a.KV * S);
-    a.splits = cdiv(span > 0 ? span : 1, a.chunk);
-    float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
-    float* ml = (float*)workspace(WS_ATTN_ML, (size_t)S * a.KV * a.splits * a.G * 2 * 4);
-    if (!o || !ml) return fail(GH_ENOMEM, "attention decode: workspace");
-    a.o_part = o;
-    a.ml_part = ml;
-    const dim3 grid(a.splits, a.KV, S);
-    switch (hd) {
-        case 16: hipLaunchKernelGGL((k_attn_decode<16, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        case 32: hipLaunchKernelGGL((k_attn_decode<32, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        case 64: hipLaunchKernelGGL((k_attn_decode<64, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        case 128: hipLaunchKernelGGL((k_attn_decode<128, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        default: return fail(GH_EUNSUPPORTED, "attention decode: head_dim %d (supported: 16, 32, 64, 128)", hd);
-    }
-    GH_LAUNCHED("k_attn_decode");
-    return GH_OK;
+template <int HD, bool PAGED>
+static void launch_dec2(const DecodeArgs& a, dim3 grid) {
+    if (a.G <= 4) hipLaunchKernelGGL((k_attn_decode2<HD, PAGED, 4>), grid, dim3(256), 0, stream(), a);
+    else hipLaunchKernelGGL((k_attn_decode2<HD, PAGED, 8>), grid, dim3(256), 0, stream(), a);
 }
 
+// Split-K decode. out == null: partials only, the merge is left to the
+// consumer (the fused output projection merges them in its prologue);
+// otherwise k_attn_combine merges them into out. (A merge by the last block
+// of each kv head was slower: the device-scope fence every block then needs
+// writes back L2.)
 template <bool PAGED>
 static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
-    a.chunk = pick_chunk(span, a.KV * S);
+    const bool v2 = dec_v2() && (hd == 64 || hd == 128) && a.G <= 8;
+    a.chunk = pick_chunk(span, a.KV * S, v2 ? DEC2_CHUNK_MAX : DEC_CHUNK_MAX);
     a.splits = cdiv(span > 0 ? span : 1, a.chunk);
     float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
     float* ml = (float*)workspace(WS_ATTN_ML, (size_t)S * a.KV * a.splits * a.G * 2 * 4);
@@ -314,15 +599,26 @@ static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
     switch (hd) {
         case 16: hipLaunchKernelGGL((k_attn_decode<16, PAGED>), grid, dim3(256), 0, stream(), a); break;
         case 32: hipLaunchKernelGGL((k_attn_decode<32, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        case 64: hipLaunchKernelGGL((k_attn_decode<64, PAGED>), grid, dim3(256), 0, stream(), a); break;
-        case 128: hipLaunchKernelGGL((k_attn_decode<128, PAGED>), grid, dim3(256), 0, stream(), a); break;
+        case 64:
+            if (v2) launch_dec2<64, PAGED>(a, grid);
+            else hipLaunchKernelGGL((k_attn_decode<64, PAGED>), grid, dim3(256), 0, stream(), a);
+            break;
+        case 128:
+            if (v2) launch_dec2<128, PAGED>(a, grid);
+            else hipLaunchKernelGGL((k_attn_decode<128, PAGED>), grid, dim3(256), 0, stream(), a);
+            break;
         default: return fail(GH_EUNSUPPORTED, "attention decode: head_dim %d (supported: 16, 32, 64, 128)", hd);
     }
     GH_LAUNCHED("k_attn_decode");
+    if (!out) return GH_OK;
     if (a.splits > COMB_MAX_SPLITS) return fail(GH_EUNSUPPORTED, "attention decode: %d splits", a.splits);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.H, S), dim3(256), 0, stream(), o, ml, out, a.H, a.KV, a.G, a.splits, hd);
     GH_LAUNCHED("k_attn_combine");
     return GH_OK;
+}
+template <bool PAGED>
+static int launch_decode_partials(DecodeArgs& a, int hd, int S, int span) {
+    return launch_decode<PAGED>(a, hd, S, span, nullptr);
 }
 
 // ============================================================== prefill

@@ -43,6 +43,7 @@
 #include <stdlib.h>
 
 #include "gemv_fuse.h"
+#include "lds_dma.h"
 
 namespace gh {
 
@@ -642,7 +643,7 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
 // global_load_lds_dwordx4 (SGPR base + per-lane offset) from inline assembly
 // with explicit in-order vmcnt waits: the compiler's own tracking of LDS DMA
 // would drain every transfer before each LDS read, and __syncthreads would
-// drain them too (gd_barrier waits for LDS only). Waves do not synchronise
+// drain them too (lds_barrier waits for LDS only). Waves do not synchronise
 // per tile: every lane leaves its partial sum in LDS, and after each group
 // of GD_S tiles (one barrier) the block adds the partials of the group and
 // stores its rows of y; groups alternate between two LDS areas, so the next
@@ -658,22 +659,6 @@ struct GdCfg {
     static constexpr int PPL = (NP + 63) / 64;  // transfers per wave and tile (the last one partial)
 };
 
-// 16 bytes per lane from base + voff into LDS at lds_base + 16 * lane
-__device__ __forceinline__ void gd_dma16s(const void* base, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory");
-}
-__device__ __forceinline__ uint32_t gd_lds_addr(const void* p) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
-}
-__device__ __forceinline__ void gd_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-// wait until at most `ahead` tiles of PPL transfers are outstanding (vmcnt takes an immediate)
-template <int PPL>
-__device__ __forceinline__ void gd_wait(int ahead) {
-    if (ahead >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PPL) : "memory");
-    else if (ahead == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PPL) : "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PPL) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
 __device__ __forceinline__ gd_i4 gd_lo_codes(uint4 u) {
     return gd_i4{(int)(u.x & 0x0F0F0F0Fu), (int)(u.y & 0x0F0F0F0Fu), (int)(u.z & 0x0F0F0F0Fu), (int)(u.w & 0x0F0F0F0Fu)};
 }
@@ -713,7 +698,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     // x: piece tid + j * blockDim.x (contiguous per wave instruction)
 #pragma unroll
     for (int j = 0; j < SBW; ++j)
-        gd_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, gd_lds_addr(&sx[wave * 64 + j * blockDim.x]));
+        lds_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, lds_addr(&sx[wave * 64 + j * blockDim.x]));
     // column `wave` of a tile -> ring slice; piece q = PR r + j of row r
     uint32_t voff[PPL];
 #pragma unroll
@@ -727,14 +712,14 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         if (tile * 16 + 16 <= N) {
 #pragma unroll
             for (int i = 0; i < PPL; ++i)
-                if (NP % 64 == 0 || i + 1 < PPL || lane + 64 * i < NP) gd_dma16s(base, voff[i], gd_lds_addr(dst + 64 * i));
+                if (NP % 64 == 0 || i + 1 < PPL || lane + 64 * i < NP) lds_dma16s(base, voff[i], lds_addr(dst + 64 * i));
         } else {  // ragged last tile: rows past N re-read row N-1
 #pragma unroll
             for (int i = 0; i < PPL; ++i) {
                 const int q = lane + 64 * i;
                 if (q < NP) {
                     const int r = q / PR, j = q - r * PR, rc = tile * 16 + r < N ? r : N - 1 - tile * 16;
-                    gd_dma16s(base, (uint32_t)(rc * rowb) + wave * (144 * SBW) + 16 * j, gd_lds_addr(dst + 64 * i));
+                    lds_dma16s(base, (uint32_t)(rc * rowb) + wave * (144 * SBW) + 16 * j, lds_addr(dst + 64 * i));
                 }
             }
         }
@@ -744,8 +729,8 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     // ring are requested after the conversion of x (the ring is always filled, so every wait is exact)
     dma(t0 < ntiles ? t0 : ntiles - 1, 0);
     // ---- x -> three int8 parts per value; scale, x sum and part sums per 32 values (8 threads each)
-    gd_wait<PPL>(1);  // x landed (the first tile in flight)
-    gd_barrier();
+    lds_dma_wait<PPL>(1);  // x landed (the first tile in flight)
+    lds_barrier();
 #pragma unroll
     for (int jj = 0; jj < SBW; ++jj) {
         const int idx = tid + jj * blockDim.x;
@@ -789,7 +774,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     // the rest of the ring (a missing tile re-reads the last one)
 #pragma unroll
     for (int b = 1; b < NB; ++b) dma(t0 + b * G < ntiles ? t0 + b * G : ntiles - 1, b);
-    gd_barrier();
+    lds_barrier();
     // A operands of this wave's super-blocks (rows m = 4g + e of group g), scales, high-nibble offsets
     gd_i4 A[SBW][2][2], hinit[SBW];
     float s_lo[SBW], s_hi[SBW], xs_lo[SBW], xs_hi[SBW];
@@ -823,7 +808,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         int ahead = 0;
 #pragma unroll
         for (int j = 1; j < NB; ++j) ahead += (it + j < NB || tile + j * G < ntiles) ? 1 : 0;
-        gd_wait<PPL>(ahead);
+        lds_dma_wait<PPL>(ahead);
         const unsigned char* rowp = (const unsigned char*)(ring + ((size_t)b * WB + wave) * NP) + n16 * (144 * SBW);
         uint4 hd[SBW], qa[SBW], qb[SBW];
 #pragma unroll
@@ -864,7 +849,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         float4* red = sred + (size_t)(grp * GD_S + slot) * WB * 16;
         ((float*)&red[wave * 16 + n16])[g] = acc;
         if (slot == GD_S - 1 || tile + G >= ntiles) {
-            gd_barrier();
+            lds_barrier();
             // thread (output o, wave w = tid % 16) adds w's four lane groups; 16 lanes add the waves
             const int w = tid & 15;
             for (int o = tid >> 4; o < 16 * (slot + 1); o += blockDim.x >> 4) {  // uniform per 16 lanes
