@@ -182,7 +182,7 @@ def kernel_suite(gh):
         o = gh.Buf.zeros(Hq * hd, np.float32)
         ms = time_launches(gh, lambda: gh.call("gh_attention_decode_ring_fp16", q.p, kc.p, vc.p, o.p, Hq, KVh, hd, 0,
                                                8, L, L, gh.fl(0.0884), None, 0), 100)
-        res[f"c4_decode_L{L}"] = entry("k_attn_decode+k_attn_combine", ms, bytes_=L * KVh * hd * 2 * 2 + 2 * Hq * hd * 4,
+        res[f"c4_decode_L{L}"] = entry("k_attn_decode2+k_attn_combine", ms, bytes_=L * KVh * hd * 2 * 2 + 2 * Hq * hd * 4,
                                        flops=4.0 * Hq * hd * L)
         del kc, vc
     ps = 64
@@ -201,7 +201,7 @@ def kernel_suite(gh):
     ob = gh.Buf.zeros(16 * Hq * hd, np.float32)
     ms = time_launches(gh, lambda: gh.call("gh_attention_decode_paged_bf16", qb.p, kp.p, vp.p, dpt.p, dl.p, 16,
                                            max_pages, ps, int(lens.max()), ob.p, Hq, KVh, hd, gh.fl(0.0884)), 50)
-    res["c4_ragged_decode_b16"] = entry("k_attn_decode<paged>+k_attn_combine", ms,
+    res["c4_ragged_decode_b16"] = entry("k_attn_decode2<paged>+k_attn_combine", ms,
                                         bytes_=int(lens.sum()) * KVh * hd * 2 * 2, flops=4.0 * Hq * hd * int(lens.sum()))
     del kp, vp
     Tp = 4096
