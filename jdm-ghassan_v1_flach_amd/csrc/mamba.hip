@@ -81,63 +81,84 @@ __global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in
     }
 }
 
-// G[c][t][tau] = C_t . B_tau inside chunk c (fp32, 64x64 tiles).
+// G[c][t][tau] = C_t . B_tau inside chunk c: 64x64 tiles, 4 waves x 32x32 on
+// the matrix cores (fp16 operands, fp32 accumulation; G only enters the
+// scan as an fp16 operand). C and B rows are staged into LDS with 16-byte loads.
+template <int N>
 __global__ void __launch_bounds__(256) k_ssd_cb(const float* __restrict__ Bm, const float* __restrict__ Cm, int ld,
-                                                float* __restrict__ G, int T, int N, int L) {
-    __shared__ float sC[64][33], sB[64][33];
+                                                float* __restrict__ G, int T, int L) {
+    constexpr int SN = N + 8;
+    __shared__ __attribute__((aligned(16))) _Float16 sC[64 * SN], sB[64 * SN];
     const int c = blockIdx.z, ti = blockIdx.y * 64, si = blockIdx.x * 64;
-    const int t0 = c * L;
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    float acc[4][4] = {};
-    for (int n0 = 0; n0 < N; n0 += 32) {
-        for (int e = threadIdx.x; e < 64 * 32; e += 256) {
-            const int r = e >> 5, k = e & 31;
-            const int tr = t0 + ti + r, sr = t0 + si + r;
-            sC[r][k] = (ti + r < L && tr < T) ? Cm[(size_t)tr * ld + n0 + k] : 0.f;
-            sB[r][k] = (si + r < L && sr < T) ? Bm[(size_t)sr * ld + n0 + k] : 0.f;
-        }
-        __syncthreads();
-        for (int k = 0; k < 32; ++k)
+    const int t0 = c * L, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int e = threadIdx.x; e < 64 * N / 4; e += 256) {
+        const int r = (4 * e) / N, k = (4 * e) % N;
+        const int tr = t0 + ti + r, sr = t0 + si + r;
+        const float4 cv = (ti + r < L && tr < T) ? *(const float4*)(Cm + (size_t)tr * ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bv = (si + r < L && sr < T) ? *(const float4*)(Bm + (size_t)sr * ld + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        f16x4 hc, hb;
+        hc[0] = (_Float16)cv.x; hc[1] = (_Float16)cv.y; hc[2] = (_Float16)cv.z; hc[3] = (_Float16)cv.w;
+        hb[0] = (_Float16)bv.x; hb[1] = (_Float16)bv.y; hb[2] = (_Float16)bv.z; hb[3] = (_Float16)bv.w;
+        *(f16x4*)(sC + r * SN + k) = hc;
+        *(f16x4*)(sB + r * SN + k) = hb;
+    }
+    __syncthreads();
+    const int wt = (wave >> 1) * 32, ws = (wave & 1) * 32;
+    f32x16 acc;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(sC[ty * 4 + i][k], sB[tx * 4 + j][k], acc[i][j]);
-        __syncthreads();
+    for (int ks = 0; ks < N / 16; ++ks) {
+        const int ko = ks * 16 + 8 * (lane >> 5);
+        const f16x8 a = *(const f16x8*)(sC + (wt + (lane & 31)) * SN + ko);
+        const f16x8 b = *(const f16x8*)(sB + (ws + (lane & 31)) * SN + ko);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int t = ti + ty * 4 + i, s = si + tx * 4 + j;
-            if (t < L && s < L) G[((size_t)c * L + t) * L + s] = acc[i][j];
-        }
+    for (int e = 0; e < 16; ++e) {
+        const int t = ti + wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), sc = si + ws + (lane & 31);
+        if (t < L && sc < L) G[((size_t)c * L + t) * L + sc] = acc[e];
+    }
 }
 
 // dS[c][h][p][n] = sum_tau e^(cum_end - cum_tau) dt_tau x_tau[p] B_tau[n]
 // (P = 64 rows, N cols in 32-wide MFMA tiles), fp16 operands, fp32 acc.
-// Stages a [64 rows][W] fp32 tile (row stride ld, rows >= nvalid read as
-// 0, optionally scaled per row by sw) into LDS as fp16 TRANSPOSED [W][S]:
-// thread = (column c, group of 64*W/256 consecutive rows); the global loads
-// coalesce across columns and each thread writes its rows as 16-byte pieces.
+// Stages a [64 rows][W] fp32 tile (row stride ld, a multiple of 4; rows >=
+// nvalid read as 0, optionally scaled per row by sw) into LDS as fp16
+// TRANSPOSED [W][S]: thread = (4 columns, a run of R = W / 16 consecutive
+// rows); each row piece is one 16-byte load (the 64 lanes of a wave cover
+// whole rows), and each of the thread's 4 columns is written as one run of R
+// halves.
 template <int W, int S, bool SCALE>
 __device__ __forceinline__ void stage_t64(const float* __restrict__ src, int ld, int nvalid, const float* sw,
                                           _Float16* dst) {
-    constexpr int G = 256 / W, R = 64 / G;
-    const int c = threadIdx.x % W, g = threadIdx.x / W;
-    float v[R];
+    constexpr int Q = W / 4, G = 256 / Q, R = 64 / G;  // float4 per row, row groups, rows per thread
+    static_assert(R == 4 || R == 8, "stage_t64: W must be 64 or 128");
+    const int cq = threadIdx.x % Q, g = threadIdx.x / Q;
+    float4 v[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int r = g * R + i;
-        v[i] = r < nvalid ? src[(size_t)r * ld + c] : 0.f;
-        if (SCALE) v[i] *= sw[r];
+        v[i] = r < nvalid ? *(const float4*)(src + (size_t)r * ld + 4 * cq) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (SCALE) {
+            const float w = sw[r];
+            v[i].x *= w; v[i].y *= w; v[i].z *= w; v[i].w *= w;
+        }
     }
+    typedef _Float16 hrun __attribute__((ext_vector_type(R)));
+    hrun h0, h1, h2, h3;
 #pragma unroll
-    for (int j = 0; j < R / 8; ++j) {
-        f16x8 hv;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) hv[k] = (_Float16)v[8 * j + k];
-        *(f16x8*)(dst + c * S + g * R + 8 * j) = hv;
+    for (int i = 0; i < R; ++i) {
+        h0[i] = (_Float16)v[i].x;
+        h1[i] = (_Float16)v[i].y;
+        h2[i] = (_Float16)v[i].z;
+        h3[i] = (_Float16)v[i].w;
     }
+    _Float16* d = dst + (4 * cq) * S + g * R;
+    *(hrun*)d = h0;
+    *(hrun*)(d + S) = h1;
+    *(hrun*)(d + 2 * S) = h2;
+    *(hrun*)(d + 3 * S) = h3;
 }
 
 template <int N>
@@ -161,7 +182,11 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict
     for (int i = 0; i < TPW; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
-    for (int k0 = 0; k0 < len; k0 += TK) {
+    // the B rows of a chunk are the same for every head: head h starts at tile h mod ntk, so the
+    // blocks of one chunk do not all read the same lines at once (that serialises them)
+    const int ntk = (len + TK - 1) / TK;
+    for (int kk = 0; kk < ntk; ++kk) {
+        const int k0 = ((kk + h) % ntk) * TK;
         __syncthreads();
         if (threadIdx.x < TK) {
             const int tau = k0 + threadIdx.x;
@@ -210,9 +235,23 @@ __global__ void k_ssd_state_pass(float* __restrict__ state, const float* __restr
     if (i >= (int64_t)H * PN) return;
     const int h = (int)(i / PN);
     float s = state[i];
-    for (int c = 0; c < nchunks; ++c) {
-        Sin[(size_t)c * H * PN + i] = s;
-        s = s * decay[(size_t)c * H + h] + dS[(size_t)c * H * PN + i];
+    // the loads of 8 chunks go out together; only the recurrence is serial
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+        float dv[8], dc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j;
+            dv[j] = c < nchunks ? dS[(size_t)c * H * PN + i] : 0.f;
+            dc[j] = c < nchunks ? decay[(size_t)c * H + h] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j;
+            if (c < nchunks) {
+                Sin[(size_t)c * H * PN + i] = s;
+                s = s * dc[j] + dv[j];
+            }
+        }
     }
     state[i] = s;
 }
@@ -220,7 +259,12 @@ __global__ void k_ssd_state_pass(float* __restrict__ state, const float* __restr
 // Chunk outputs: y[t][p] = sum_{tau<=t} G[t][tau] e^(cum_t-cum_tau) dt_tau x_tau[p]
 //                 + e^(cum_t) sum_n C_t[n] S_in[p][n] + D x_t[p].
 // Block = (chunk, head, 64-row t tile): 4 waves x (32 t rows x 32 p cols),
-// MFMA 32x32x16 with fp16 operands and fp32 accumulation.
+// MFMA 32x32x16 with fp16 operands and fp32 accumulation. Every operand goes
+// through LDS with coalesced 16-byte loads: the C rows (pre-scaled by
+// e^(cum_t)) with S_in for the inter-chunk term, then per 64-wide tau tile the
+// decay-masked A = G e^(cum_t-cum_tau) dt_tau (fp16) with X^T. G and C are the
+// same for every head, so head h walks the tau tiles from tile h mod ntk (the
+// blocks of one chunk then do not all read the same lines at once).
 template <int N>
 __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__ xs, int ldx,
                                                        const float* __restrict__ Cm, int ldc,
@@ -229,72 +273,84 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
                                                        const float* __restrict__ D, float* __restrict__ y, int ldy,
                                                        int T, int H, int L) {
     constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
-    __shared__ __attribute__((aligned(16))) _Float16 sXt[P * S];   // [p][tau]
-    __shared__ __attribute__((aligned(16))) _Float16 sS[P * SN];   // [p][n]  (S_in)
-    __shared__ float scum[TK], sdt[TK];
+    // phase 1 (inter-chunk term): sC [t][n] and sS [p][n]; phase 2: sA [t][tau] and sXt [p][tau]
+    constexpr int U1 = (64 * SN + P * SN) * 2, U2 = (64 * S + P * S) * 2;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[U1 > U2 ? U1 : U2];
+    _Float16* sC = (_Float16*)smem;
+    _Float16* sS = sC + 64 * SN;
+    _Float16* sA = (_Float16*)smem;
+    _Float16* sXt = sA + 64 * S;
+    __shared__ float scum[TK], sdt[TK], srow[64];
     const int c = blockIdx.x, h = blockIdx.y, tt = blockIdx.z * 64;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = c * L, len = min(L, T - t0);
     if (tt >= len) return;
     const int wt = (wave >> 1) * 32, wp = (wave & 1) * 32;  // wave tile: t rows tt+wt.., p cols wp..
-    const int trow = tt + wt + (lane & 31);                  // A-operand row of this lane
-    const bool trow_ok = trow < len;
-    const float cum_t = trow_ok ? cum[(size_t)(t0 + trow) * H + h] : 0.f;
-    const float cum_t2 = cum_t * 1.4426950408889634f;
+    const int ar = wt + (lane & 31);                          // A-operand row (local) of this lane
+    if (tid < 64) srow[tid] = tt + tid < len ? cum[(size_t)(t0 + tt + tid) * H + h] * 1.4426950408889634f : 0.f;
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 
-    // ---- inter-chunk term: e^(cum_t) C_t S_in^T
+    // ---- inter-chunk term: (e^(cum_t) C_t) S_in^T
     const float* Sc = Sin + ((size_t)c * H + h) * P * N;
-    for (int e = threadIdx.x; e < P * N / 4; e += 256) {
-        const float4 v = ((const float4*)Sc)[e];
+    __syncthreads();
+    for (int e = tid; e < 64 * N / 4; e += 256) {
         const int r = (4 * e) / N, cc = (4 * e) % N;
+        const bool ok = tt + r < len;
+        const float4 v = ok ? *(const float4*)(Cm + (size_t)(t0 + tt + r) * ldc + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float sc = ok ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
         f16x4 hv;
-        hv[0] = (_Float16)v.x; hv[1] = (_Float16)v.y; hv[2] = (_Float16)v.z; hv[3] = (_Float16)v.w;
-        *(f16x4*)(sS + r * SN + cc) = hv;
+        hv[0] = (_Float16)(v.x * sc); hv[1] = (_Float16)(v.y * sc); hv[2] = (_Float16)(v.z * sc); hv[3] = (_Float16)(v.w * sc);
+        *(f16x4*)(sC + r * SN + cc) = hv;
+        const float4 w = ((const float4*)Sc)[e];  // P * N / 4 == 64 * N / 4
+        f16x4 hw;
+        hw[0] = (_Float16)w.x; hw[1] = (_Float16)w.y; hw[2] = (_Float16)w.z; hw[3] = (_Float16)w.w;
+        *(f16x4*)(sS + r * SN + cc) = hw;
     }
     __syncthreads();
-    {
-        const float sc = trow_ok ? expf(cum_t) : 0.f;
-        const float* crow = Cm + (size_t)(t0 + (trow_ok ? trow : 0)) * ldc;
-#pragma unroll 4
-        for (int ks = 0; ks < N / 16; ++ks) {
-            const int ko = ks * 16 + 8 * (lane >> 5);
-            f16x8 a;
-            const float4 c0 = *(const float4*)(crow + ko), c1 = *(const float4*)(crow + ko + 4);
-            a[0] = (_Float16)(c0.x * sc); a[1] = (_Float16)(c0.y * sc); a[2] = (_Float16)(c0.z * sc); a[3] = (_Float16)(c0.w * sc);
-            a[4] = (_Float16)(c1.x * sc); a[5] = (_Float16)(c1.y * sc); a[6] = (_Float16)(c1.z * sc); a[7] = (_Float16)(c1.w * sc);
-            const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
-        }
+#pragma unroll
+    for (int ks = 0; ks < N / 16; ++ks) {
+        const int ko = ks * 16 + 8 * (lane >> 5);
+        const f16x8 a = *(const f16x8*)(sC + ar * SN + ko);
+        const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
     }
     // ---- intra-chunk term over tau tiles up to the last row of this block
     const int kend = min(len, tt + 64);
-    for (int k0 = 0; k0 < kend; k0 += TK) {
-        __syncthreads();
-        if (threadIdx.x < TK) {
-            const int tau = k0 + threadIdx.x;
-            scum[threadIdx.x] = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
-            sdt[threadIdx.x] = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
+    const int ntk = (kend + TK - 1) / TK;
+    for (int kk = 0; kk < ntk; ++kk) {
+        const int k0 = ((kk + h) % ntk) * TK;
+        __syncthreads();  // previous tile (or the inter-chunk operands) consumed
+        if (tid < TK) {
+            const int tau = k0 + tid;
+            scum[tid] = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
+            sdt[tid] = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
         }
         stage_t64<P, S, false>(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0, nullptr, sXt);
         __syncthreads();
+        // A[t][tau] = G e^(cum_t - cum_tau) dt_tau for tau <= t (both inside the chunk), fp16
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = tid + 256 * j, r = e >> 4, q = (e & 15) * 4;
+            const int t = tt + r;
+            const float4 g4 = t < len ? *(const float4*)(G + ((size_t)c * L + t) * L + k0 + q) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+            f16x4 hv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tau = k0 + q + i;
+                const bool vis = t < len && tau <= t && tau < len;
+                hv[i] = (_Float16)(vis ? gv[i] * __builtin_amdgcn_exp2f(srow[r] - scum[q + i]) * sdt[q + i] : 0.f);
+            }
+            *(f16x4*)(sA + r * S + q) = hv;
+        }
+        __syncthreads();
         if (k0 > tt + wt + 31) continue;  // wave-uniform: tile entirely in this wave's future
-        const float* grow = G + ((size_t)c * L + (trow_ok ? trow : 0)) * L + k0;
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ++ks) {
             const int ko = ks * 16 + 8 * (lane >> 5);
-            f16x8 a;
-            const float4 g0 = *(const float4*)(grow + ko), g1 = *(const float4*)(grow + ko + 4);
-            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int tau = k0 + ko + i;
-                const bool vis = trow_ok && tau <= trow && tau < len;
-                const float m = vis ? gv[i] * __builtin_amdgcn_exp2f(cum_t2 - scum[ko + i]) * sdt[ko + i] : 0.f;
-                a[i] = (_Float16)m;
-            }
+            const f16x8 a = *(const f16x8*)(sA + ar * S + ko);
             const f16x8 b = *(const f16x8*)(sXt + (wp + (lane & 31)) * S + ko);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
         }
@@ -334,7 +390,8 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     float* decay = Sin + f_S;
     hipLaunchKernelGGL(k_ssd_prep, dim3(nch, H), dim3(64), 0, stream(), dt_raw, dt_ld, dt_bias, A, a_log, dt, cum, T,
                        H, L);
-    hipLaunchKernelGGL(k_ssd_cb, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, N, L);
+    if (N == 128) hipLaunchKernelGGL(k_ssd_cb<128>, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, L);
+    else hipLaunchKernelGGL(k_ssd_cb<64>, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, L);
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_chunk_state<128>, dim3(nch, H), dim3(256), 0, stream(), xs, ldx, Bm, ldbc, dt, cum, dS,
                            decay, T, H, L);
