@@ -28,8 +28,9 @@ namespace gh {
 // when they fit; the lane sums run on across windows, still in order).
 // Softmax + top-k of one token's logits sp[0..ne) (LDS, overwritten with
 // the exponentials), run by the 64 lanes of one wave (see k_route).
-__device__ void route_finish(float* sp, const float* __restrict__ bias, int ne, int K, int t,
-                             int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs) {
+__device__ __forceinline__ void route_finish(float* sp, const float* __restrict__ bias, int ne, int K, int t,
+                             int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs,
+                             int* sel_lds = nullptr) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     float mx = sp[0];
@@ -81,29 +82,29 @@ __device__ void route_finish(float* sp, const float* __restrict__ bias, int ne, 
             for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
         }
         for (int k = 0; k < K; ++k) {
-            idx[(size_t)t * K + k] = sel_idx[k];
-            wout[(size_t)t * K + k] = wv[k];
+            if (idx) idx[(size_t)t * K + k] = sel_idx[k];
+            if (wout) wout[(size_t)t * K + k] = wv[k];
+            if (sel_lds) sel_lds[k] = sel_idx[k];
         }
     }
     if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
 }
 
 constexpr int ROUTE_RB = 8;  // float4 weight loads per thread per batch
-// With `nw` set, the token is first RMS-normalised (elementwise.hip
-// k_rmsnorm arithmetic) and the normalised row is also written to xn.
-__global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, const float* __restrict__ rw,
-                                               const float* __restrict__ bias, float* __restrict__ probs,
-                                               int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
-                                               int K, const float* __restrict__ nw, float eps,
-                                               float* __restrict__ xn, int GW) {
+// Routing of token t by a block of 256 threads. With `nw` set, the token is
+// first RMS-normalised (elementwise.hip k_rmsnorm arithmetic); the
+// (normalised) row stays in sx [d] (LDS) and is also written to xn when
+// given. term: LDS [ne][GW + 1]. sel_lds (LDS [K], optional) receives the
+// selected experts; idx / wout / probs (global) may be null.
+__device__ __forceinline__ void route_token(const float* __restrict__ x, const float* __restrict__ rw, const float* __restrict__ bias,
+                            float* __restrict__ probs, int32_t* __restrict__ idx, float* __restrict__ wout, int d,
+                            int ne, int K, const float* __restrict__ nw, float eps, float* __restrict__ xn, int GW,
+                            int t, float* sx, float* term, int* sel_lds) {
 #pragma clang fp contract(off)
-    extern __shared__ float route_sm[];
-    float* sx = route_sm;
-    float* term = route_sm + d;
     const int ngroups = d / 4, ts = GW + 1;
     __shared__ float sp[64];
     __shared__ double dred[4];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const float4* xt = (const float4*)(x + (size_t)t * d);
     const float4* rw4 = (const float4*)rw;
     auto widx = [&](int q, int g0, int gw) {  // pair q of a window -> float4 index in rw
@@ -137,7 +138,7 @@ __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, cons
         for (int i = tid; i < d; i += 256) {
             const float v = sx[i] * inv * nw[i];
             sx[i] = v;
-            xn[(size_t)t * d + i] = v;
+            if (xn) xn[(size_t)t * d + i] = v;
         }
     }
     __syncthreads();
@@ -182,7 +183,17 @@ __global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, cons
     }
     if (tid < ne) sp[tid] = s;
     __syncthreads();
-    if (tid < 64) route_finish(sp, bias, ne, K, t, idx, wout, probs);
+    if (tid < 64) route_finish(sp, bias, ne, K, t, idx, wout, probs, sel_lds);
+    __syncthreads();  // sel_lds, sx visible to the block
+}
+
+__global__ void __launch_bounds__(256) k_route(const float* __restrict__ x, const float* __restrict__ rw,
+                                               const float* __restrict__ bias, float* __restrict__ probs,
+                                               int32_t* __restrict__ idx, float* __restrict__ wout, int d, int ne,
+                                               int K, const float* __restrict__ nw, float eps,
+                                               float* __restrict__ xn, int GW) {
+    extern __shared__ float route_sm[];
+    route_token(x, rw, bias, probs, idx, wout, d, ne, K, nw, eps, xn, GW, blockIdx.x, route_sm, route_sm + d, nullptr);
 }
 
 // window of router groups whose terms fit 60 KB of LDS next to the token;
@@ -440,12 +451,24 @@ struct GemvJobs {
     float* out_r;            // [S][rows_r]
     float* out_s;            // [N][rows_s]
     const float* in_s;       // shared input (down: shared act)
+    // routing in the gate/up kernel itself (k_moe_gemv<.., true>): the raw token rows, the
+    // router and its norm; idx / w are written by the first block of each token
+    const float* rx;
+    const float* rw;
+    const float* rbias;
+    const float* rnw;
+    float reps;
+    int ne, gw;
+    int32_t* ridx;
+    float* rwout;
 };
 
-template <int KIND, bool DUAL>
+template <int KIND, bool DUAL, bool ROUTE = false>
 __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     const int job = blockIdx.y;
     const bool shared = job >= J.S;
+    extern __shared__ float msm[];  // ROUTE: token row [d] | router terms
+    __shared__ int ssel[8];
     const int rows = shared ? J.rows_s : J.rows_r;
     const int kin = shared ? J.kin_s : J.kin_r;
     const size_t rowb = shared ? J.rowb_s : J.rowb_r;
@@ -453,6 +476,15 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     int LPR = 64;
     while (LPR > 1 && LPR > T) LPR >>= 1;
     const int RP = 64 / LPR;
+    if (ROUTE) {
+        if (blockIdx.x * 4 * RP >= rows) return;  // no rows here (block 0, the writer, always has some)
+        // every block routes its token (identical arithmetic, so all agree); the normalised row
+        // stays in LDS as the GEMV input
+        const int token = shared ? job - J.S : job / J.K;
+        const bool writer = !shared && blockIdx.x == 0 && job % J.K == 0;
+        route_token(J.rx, J.rw, J.rbias, nullptr, writer ? J.ridx : nullptr, writer ? J.rwout : nullptr, J.d, J.ne,
+                    J.K, J.rnw, J.reps, nullptr, J.gw, token, msm, msm + J.d, ssel);
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, rp = lane / LPR;
     const int row = (blockIdx.x * 4 + wave) * RP + rp;
@@ -462,12 +494,12 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     const uint8_t *Wa, *Wb = nullptr;
     if (shared) {
         const int t = job - J.S;
-        xin = (DUAL ? J.x + (size_t)t * J.d : J.in_s + (size_t)t * kin);
+        xin = ROUTE ? msm : (DUAL ? J.x + (size_t)t * J.d : J.in_s + (size_t)t * kin);
         Wa = J.sa;
         if (DUAL) Wb = J.sb;
     } else {
-        const int e = J.idx[job];
-        xin = DUAL ? J.x + (size_t)(job / J.K) * J.d : J.x + (size_t)job * kin;
+        const int e = ROUTE ? ssel[job % J.K] : J.idx[job];
+        xin = ROUTE ? msm : (DUAL ? J.x + (size_t)(job / J.K) * J.d : J.x + (size_t)job * kin);
         Wa = J.wa + (size_t)e * J.estride;
         if (DUAL) Wb = J.wb + (size_t)e * J.estride;
     }
@@ -1051,7 +1083,11 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     if (!r || !xn || !act || !sh_act) return fail(GH_ENOMEM, "moe: workspace");
     int32_t* idx = (int32_t*)r;
     float* w = (float*)(r + (size_t)S * 4);
-    {
+    // a small router runs inside the gate/up kernel (one launch less); a large one on its own
+    const int gw = route_window(d, ne, N);
+    const size_t rlds = route_lds(d, ne, N);
+    const bool fused_route = K <= 8 && gw >= d / 4 && rlds <= 32 * 1024 && (size_t)ne * d <= 16384;
+    if (!fused_route) {
         const int rc = launch_route(xres, rw, bias, nullptr, idx, w, N, d, ne, K, nw, eps, xn);
         if (rc) return rc;
     }
@@ -1067,8 +1103,14 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
         return 4 * (64 / LPR);
     };
     const int maxrows = has_sh ? (E > SH ? E : SH) : E;
-    hipLaunchKernelGGL((k_moe_gemv<KIND, true>), dim3(cdiv(maxrows, rows_per_block(d)), S + J.N), dim3(256), 0,
-                       stream(), J);
+    const dim3 g1(cdiv(maxrows, rows_per_block(d)), S + J.N);
+    if (fused_route) {
+        J.rx = xres; J.rw = rw; J.rbias = bias; J.rnw = nw; J.reps = eps; J.ne = ne; J.gw = gw;
+        J.ridx = idx; J.rwout = w;
+        hipLaunchKernelGGL((k_moe_gemv<KIND, true, true>), g1, dim3(256), rlds, stream(), J);
+    } else {
+        hipLaunchKernelGGL((k_moe_gemv<KIND, true>), g1, dim3(256), 0, stream(), J);
+    }
     GH_LAUNCHED("k_moe_gemv(gate/up)");
     GemvJobs D{};
     D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
