@@ -152,6 +152,55 @@ __device__ __forceinline__ void gm_kinv(int kk, int& r8, int& g, int& el) {
 }
 
 // ---------------------------------------------------------- fusion hooks
+// Cross-lane moves on the DPP path (no LDS round trip): quad_perm 0xB1 /
+// 0x4E = lane xor 1 / 2, row_ror 4 / 8 rotate inside a row of 16 lanes,
+// row_bcast 15 / 31 pass a row's last lane to the next row(s) given by the
+// row mask; lanes without a source read 0.
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float gm_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, RM, 0xF, false));
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ double gm_dpp(double v) {
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    const i2 p = __builtin_bit_cast(i2, v);
+    i2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, p.x, CTRL, RM, 0xF, false);
+    r.y = __builtin_amdgcn_update_dpp(0, p.y, CTRL, RM, 0xF, false);
+    return __builtin_bit_cast(double, r);
+}
+// Sum over a whole wave (every lane active); the total ends in lane 63.
+template <typename T>
+__device__ __forceinline__ T gm_wave_total(T v) {
+    v += gm_dpp<0xB1>(v);
+    v += gm_dpp<0x4E>(v);
+    v += gm_dpp<0x124>(v);
+    v += gm_dpp<0x128>(v);          // every lane: its row of 16
+    v += gm_dpp<0x142, 0xA>(v);     // rows 1, 3 += rows 0, 2
+    v += gm_dpp<0x143, 0xC>(v);     // rows 2, 3 += lane 31 (rows 0 + 1)
+    return v;
+}
+__device__ __forceinline__ double gm_lane63(double v) {
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    const i2 p = __builtin_bit_cast(i2, v);
+    i2 r;
+    r.x = __builtin_amdgcn_readlane(p.x, 63);
+    r.y = __builtin_amdgcn_readlane(p.y, 63);
+    return __builtin_bit_cast(double, r);
+}
+// Block-wide sum of a double over DPP and one LDS exchange (all threads get the total).
+__device__ __forceinline__ double gm_block_sum_dpp(double v, double* red) {
+    v = gm_lane63(gm_wave_total(v));
+    const int nw = blockDim.x >> 6;
+    if (nw == 1) return v;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
 // Block-wide sum of a double (all threads get the total).
 __device__ __forceinline__ double gm_block_sum(double v, double* red) {
 #pragma unroll
@@ -204,37 +253,42 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
     __shared__ double red[16];
     const int tid = threadIdx.x, nth = blockDim.x;
     if (f.pro == GM_PRO_RMSNORM || f.pro == GM_PRO_GATED) {
+        // elementwise.hip k_rmsnorm: double sum of squares, x * inv * w;
+        // mamba.hip k_gated_norm: v = y * silu(z), double variance, float rsqrt.
+        // Thread tid holds the 8 consecutive elements 8 tid .. 8 tid + 7 (further chunks of
+        // 8 nth go through xf), so a 32-value group sits in 4 lanes of a quad.
         const bool gated = f.pro == GM_PRO_GATED;
-        float xr[GM_PR], wr[GM_PR], zr[GM_PR];
-#pragma unroll
-        for (int j = 0; j < GM_PR; ++j) {
-            const int i = tid + j * nth;
-            if (i < K) {
-                xr[j] = x[i];
-                wr[j] = f.pw[i];
-                zr[j] = gated ? f.pz[i] : 0.f;
+        const int c0 = 8 * tid;
+        const bool mine = c0 < K;
+        float xr[8], wr[8], zr[8];
+        if (mine) {
+            const float4 x0 = *(const float4*)(x + c0), x1 = *(const float4*)(x + c0 + 4);
+            const float4 w0 = *(const float4*)(f.pw + c0), w1 = *(const float4*)(f.pw + c0 + 4);
+            xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w; xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
+            wr[0] = w0.x; wr[1] = w0.y; wr[2] = w0.z; wr[3] = w0.w; wr[4] = w1.x; wr[5] = w1.y; wr[6] = w1.z; wr[7] = w1.w;
+            if (gated) {
+                const float4 z0 = *(const float4*)(f.pz + c0), z1 = *(const float4*)(f.pz + c0 + 4);
+                zr[0] = z0.x; zr[1] = z0.y; zr[2] = z0.z; zr[3] = z0.w; zr[4] = z1.x; zr[5] = z1.y; zr[6] = z1.z; zr[7] = z1.w;
             }
         }
-        // elementwise.hip k_rmsnorm: double sum of squares, x * inv * w;
-        // mamba.hip k_gated_norm: v = y * silu(z), double variance, float rsqrt
         double ss = 0.0;
+        if (mine) {
 #pragma unroll
-        for (int j = 0; j < GM_PR; ++j) {
-            const int i = tid + j * nth;
-            if (i < K) {
+            for (int j = 0; j < 8; ++j) {
                 float v = xr[j];
                 if (gated) v = v * (zr[j] / (1.0f + expf(-zr[j])));
                 xr[j] = v;
                 ss += (double)v * v;
             }
         }
-        for (int i = tid + GM_PR * nth; i < K; i += nth) {  // elements beyond the registers
-            float v = x[i];
-            if (gated) v = v * (f.pz[i] / (1.0f + expf(-f.pz[i])));
-            xf[i] = v;
-            ss += (double)v * v;
-        }
-        const double tot = gm_block_sum(ss, red);
+        for (int c = c0 + 8 * nth; c < K; c += 8 * nth)  // chunks beyond the registers
+            for (int j = 0; j < 8; ++j) {
+                float v = x[c + j];
+                if (gated) v = v * (f.pz[c + j] / (1.0f + expf(-f.pz[c + j])));
+                xf[c + j] = v;
+                ss += (double)v * v;
+            }
+        const double tot = gm_block_sum_dpp(ss, red);
         float inv;
         if (gated) {
             inv = 1.0f / sqrtf((float)(tot / (double)K) + f.eps);
@@ -242,12 +296,23 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
             const double invd = 1.0 / sqrt(tot / (double)K + (double)f.eps);
             inv = isfinite(invd) ? (float)invd : 0.0f;
         }
+        // values into the A layout; the 32-value sums over the quad (every lane runs the DPP)
+        const int rounds = (K + 8 * nth - 1) / (8 * nth);  // the same for every lane
+        for (int m = 0; m < rounds; ++m) {
+            const int c = c0 + 8 * nth * m;
+            float sum = 0.f;
+            if (c < K) {
 #pragma unroll
-        for (int j = 0; j < GM_PR; ++j) {
-            const int i = tid + j * nth;
-            if (i < K) gm_put_one<KIND>(a16, xsum, i, xr[j] * inv * wr[j]);
+                for (int j = 0; j < 8; ++j) {
+                    const float v = (m == 0 ? xr[j] : xf[c + j]) * inv * (m == 0 ? wr[j] : f.pw[c + j]);
+                    gm_put_a<KIND>(a16, 1, 0, c + j, v);
+                    sum += v;
+                }
+            }
+            sum += gm_dpp<0xB1>(sum);
+            sum += gm_dpp<0x4E>(sum);
+            if (c < K && (tid & 3) == 0) xsum[c >> 5] = sum;
         }
-        for (int i = tid + GM_PR * nth; i < K; i += nth) gm_put_one<KIND>(a16, xsum, i, xf[i] * inv * f.pw[i]);
     } else {
         // attention.hip k_attn_combine for all H heads at once. Output
         // i = h*hd + c. (A) every (m, l) pair goes to LDS and every thread
@@ -263,17 +328,21 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
             sm[q] = p[0];
             sl[q] = p[1];
         }
-        float ov[GM_PR][GM_SPR];
+        // thread tid: the 8 consecutive elements 8 tid .. (one head), their first GM_SPR splits
+        // requested now; further chunks of 8 nth load their partials when merged
+        const int c0 = 8 * tid;
+        float ov[GM_SPR][8];
+        if (c0 < K) {
+            const int h = c0 / hd, c = c0 - h * hd;
+            const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + c;
 #pragma unroll
-        for (int j = 0; j < GM_PR; ++j) {
-            const int i = tid + j * nth;
-            if (i < K) {
-                const int h = i / hd, c = i - h * hd;
-                const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + c;
-#pragma unroll
-                for (int sp = 0; sp < GM_SPR; ++sp)
-                    if (sp < S) ov[j][sp] = op[(size_t)sp * f.G * hd];
-            }
+            for (int sp = 0; sp < GM_SPR; ++sp)
+                if (sp < S) {
+                    const float4 a0 = *(const float4*)(op + (size_t)sp * f.G * hd);
+                    const float4 a1 = *(const float4*)(op + (size_t)sp * f.G * hd + 4);
+                    ov[sp][0] = a0.x; ov[sp][1] = a0.y; ov[sp][2] = a0.z; ov[sp][3] = a0.w;
+                    ov[sp][4] = a1.x; ov[sp][5] = a1.y; ov[sp][6] = a1.z; ov[sp][7] = a1.w;
+                }
         }
         __syncthreads();
         if (tid < H) {
@@ -290,23 +359,41 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
             sinv[tid] = L > 0.f ? 1.0f / L : 0.0f;
         }
         __syncthreads();
-        auto merge = [&](int i, const float* o4) {
-            const int h = i / hd, c = i - h * hd;
-            const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + c;
-            float acc = 0.f;
-            for (int sp = 0; sp < S; ++sp) {
-                const float w = sm[h * S + sp];
-                const float o = (o4 && sp < GM_SPR) ? o4[sp] : op[(size_t)sp * f.G * hd];
-                if (w != 0.f) acc += w * o;
-            }
-            return acc * sinv[h];
-        };
+        const int rounds = (K + 8 * nth - 1) / (8 * nth);  // the same for every lane
+        for (int m = 0; m < rounds; ++m) {
+            const int c = c0 + 8 * nth * m;
+            float sum = 0.f;
+            if (c < K) {
+                const int h = c / hd, cc = c - h * hd;
+                const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * hd + cc;
+                float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                // splits in order; an empty split (weight 0) has no partials written and is skipped
 #pragma unroll
-        for (int j = 0; j < GM_PR; ++j) {
-            const int i = tid + j * nth;
-            if (i < K) gm_put_one<KIND>(a16, xsum, i, merge(i, ov[j]));
+                for (int sp = 0; sp < GM_SPR; ++sp) {
+                    const float w = sp < S ? sm[h * S + sp] : 0.f;
+                    if (w != 0.f) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc[j] += w * (m == 0 ? ov[sp][j] : op[(size_t)sp * f.G * hd + j]);
+                    }
+                }
+                for (int sp = GM_SPR; sp < S; ++sp) {
+                    const float w = sm[h * S + sp];
+                    if (w != 0.f) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) acc[j] += w * op[(size_t)sp * f.G * hd + j];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float v = acc[j] * sinv[h];
+                    gm_put_a<KIND>(a16, 1, 0, c + j, v);
+                    sum += v;
+                }
+            }
+            sum += gm_dpp<0xB1>(sum);
+            sum += gm_dpp<0x4E>(sum);
+            if (c < K && (tid & 3) == 0) xsum[c >> 5] = sum;
         }
-        for (int i = tid + GM_PR * nth; i < K; i += nth) gm_put_one<KIND>(a16, xsum, i, merge(i, nullptr));
     }
     __syncthreads();
 }
