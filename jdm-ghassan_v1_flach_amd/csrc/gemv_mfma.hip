@@ -152,45 +152,9 @@ __device__ __forceinline__ void gm_kinv(int kk, int& r8, int& g, int& el) {
 }
 
 // ---------------------------------------------------------- fusion hooks
-// Cross-lane moves on the DPP path (no LDS round trip): quad_perm 0xB1 /
-// 0x4E = lane xor 1 / 2, row_ror 4 / 8 rotate inside a row of 16 lanes,
-// row_bcast 15 / 31 pass a row's last lane to the next row(s) given by the
-// row mask; lanes without a source read 0.
-template <int CTRL, int RM = 0xF>
-__device__ __forceinline__ float gm_dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, RM, 0xF, false));
-}
-template <int CTRL, int RM = 0xF>
-__device__ __forceinline__ double gm_dpp(double v) {
-    typedef int i2 __attribute__((ext_vector_type(2)));
-    const i2 p = __builtin_bit_cast(i2, v);
-    i2 r;
-    r.x = __builtin_amdgcn_update_dpp(0, p.x, CTRL, RM, 0xF, false);
-    r.y = __builtin_amdgcn_update_dpp(0, p.y, CTRL, RM, 0xF, false);
-    return __builtin_bit_cast(double, r);
-}
-// Sum over a whole wave (every lane active); the total ends in lane 63.
-template <typename T>
-__device__ __forceinline__ T gm_wave_total(T v) {
-    v += gm_dpp<0xB1>(v);
-    v += gm_dpp<0x4E>(v);
-    v += gm_dpp<0x124>(v);
-    v += gm_dpp<0x128>(v);          // every lane: its row of 16
-    v += gm_dpp<0x142, 0xA>(v);     // rows 1, 3 += rows 0, 2
-    v += gm_dpp<0x143, 0xC>(v);     // rows 2, 3 += lane 31 (rows 0 + 1)
-    return v;
-}
-__device__ __forceinline__ double gm_lane63(double v) {
-    typedef int i2 __attribute__((ext_vector_type(2)));
-    const i2 p = __builtin_bit_cast(i2, v);
-    i2 r;
-    r.x = __builtin_amdgcn_readlane(p.x, 63);
-    r.y = __builtin_amdgcn_readlane(p.y, 63);
-    return __builtin_bit_cast(double, r);
-}
 // Block-wide sum of a double over DPP and one LDS exchange (all threads get the total).
 __device__ __forceinline__ double gm_block_sum_dpp(double v, double* red) {
-    v = gm_lane63(gm_wave_total(v));
+    v = wave_sum(v);
     const int nw = blockDim.x >> 6;
     if (nw == 1) return v;
     __syncthreads();
@@ -309,8 +273,8 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
                     sum += v;
                 }
             }
-            sum += gm_dpp<0xB1>(sum);
-            sum += gm_dpp<0x4E>(sum);
+            sum += dpp_f32<0xB1>(sum);
+            sum += dpp_f32<0x4E>(sum);
             if (c < K && (tid & 3) == 0) xsum[c >> 5] = sum;
         }
     } else {
@@ -390,8 +354,8 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
                     sum += v;
                 }
             }
-            sum += gm_dpp<0xB1>(sum);
-            sum += gm_dpp<0x4E>(sum);
+            sum += dpp_f32<0xB1>(sum);
+            sum += dpp_f32<0x4E>(sum);
             if (c < K && (tid & 3) == 0) xsum[c >> 5] = sum;
         }
     }

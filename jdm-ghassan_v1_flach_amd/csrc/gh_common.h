@@ -125,15 +125,70 @@ __host__ __device__ inline uint16_t f32_to_bf16(float f) {
 }
 
 // ------------------------------------------------------------ wave helpers
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Cross-lane moves on the DPP path (no LDS round trip): quad_perm 0xB1 /
+// 0x4E = lane xor 1 / 2, row_ror 4 / 8 rotate inside a row of 16 lanes,
+// row_shl 4 / 8 read lane + 4 / + 8 of the row, row_bcast 15 / 31 pass a
+// row's last lane to the next row(s) selected by the row mask. A lane without
+// a source (or in an unselected row) gets `old`.
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ int dpp_i32(int v, int old) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, RM, 0xF, false);
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ float dpp_f32(float v, float old = 0.f) {
+    return __builtin_bit_cast(float, dpp_i32<CTRL, RM>(__builtin_bit_cast(int, v), __builtin_bit_cast(int, old)));
+}
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ double dpp_f64(double v) {  // old = 0
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    const i2 p = __builtin_bit_cast(i2, v);
+    i2 r;
+    r.x = dpp_i32<CTRL, RM>(p.x, 0);
+    r.y = dpp_i32<CTRL, RM>(p.y, 0);
+    return __builtin_bit_cast(double, r);
+}
+// Sum over a whole wave (every lane active): the total ends in lane 63.
+template <typename T>
+__device__ __forceinline__ T wave_total63(T v) {
+    if constexpr (sizeof(T) == 8) {
+        v += dpp_f64<0xB1>(v);
+        v += dpp_f64<0x4E>(v);
+        v += dpp_f64<0x124>(v);
+        v += dpp_f64<0x128>(v);       // every lane: its row of 16
+        v += dpp_f64<0x142, 0xA>(v);  // rows 1, 3 += rows 0, 2
+        v += dpp_f64<0x143, 0xC>(v);  // rows 2, 3 += lane 31 (rows 0 + 1)
+    } else {
+        v += dpp_f32<0xB1>(v);
+        v += dpp_f32<0x4E>(v);
+        v += dpp_f32<0x124>(v);
+        v += dpp_f32<0x128>(v);
+        v += dpp_f32<0x142, 0xA>(v);
+        v += dpp_f32<0x143, 0xC>(v);
+    }
     return v;
 }
+__device__ __forceinline__ float lane63(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ double lane63(double v) {
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    const i2 p = __builtin_bit_cast(i2, v);
+    i2 r;
+    r.x = __builtin_amdgcn_readlane(p.x, 63);
+    r.y = __builtin_amdgcn_readlane(p.y, 63);
+    return __builtin_bit_cast(double, r);
+}
+// Sum / max over a whole wave (every lane active); every lane gets the result.
+__device__ inline float wave_sum(float v) { return lane63(wave_total63(v)); }
+__device__ inline double wave_sum(double v) { return lane63(wave_total63(v)); }
 __device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v, v));
+    v = fmaxf(v, dpp_f32<0x4E>(v, v));
+    v = fmaxf(v, dpp_f32<0x124>(v, v));
+    v = fmaxf(v, dpp_f32<0x128>(v, v));
+    v = fmaxf(v, dpp_f32<0x142, 0xA>(v, v));
+    v = fmaxf(v, dpp_f32<0x143, 0xC>(v, v));
+    return lane63(v);
 }
 
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }

@@ -33,19 +33,25 @@ __device__ __forceinline__ void route_finish(float* sp, const float* __restrict_
                              int* sel_lds = nullptr) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    float mx = sp[0];
-    if (lane == 0)
-        for (int e = 1; e < ne; ++e) mx = fmaxf(mx, sp[e]);
-    mx = __shfl(mx, 0, 64);
-    const float ev = lane < ne ? (float)exp((double)(sp[lane] - mx)) : 0.f;
+    const float lg = lane < ne ? sp[lane] : -INFINITY;
+    const float mx = wave_max(lg);  // order-free
+    const float ev = lane < ne ? (float)exp((double)(lg - mx)) : 0.f;
     if (lane < ne) sp[lane] = ev;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // sequential sum in expert order (the reference's rounding): lane 0 reads 8 at a time
     float sum = 0.f;
     if (lane == 0)
-        for (int e = 0; e < ne; ++e) sum += sp[e];
-    sum = __shfl(sum, 0, 64);
+        for (int e0 = 0; e0 < ne; e0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = e0 + j < ne ? sp[e0 + j] : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (e0 + j < ne) sum += v[j];
+        }
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
     const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
     const float p = ev * inv;
     const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
@@ -53,18 +59,27 @@ __device__ __forceinline__ void route_finish(float* sp, const float* __restrict_
     bool taken = false;
     int sel_idx[8];
     for (int k = 0; k < K; ++k) {
-        float bv = (!taken && lane < ne && sel > -1e30f) ? sel : -INFINITY;
-        int bi = (!taken && lane < ne && sel > -1e30f) ? lane : 64;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
+        // candidate key (hi, lo): the value in an order-preserving unsigned form, then 63 - lane,
+        // so the unsigned maximum is the largest value with the lowest index; 0 = no candidate
+        const bool cand = !taken && lane < ne && sel > -1e30f;
+        const uint32_t u = __builtin_bit_cast(uint32_t, sel);
+        uint32_t hi = cand ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+        uint32_t lo = cand ? (uint32_t)(63 - lane) : 0u;
+        auto step = [&](uint32_t oh, uint32_t ol) {
+            if (oh > hi || (oh == hi && ol > lo)) {
+                hi = oh;
+                lo = ol;
             }
-        }
-        if (bi >= 64) bi = 0;  // nothing selectable: the reference falls back to expert 0
+        };
+        step((uint32_t)dpp_i32<0xB1>((int)hi, (int)hi), (uint32_t)dpp_i32<0xB1>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x4E>((int)hi, (int)hi), (uint32_t)dpp_i32<0x4E>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x124>((int)hi, (int)hi), (uint32_t)dpp_i32<0x124>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x128>((int)hi, (int)hi), (uint32_t)dpp_i32<0x128>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x142, 0xA>((int)hi, (int)hi), (uint32_t)dpp_i32<0x142, 0xA>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x143, 0xC>((int)hi, (int)hi), (uint32_t)dpp_i32<0x143, 0xC>((int)lo, (int)lo));
+        const uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 63);
+        const int bl = __builtin_amdgcn_readlane((int)lo, 63);
+        const int bi = bh ? 63 - bl : 0;  // nothing selectable: the reference falls back to expert 0
         sel_idx[k] = bi;
         if (lane == bi) taken = true;
     }
@@ -128,8 +143,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ x, const f
         ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
     }
     if (nw) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = wave_sum(ss);
         if ((tid & 63) == 0) dred[tid >> 6] = ss;
         __syncthreads();
         const double tot = dred[0] + dred[1] + dred[2] + dred[3];
@@ -241,8 +255,7 @@ __global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x
         ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
     }
     if (nw) {
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        ss = wave_sum(ss);
         if ((tid & 63) == 0) dred[tid >> 6] = ss;
         __syncthreads();
         const double tot = dred[0] + dred[1] + dred[2] + dred[3];
