@@ -54,8 +54,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
     double ss = 0.0;
     for (int i = threadIdx.x; i < dim; i += 256) ss += (double)xr[i] * xr[i];
     __shared__ double red[4];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const double tot = red[0] + red[1] + red[2] + red[3];
@@ -80,11 +79,25 @@ __global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ l, in
     }
     __shared__ float sv[16];
     __shared__ int si[16];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    {
+        // the wave's best as an unsigned key (value in an order-preserving form, then ~index so
+        // the lower index wins ties; 0 = none) reduced on the DPP path into lane 63
+        const uint32_t u = __builtin_bit_cast(uint32_t, bv);
+        uint32_t hi = bi >= 0 ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+        uint32_t lo = bi >= 0 ? ~(uint32_t)bi : 0u;
+        auto step = [&](uint32_t oh, uint32_t ol) {
+            if (oh > hi || (oh == hi && ol > lo)) { hi = oh; lo = ol; }
+        };
+        step((uint32_t)dpp_i32<0xB1>((int)hi, (int)hi), (uint32_t)dpp_i32<0xB1>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x4E>((int)hi, (int)hi), (uint32_t)dpp_i32<0x4E>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x124>((int)hi, (int)hi), (uint32_t)dpp_i32<0x124>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x128>((int)hi, (int)hi), (uint32_t)dpp_i32<0x128>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x142, 0xA>((int)hi, (int)hi), (uint32_t)dpp_i32<0x142, 0xA>((int)lo, (int)lo));
+        step((uint32_t)dpp_i32<0x143, 0xC>((int)hi, (int)hi), (uint32_t)dpp_i32<0x143, 0xC>((int)lo, (int)lo));
+        const uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 63);
+        const uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)lo, 63);
+        bi = bh ? (int)~bl : -1;
+        bv = bh ? ((bh & 0x80000000u) ? __builtin_bit_cast(float, bh & 0x7FFFFFFFu) : __builtin_bit_cast(float, ~bh)) : 0.f;
     }
     if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
     __syncthreads();

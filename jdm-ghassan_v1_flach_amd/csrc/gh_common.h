@@ -181,6 +181,19 @@ __device__ __forceinline__ double lane63(double v) {
 // Sum / max over a whole wave (every lane active); every lane gets the result.
 __device__ inline float wave_sum(float v) { return lane63(wave_total63(v)); }
 __device__ inline double wave_sum(double v) { return lane63(wave_total63(v)); }
+// Sum over groups of lpr consecutive lanes (lpr a power of two <= 64); every
+// lane of a group gets its total. Inside a row by mirrors (row_mirror: lane i
+// <-> 15 - i, row_half_mirror: i <-> 7 - i, each lane then holds a pair) and
+// the two quad xors; across rows by lane permutes.
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+    if (lpr >= 16) v += dpp_f32<0x140>(v);
+    if (lpr >= 8) v += dpp_f32<0x141>(v);
+    if (lpr >= 4) v += dpp_f32<0x4E>(v);
+    if (lpr >= 2) v += dpp_f32<0xB1>(v);
+    if (lpr >= 32) v += __shfl_xor(v, 16, 64);
+    if (lpr >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
 __device__ inline float wave_max(float v) {
     v = fmaxf(v, dpp_f32<0xB1>(v, v));
     v = fmaxf(v, dpp_f32<0x4E>(v, v));

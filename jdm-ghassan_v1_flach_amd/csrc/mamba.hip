@@ -431,8 +431,7 @@ __global__ void __launch_bounds__(256) k_gated_norm(const float* __restrict__ y,
         ss += (double)v * v;
     }
     __shared__ double red[4];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const double var = (red[0] + red[1] + red[2] + red[3]) / (double)n;
@@ -493,8 +492,7 @@ __global__ void __launch_bounds__(256) k_step_scan(const float* __restrict__ xbc
     }
     *(float4*)srow = make_float4(s[0], s[1], s[2], s[3]);
     *(float4*)(srow + 4) = make_float4(s[4], s[5], s[6], s[7]);
-#pragma unroll
-    for (int o = TPR >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    acc = group_sum(acc, TPR);
     if (tc == 0) y[i] = acc + D[h] * xv;
 }
 

@@ -533,10 +533,8 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
         ga += task_dot<KIND>(w0, xv, xs, t);
         if (DUAL) ub += task_dot<KIND>(w1, xv, xs, t);
     }
-    for (int o = LPR >> 1; o > 0; o >>= 1) {
-        ga += __shfl_xor(ga, o, 64);
-        if (DUAL) ub += __shfl_xor(ub, o, 64);
-    }
+    ga = group_sum(ga, LPR);
+    if (DUAL) ub = group_sum(ub, LPR);
     if (sub == 0 && row < rows) {
         const float v = DUAL ? ga / (1.0f + expf(-ga)) * ub : ga;
         if (shared) J.out_s[(size_t)(job - J.S) * rows + row] = v;
@@ -622,7 +620,7 @@ __global__ void __launch_bounds__(256) k_moe_down_combine(GemvJobs J, const floa
                 ga += task_dot<KIND>(wa[q], xv, xs, t);
             }
         }
-        for (int o = LPR >> 1; o > 0; o >>= 1) ga += __shfl_xor(ga, o, 64);
+        ga = group_sum(ga, LPR);
         if (shared) acc = ga;
         else acc += wk[j] * ga;
 #pragma unroll

@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(256) k_gemv(const float* __restrict__ x, const
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     float v = acc[r][m];
-                    for (int o = LPR >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+                    v = group_sum(v, LPR);
                     const int n = grp * rows_per_wave + rp + RP * r;
                     if (sub == 0 && m < M && n < N) y[(size_t)m * N + n] = v;
                     acc[r][m] = 0.f;
