@@ -138,7 +138,7 @@ def kernel_suite(gh):
                 kern = "k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else "k_gemv_mfma"
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
-                res[tag] = entry("k_to_f16+k_gemm_q2", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
+                res[tag] = entry("k_to_f16+k_gemm_q4", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
                                  bound="mfma")
             del dw, dx, y
     # ---------------- c3: SSD scan T=4096 + decode state update

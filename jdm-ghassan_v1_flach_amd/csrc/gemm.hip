@@ -15,8 +15,10 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_tile.h"
+#include "lds_dma.h"
 
 namespace gh {
 
@@ -233,33 +235,179 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__
         }
 }
 
-// ---------------------------------------------------------------- v3
-// Large tiles for large M: a block of 4 waves computes 256x256, each wave
-// 128x128 as 4x4 v_mfma_f32_32x32x16_f16 tiles (accumulators in the
-// accumulation registers, one wave per SIMD). Per K step of 64 a wave issues
-// 64 MFMAs (2048 cycles at the issue rate) against 32 16-byte operand reads
-// from LDS, so the matrix cores rather than LDS bound the step (the 128x128
-// tile of v2 read one operand per MFMA). LDS double-buffered, one barrier per
-// step, next step's pieces in registers while the MFMAs run.
-constexpr int B3M = 256, B3N = 256;
+// ---------------------------------------------------------------- v4
+// Large tiles for large M, Q4_K / Q8_0 weights: a block of 4 waves computes
+// 256 (tokens) x 256 (output rows), each wave 128x128 as 4x4
+// v_mfma_f32_32x32x16_f16 tiles (accumulators in the accumulation registers,
+// one wave per SIMD). Per K step of 64:
+//  - the fp16 activation tile (256 rows x 128 B) moves global -> LDS by
+//    direct transfers (global_load_lds_dwordx4, no register round trip);
+//  - every thread dequantises 64 weights of one output row (loaded one step
+//    ahead) into the other LDS buffer, a quarter after each k-substep's
+//    MFMAs, so the decode overlaps the matrix cores;
+//  - MFMA operands are read one k-substep ahead (scheduling barriers keep
+//    the compiler from sinking the reads next to their use).
+// LDS rows are 128 B with the 16-byte piece c of row r stored at
+// c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 / ds_write_b128 phase
+// touches then cover all 64 banks. A and B are double-buffered (128 KB), one
+// barrier per step. gridDim.y = 2 splits K for grids that would not fill the
+// chip; the two halves then add into a zeroed Y (two addends onto 0 give the
+// same sum in either order, so the result stays deterministic).
+constexpr int G4M = 256, G4N = 256;
+constexpr size_t G4_LDS = 4 * 256 * 128;  // A[2], B[2]: 256 rows x 128 bytes
+
+__device__ __forceinline__ void g4_dma(const void* base, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory");
+}
+
+struct G4Scale {
+    float d1[2], m1[2];
+};
 template <int KIND>
-__global__ void __launch_bounds__(256, 1) k_gemm_q3(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t g3_smem[];
-    uint16_t* sA0 = g3_smem;                        // [2][B3M * LDS_STRIDE]
-    uint16_t* sB0 = g3_smem + 2 * B3M * LDS_STRIDE;  // [2][B3N * LDS_STRIDE]
+struct G4Raw;
+template <>
+struct G4Raw<3> {  // Q4_K: super-block header + the 32 nibble bytes of pair t&3
+    gh_u32x4v hd, a, b;
+    __device__ __forceinline__ void load(const uint8_t* row, int t) {
+        const uint8_t* sb = row + (size_t)(t >> 2) * 144;
+        const int p = t & 3;
+        hd = *(const gh_u32x4v*)sb;
+        a = *(const gh_u32x4v*)(sb + 16 + 32 * p);
+        b = *(const gh_u32x4v*)(sb + 32 + 32 * p);
+    }
+};
+template <>
+struct G4Raw<2> {  // Q8_0: two 34-byte blocks at t*68 (4-byte aligned)
+    gh_u32x4v q[4];
+    uint32_t last;
+    __device__ __forceinline__ void load(const uint8_t* row, int t) {
+        const uint8_t* p = row + (size_t)t * 68;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = *(const gh_u32x4v*)(p + 16 * i);
+        last = *(const uint32_t*)(p + 64);
+    }
+    __device__ __forceinline__ uint32_t w(int i) const { return i < 16 ? q[i >> 2][i & 3] : last; }
+};
+
+__device__ __forceinline__ uint32_t g4_pack(float lo, float hi) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 v;
+    v[0] = (_Float16)lo;  // RNE, as fp32_to_fp16
+    v[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ G4Scale g4_scales(const G4Raw<2>&, int) { return G4Scale{}; }
+// Q4_K scales of the two sub-blocks (2p, 2p+1) of step t: y = q * (d*sc) - dmin*m
+__device__ __forceinline__ G4Scale g4_scales(const G4Raw<3>& r, int t) {
+    // scale bytes 0..7 in lo, 8..11 in hi; shifts instead of an indexed array (t is a runtime value)
+    const uint64_t lo = (uint64_t)r.hd[1] | ((uint64_t)r.hd[2] << 32);
+    const uint32_t hi = r.hd[3];
+    const float d = f16_to_f32((uint16_t)(r.hd[0] & 0xFFFF)), dm = f16_to_f32((uint16_t)(r.hd[0] >> 16));
+    const int p = t & 3;
+    G4Scale s;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * p + h;
+        int scv, mv;
+        if (p < 2) {
+            scv = (int)(lo >> (8 * j)) & 63;
+            mv = (int)(lo >> (8 * j + 32)) & 63;
+        } else {
+            const int b4 = (int)(hi >> (8 * (j - 4))) & 0xFF;
+            scv = (b4 & 0xF) | ((((int)(lo >> (8 * (j - 4))) >> 6) & 3) << 4);
+            mv = (b4 >> 4) | ((((int)(lo >> (8 * j))) >> 6 & 3) << 4);
+        }
+        s.d1[h] = d * (float)scv;
+        s.m1[h] = dm * (float)mv;
+    }
+    return s;
+}
+
+// values 16Q..16Q+15 of a row's step as 8 packed fp16 pairs
+template <int Q>
+__device__ __forceinline__ void g4_quarter(const G4Raw<3>& r, const G4Scale& s, uint32_t, uint32_t (&h)[8]) {
+    constexpr int hi = Q >> 1;  // values 0..31: low nibbles (sub-block 2p), 32..63: high (2p+1)
+    const gh_u32x4v& src = (Q & 1) ? r.b : r.a;
+    const float d1 = s.d1[hi], nm = -s.m1[hi];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (hi ? (src[i] >> 4) : src[i]) & 0x0F0F0F0Fu;
+        const float q0 = (float)(w & 0xFF), q1 = (float)((w >> 8) & 0xFF);
+        const float q2 = (float)((w >> 16) & 0xFF), q3 = (float)(w >> 24);
+        // q * d1 is exact (4 + 17 bits), so one fma rounds like q*d1 - m1 in fp32
+        h[2 * i] = g4_pack(fmaf(q0, d1, nm), fmaf(q1, d1, nm));
+        h[2 * i + 1] = g4_pack(fmaf(q2, d1, nm), fmaf(q3, d1, nm));
+    }
+}
+template <int Q>
+__device__ __forceinline__ void g4_quarter(const G4Raw<2>& r, const G4Scale&, uint32_t magic, uint32_t (&h)[8]) {
+    // block Q>>1; its quants 16(Q&1)..+15 start at byte 34(Q>>1) + 2 + 16(Q&1)
+    constexpr int off = 34 * (Q >> 1) + 2 + 16 * (Q & 1);
+    const uint32_t dbits = (Q >> 1) ? (r.w(8) >> 16) : (r.w(0) & 0xFFFF);
+    const float d = f16_to_f32((uint16_t)dbits);
+    const float nb = -1152.f * d;  // (1152 + q) d - 1152 d = q d exactly
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        constexpr int dw = off >> 2;
+        uint32_t u;
+        if constexpr ((off & 3) == 2) u = __builtin_amdgcn_alignbyte(r.w(dw + i + 1), r.w(dw + i), 2);
+        else u = r.w(dw + i);
+        u ^= 0x80808080u;
+        const uint32_t c0 = gq_and_or(u, 0x00FF00FFu, magic);
+        const uint32_t c1 = gq_and_or(u >> 8, 0x00FF00FFu, magic);
+        h[2 * i] = g4_pack(fmaf(gq_lo(c0), d, nb), fmaf(gq_lo(c1), d, nb));
+        h[2 * i + 1] = g4_pack(fmaf(gq_hi(c0), d, nb), fmaf(gq_hi(c1), d, nb));
+    }
+}
+template <int KIND>
+__device__ __forceinline__ void g4_quarter_rt(const G4Raw<KIND>& r, const G4Scale& s, uint32_t magic, int q,
+                                              uint32_t (&h)[8]) {
+    if (q == 0) g4_quarter<0>(r, s, magic, h);
+    if (q == 1) g4_quarter<1>(r, s, magic, h);
+    if (q == 2) g4_quarter<2>(r, s, magic, h);
+    if (q == 3) g4_quarter<3>(r, s, magic, h);
+}
+
+// K steps [t_beg, t_beg + T) of block (tile, blockIdx.y); T even, >= 2
+template <int KIND>
+__global__ void __launch_bounds__(256, 1) k_gemm_q4(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
+                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb, int T) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t g4_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tilesN = cdiv(N, B3N), tilesM = cdiv(M, B3M);
+    const int tilesN = cdiv(N, G4N), tilesM = cdiv(M, G4M);
     const int nblk = tilesN * tilesM;
     int bid = blockIdx.x;
-    if (nblk % 8 == 0) bid = (bid % 8) * (nblk / 8) + bid / 8;  // XCD-aware: an XCD keeps a run of N tiles
+    // XCD-aware order: consecutive block ids land on different XCDs, so give
+    // each XCD a contiguous run of tiles (all M tiles of a few N tiles)
+    if (nblk % 8 == 0) bid = (bid % 8) * (nblk / 8) + bid / 8;
     const int tm = bid % tilesM, tn = bid / tilesM;
-    const int m0 = tm * B3M, n0 = tn * B3N;
-    // A pieces: thread -> rows ar + 32 i (i < 8), 8 halves at ac
-    const int ar = tid >> 3, ac = (tid & 7) * 8;
-    // B: thread -> row tid, both halves of the step's 64 values
+    const int m0 = tm * G4M, n0 = tn * G4N;
+    const int t_beg = blockIdx.y * T;
+    const uint32_t lds0 = lds_addr(g4_smem);
+
+    // A: wave w moves rows 64w..64w+63 as 8 transfers of 8 rows (16 B per lane)
+    uint32_t avoff[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 64 * wave + 8 * i + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int rr = m0 + r < M ? m0 + r : M - 1;  // rows past M: any valid row (outputs masked)
+        avoff[i] = (uint32_t)(((size_t)rr * K + c * 8) * 2);
+    }
+    const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + 64 * wave * 128);
+    // B: thread -> output row tid of the tile
     const int bn = n0 + tid;
     const uint8_t* wrow = W + (size_t)(bn < N ? bn : N - 1) * rowb;
+    const int bsw = (tid >> 1) & 7;
+    uint8_t* bdst0 = g4_smem + 65536 + tid * 128;
+    // MFMA operands: row = wm/wn + 32 i + lane%32, logical piece 2 ks + lane/32
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int fsw = (lane >> 1) & 7, fhi = lane >> 5;
+    const int frow = (lane & 31) * 128;
+
     f32x16 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -267,78 +415,92 @@ __global__ void __launch_bounds__(256, 1) k_gemm_q3(const uint16_t* __restrict__
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
-    const int T = K / BK;
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));
 
-    gh_u32x4v xa[8];
-    WLoad<KIND> wl0, wl1;
-    size_t xoff[8];
+    auto dma_a = [&](int t, int buf) {
+        const uint16_t* base = X16 + (size_t)(t_beg + t) * 64;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int am = m0 + ar + 32 * i;
-        xoff[i] = (size_t)(am < M ? am : M - 1) * K + ac;
-    }
-    // the blocks of one M tile (and of one N tile) run together and would read the same lines in
-    // lockstep: each block starts its K walk at its own step
-    const int t0 = (tn * 5 + tm * 3) % T;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xa[i] = *(const gh_u32x4v*)(X16 + xoff[i] + (size_t)t0 * BK);
-    wl0.load(wrow, t0, 0);
-    wl1.load(wrow, t0, 1);
-    int buf = 0;
-    for (int tt = 0; tt < T; ++tt, buf ^= 1) {
-        const int tnext = tt + 1 + t0 < T ? tt + 1 + t0 : tt + 1 + t0 - T;
-        uint16_t* sA = sA0 + buf * B3M * LDS_STRIDE;
-        uint16_t* sB = sB0 + buf * B3N * LDS_STRIDE;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            gh_u32x4v v = xa[i];
-            if (m0 + ar + 32 * i >= M) v = gh_u32x4v{0u, 0u, 0u, 0u};
-            *(gh_u32x4v*)(sA + (ar + 32 * i) * LDS_STRIDE + ac) = v;
-        }
-        {
-            uint16_t* dst = sB + tid * LDS_STRIDE;
-            if (bn < N) {
-                decode16<KIND>(wl0, dst, magic);
-                decode16<KIND>(wl1, dst + 32, magic);
-            } else {
-                float z[32];
-#pragma unroll
-                for (int i = 0; i < 32; ++i) z[i] = 0.f;
-                store_f16x32(dst, z);
-                store_f16x32(dst + 32, z);
-            }
-        }
-        __syncthreads();
-        if (tt + 1 < T) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xa[i] = *(const gh_u32x4v*)(X16 + xoff[i] + (size_t)tnext * BK);
-            wl0.load(wrow, tnext, 0);
-            wl1.load(wrow, tnext, 1);
-        }
-        // operand fragments of k-substep ks + 1 are read while the MFMAs of ks run
+        for (int i = 0; i < 8; ++i) g4_dma(base, avoff[i], a_lds + buf * 32768 + i * 1024);
+    };
+    auto load_b = [&](G4Raw<KIND>& r, int t) { r.load(wrow, t_beg + t); };
+    auto put_b = [&](int buf, int q, const uint32_t (&h)[8]) {
+        uint8_t* d = bdst0 + buf * 32768;
+        *(gh_u32x4v*)(d + (((2 * q) ^ bsw) * 16)) = gh_u32x4v{h[0], h[1], h[2], h[3]};
+        *(gh_u32x4v*)(d + (((2 * q + 1) ^ bsw) * 16)) = gh_u32x4v{h[4], h[5], h[6], h[7]};
+    };
+    // one step: MFMAs on buffer cur, decode of rn (step tt+1) into the other;
+    // `issue` requests later steps' data once the first operand reads are out
+    auto compute = [&](int tt, int cur, const G4Raw<KIND>& rn, auto has_next_c, auto issue) {
+        constexpr bool has_next = decltype(has_next_c)::value;
+        const uint8_t* sA = g4_smem + cur * 32768 + wm * 128 + frow;
+        const uint8_t* sB = g4_smem + 65536 + cur * 32768 + wn * 128 + frow;
         f16x8 a[2][4], b[2][4];
         auto frag = [&](int ks, f16x8 (&fa)[4], f16x8 (&fb)[4]) {
-            const int kofs = ks * 16 + (lane >> 5) * 8;
+            const int co = (((2 * ks + fhi) ^ fsw) * 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                fa[i] = *(const f16x8*)(sA + (wm + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
-                fb[i] = *(const f16x8*)(sB + (wn + i * 32 + (lane & 31)) * LDS_STRIDE + kofs);
+                fa[i] = *(const f16x8*)(sA + i * 32 * 128 + co);
+                fb[i] = *(const f16x8*)(sB + i * 32 * 128 + co);
             }
         };
         frag(0, a[0], b[0]);
+        issue();
+        __builtin_amdgcn_sched_barrier(0);
+        [[maybe_unused]] G4Scale s;
+        if constexpr (has_next) s = g4_scales(rn, t_beg + tt + 1);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            if (ks + 1 < BK / 16) frag(ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks + 1 < 4) frag(ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
+            if constexpr (has_next) {
+                uint32_t h[8];
+                g4_quarter_rt<KIND>(rn, s, magic, ks, h);
+                put_b(cur ^ 1, ks, h);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto sync = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): A transfers, weight bytes, B stores
+        __builtin_amdgcn_s_barrier();
+    };
+    using YES = std::integral_constant<bool, true>;
+    using NO = std::integral_constant<bool, false>;
+    auto nothing = [] {};
+
+    G4Raw<KIND> r0, r1;
+    dma_a(0, 0);
+    load_b(r0, 0);
+    load_b(r1, 1);
+    {
+        const G4Scale s0 = g4_scales(r0, t_beg);
+        uint32_t h[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            g4_quarter_rt<KIND>(r0, s0, magic, q, h);
+            put_b(0, q, h);
         }
     }
+    sync();
+    int tt = 0;
+    // steady state: buffer tt&1 holds step tt; r1 (even tt) / r0 (odd tt) holds step tt+1
+    for (; tt + 3 < T; tt += 2) {
+        compute(tt, 0, r1, YES{}, [&] { dma_a(tt + 1, 1); load_b(r0, tt + 2); });
+        sync();
+        compute(tt + 1, 1, r0, YES{}, [&] { dma_a(tt + 2, 0); load_b(r1, tt + 3); });
+        sync();
+    }
+    compute(tt, 0, r1, YES{}, [&] { dma_a(tt + 1, 1); });
+    sync();
+    compute(tt + 1, 1, r0, NO{}, nothing);
+
+    const bool split = gridDim.y > 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -348,11 +510,17 @@ __global__ void __launch_bounds__(256, 1) k_gemm_q3(const uint16_t* __restrict__
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) Y[(size_t)row * N + col] = acc[i][j][e];
+                if (row >= M) continue;
+                if (split) atomicAdd(&Y[(size_t)row * N + col], acc[i][j][e]);
+                else Y[(size_t)row * N + col] = acc[i][j][e];
             }
         }
 }
-constexpr size_t G3_LDS = (size_t)2 * (B3M + B3N) * LDS_STRIDE * 2;
+
+__global__ void k_zero_f32(float* __restrict__ y, int64_t n4) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+        ((float4*)y)[i] = float4{0.f, 0.f, 0.f, 0.f};
+}
 
 int launch_to_f16(const float* x, uint16_t* y, int64_t n) {
     const int64_t n4 = n / 4;
@@ -369,23 +537,32 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
     const int64_t n4 = (int64_t)M * K / 4;
     hipLaunchKernelGGL(k_to_f16, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 8192)), dim3(256), 0, stream(), x,
                        x16, n4);
-    static const int v3 = [] {
-        const char* e = getenv("GH_GEMM_V3");
-        return e ? atoi(e) : 1;
-    }();
-    if (v3 && (int64_t)cdiv(M, B3M) * cdiv(N, B3N) >= num_cus()) {  // large tiles once they fill the chip
-        static bool configured = false;
-        if (!configured) {
-            const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q3<KIND>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)G3_LDS);
-            if (e != hipSuccess) return fail(GH_EHIP, "k_gemm_q3 LDS attribute: %s", hipGetErrorString(e));
-            configured = true;
+    if constexpr (KIND == 2 || KIND == 3) {
+        static const int v4 = [] {
+            const char* e = getenv("GH_GEMM_V4");
+            return e ? atoi(e) : 1;
+        }();
+        const int tiles = cdiv(M, G4M) * cdiv(N, G4N), T = K / 64;
+        // 256x256 tiles once they fill the chip (split K in two when that is needed to fill it)
+        const int split = tiles >= num_cus() ? 1 : (2 * tiles >= num_cus() && T % 4 == 0) ? 2 : 0;
+        if (v4 && K % 256 == 0 && split && (split == 1 || ((size_t)M * N % 4 == 0 && ((uintptr_t)y & 15) == 0))) {
+            static bool configured = false;
+            if (!configured) {
+                const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4<KIND>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)G4_LDS);
+                if (e != hipSuccess) return fail(GH_EHIP, "k_gemm_q4 LDS attribute: %s", hipGetErrorString(e));
+                configured = true;
+            }
+            if (split > 1) {
+                const int64_t n4 = (int64_t)M * N / 4;
+                hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 4096)), dim3(256), 0,
+                                   stream(), y, n4);
+            }
+            hipLaunchKernelGGL(k_gemm_q4<KIND>, dim3(tiles, split), dim3(256), G4_LDS, stream(), x16,
+                               (const uint8_t*)w, y, M, K, N, rowb, T / split);
+            GH_LAUNCHED("k_gemm_q4");
+            return GH_OK;
         }
-        const int blocks = cdiv(M, B3M) * cdiv(N, B3N);
-        hipLaunchKernelGGL(k_gemm_q3<KIND>, dim3(blocks), dim3(256), G3_LDS, stream(), x16, (const uint8_t*)w, y, M, K,
-                           N, rowb);
-        GH_LAUNCHED("k_gemm_q3");
-        return GH_OK;
     }
     const int blocks = cdiv(M, BM) * cdiv(N, BN);
     hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, (const uint8_t*)w, y, M, K, N,
