@@ -32,75 +32,48 @@ __device__ __forceinline__ void route_finish(float* sp, const float* __restrict_
                              int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs,
                              int* sel_lds = nullptr) {
 #pragma clang fp contract(off)
+    // one wave of the block runs this (K <= 8, ne <= 64)
+    __shared__ int rf_sel[8];
     const int lane = threadIdx.x & 63;
     const float lg = lane < ne ? sp[lane] : -INFINITY;
     const float mx = wave_max(lg);  // order-free
     const float ev = lane < ne ? (float)exp((double)(lg - mx)) : 0.f;
-    if (lane < ne) sp[lane] = ev;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // sequential sum in expert order (the reference's rounding): lane 0 reads 8 at a time
+    // sequential sum in expert order (the reference's rounding), operands by readlane
     float sum = 0.f;
-    if (lane == 0)
-        for (int e0 = 0; e0 < ne; e0 += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = e0 + j < ne ? sp[e0 + j] : 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (e0 + j < ne) sum += v[j];
-        }
-    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
+    for (int i = 0; i < ne; ++i) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), i));
     const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
     const float p = ev * inv;
     const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
-    // K rounds of argmax: larger value wins, equal values -> lower index
-    bool taken = false;
-    int sel_idx[8];
-    for (int k = 0; k < K; ++k) {
-        // candidate key (hi, lo): the value in an order-preserving unsigned form, then 63 - lane,
-        // so the unsigned maximum is the largest value with the lowest index; 0 = no candidate
-        const bool cand = !taken && lane < ne && sel > -1e30f;
-        const uint32_t u = __builtin_bit_cast(uint32_t, sel);
-        uint32_t hi = cand ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
-        uint32_t lo = cand ? (uint32_t)(63 - lane) : 0u;
-        auto step = [&](uint32_t oh, uint32_t ol) {
-            if (oh > hi || (oh == hi && ol > lo)) {
-                hi = oh;
-                lo = ol;
-            }
-        };
-        step((uint32_t)dpp_i32<0xB1>((int)hi, (int)hi), (uint32_t)dpp_i32<0xB1>((int)lo, (int)lo));
-        step((uint32_t)dpp_i32<0x4E>((int)hi, (int)hi), (uint32_t)dpp_i32<0x4E>((int)lo, (int)lo));
-        step((uint32_t)dpp_i32<0x124>((int)hi, (int)hi), (uint32_t)dpp_i32<0x124>((int)lo, (int)lo));
-        step((uint32_t)dpp_i32<0x128>((int)hi, (int)hi), (uint32_t)dpp_i32<0x128>((int)lo, (int)lo));
-        step((uint32_t)dpp_i32<0x142, 0xA>((int)hi, (int)hi), (uint32_t)dpp_i32<0x142, 0xA>((int)lo, (int)lo));
-        step((uint32_t)dpp_i32<0x143, 0xC>((int)hi, (int)hi), (uint32_t)dpp_i32<0x143, 0xC>((int)lo, (int)lo));
-        const uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)hi, 63);
-        const int bl = __builtin_amdgcn_readlane((int)lo, 63);
-        const int bi = bh ? 63 - bl : 0;  // nothing selectable: the reference falls back to expert 0
-        sel_idx[k] = bi;
-        if (lane == bi) taken = true;
+    // K rounds of "largest value, lowest index among the rest" pick the candidates in the
+    // order of this key: the value in an order-preserving unsigned form, ties by index.
+    // Each candidate's rank (number of candidates before it) is its round.
+    const bool cand = lane < ne && sel > -1e30f;
+    const uint32_t u = __builtin_bit_cast(uint32_t, sel);
+    const uint32_t key = cand ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
+    int r0 = 0, r1 = 0;
+    for (int j = 0; j < ne; j += 2) {
+        const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
+        const uint32_t k1 = j + 1 < ne ? (uint32_t)__builtin_amdgcn_readlane((int)key, j + 1) : 0u;
+        r0 += (k0 > key || (k0 == key && j < lane)) ? 1 : 0;
+        r1 += (k1 > key || (k1 == key && j + 1 < lane)) ? 1 : 0;
     }
-    // weights from the unbiased probabilities, renormalised in order
-    float wv[8], sw = 0.f;
-    for (int k = 0; k < K; ++k) {
-        wv[k] = __shfl(p, sel_idx[k], 64);
-        sw += wv[k];
-    }
-    if (lane == 0) {
-        if (sw > 1e-8f) {
-            const float iw = 1.0f / sw;
-            for (int k = 0; k < K; ++k) wv[k] *= iw;
-        } else {
-            for (int k = 0; k < K; ++k) wv[k] = 1.0f / (float)K;
-        }
-        for (int k = 0; k < K; ++k) {
-            if (idx) idx[(size_t)t * K + k] = sel_idx[k];
-            if (wout) wout[(size_t)t * K + k] = wv[k];
-            if (sel_lds) sel_lds[k] = sel_idx[k];
-        }
+    const int rank = r0 + r1;
+    const int ncand = __popcll(__ballot(cand));
+    if (cand && rank < K) rf_sel[rank] = lane;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane k < K: the expert of round k (a round without candidates takes expert 0, as the reference)
+    const int mine = (lane < K && lane < ncand) ? rf_sel[lane] : 0;
+    const float wv = __shfl(p, mine, 64);
+    // weights from the unbiased probabilities, renormalised in round order
+    float sw = 0.f;
+    for (int k = 0; k < K; ++k) sw += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), k));
+    if (lane < K) {
+        const float wk = (sw > 1e-8f) ? wv * (1.0f / sw) : 1.0f / (float)K;
+        if (idx) idx[(size_t)t * K + lane] = mine;
+        if (wout) wout[(size_t)t * K + lane] = wk;
+        if (sel_lds) sel_lds[lane] = mine;
     }
     if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
 }
@@ -224,14 +197,15 @@ static size_t route_lds(int d, int ne, int N) {
 }
 
 // Router of a large expert set for few tokens, over many blocks: block
-// (x, t) computes the group terms of groups [64x, 64x+64) of token t for
-// every expert (same arithmetic as k_route) into terms [t][group][expert];
-// k_route_select then adds each expert's terms in group order and finishes.
-constexpr int RT_G = 64;
+// (x, t) computes the group terms of groups [gpb x, gpb x + gpb) of token t
+// for every expert (same arithmetic as k_route) into terms
+// [t][group/4][expert][group%4]; k_route_select then adds each expert's terms in group
+// order and finishes. gpb is chosen so that the router matrix is spread over
+// about 64 blocks (one batch of weight loads each).
 __global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x, const float* __restrict__ rw,
                                                      float* __restrict__ terms, int d, int ne,
                                                      const float* __restrict__ nw, float eps,
-                                                     float* __restrict__ xn) {
+                                                     float* __restrict__ xn, int RT_G) {
 #pragma clang fp contract(off)
     extern __shared__ float rt_sx[];  // [d]
     __shared__ double dred[4];
@@ -268,7 +242,7 @@ __global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x
         }
     }
     __syncthreads();
-    float* tt = terms + ((size_t)t * ngroups + g0) * ne;
+    float* tt = terms + (size_t)t * (size_t)cdiv(ngroups, 4) * 4 * ne;  // [t][group/4][expert][4]
     for (int q0 = 0; q0 < ne * gw; q0 += ROUTE_RB * 256) {
         if (q0 > 0) {
 #pragma unroll
@@ -289,32 +263,40 @@ __global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x
                 const float4 w = wreg[b];
                 const float p0 = rt_sx[i] * w.x, p1 = rt_sx[i + 1] * w.y, p2 = rt_sx[i + 2] * w.z,
                             p3 = rt_sx[i + 3] * w.w;
-                tt[(size_t)gl * ne + e] = ((p0 + p1) + p2) + p3;
+                const int g = g0 + gl;
+                tt[((size_t)(g >> 2) * ne + e) * 4 + (g & 3)] = ((p0 + p1) + p2) + p3;
             }
         }
     }
 }
 
+// The sequential per-expert sums (the reference's rounding order) are one
+// dependent chain of ngroups additions per expert: lane e runs expert e's
+// chain; its terms arrive by coalesced 16-byte loads (4 groups per lane, the
+// 64 lanes of a load cover one run of 4 groups), 96 loads in flight.
+constexpr int RS_C = 96;  // float4 per chunk
 __global__ void __launch_bounds__(64) k_route_select(const float* __restrict__ terms, int ngroups, int ne, int K,
                                                      const float* __restrict__ bias, int32_t* __restrict__ idx,
                                                      float* __restrict__ wout, float* __restrict__ probs) {
 #pragma clang fp contract(off)
     __shared__ float sp[64];
     const int t = blockIdx.x, lane = threadIdx.x;
-    const float* tt = terms + (size_t)t * ngroups * ne + lane;
+    const int e = lane < ne ? lane : 0;
+    const float* tt = terms + (size_t)t * (size_t)cdiv(ngroups, 4) * 4 * ne;  // 16-byte aligned per token
+    const float4* t4 = (const float4*)tt + e;  // run r of expert e at t4[r * ne]
+    const int nq = ngroups / 4;
     float s = 0.0f;
-    if (lane < ne) {
-        int g = 0;
-        for (; g + 16 <= ngroups; g += 16) {
-            float v[16];
+    float4 R[RS_C];
+    for (int c = 0; c < nq; c += RS_C) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = tt[(size_t)(g + j) * ne];
+        for (int j = 0; j < RS_C; ++j)
+            if (c + j < nq) R[j] = t4[(size_t)(c + j) * ne];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) s += v[j];
-        }
-        for (; g < ngroups; ++g) s += tt[(size_t)g * ne];
-        sp[lane] = s;
+        for (int j = 0; j < RS_C; ++j)
+            if (c + j < nq) s = (((s + R[j].x) + R[j].y) + R[j].z) + R[j].w;
     }
+    for (int g = 4 * nq; g < ngroups; ++g) s += tt[((size_t)(g >> 2) * ne + e) * 4 + (g & 3)];
+    if (lane < ne) sp[lane] = s;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     route_finish(sp, bias, ne, K, t, idx, wout, probs);
@@ -324,12 +306,12 @@ __global__ void __launch_bounds__(64) k_route_select(const float* __restrict__ t
 // router matrix and few tokens
 static int launch_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w,
                         int N, int d, int ne, int K, const float* nw, float eps, float* xn) {
-    if (N <= 8 && (size_t)ne * d > 16384) {
-        const int ngroups = d / 4;
-        float* terms = (float*)workspace(WS_MOE_TERMS, (size_t)N * ngroups * ne * 4);
+    if (N <= 8 && (size_t)ne * d > 16384 && ne <= 64) {
+        const int ngroups = d / 4, gpb = std::max(4, cdiv(ngroups, 64));
+        float* terms = (float*)workspace(WS_MOE_TERMS, (size_t)N * cdiv(ngroups, 4) * 4 * ne * 4);
         if (!terms) return fail(GH_ENOMEM, "moe route: workspace");
-        hipLaunchKernelGGL(k_route_terms, dim3(cdiv(ngroups, RT_G), N), dim3(256), (size_t)d * 4, stream(), x, rw,
-                           terms, d, ne, nw, eps, xn);
+        hipLaunchKernelGGL(k_route_terms, dim3(cdiv(ngroups, gpb), N), dim3(256), (size_t)d * 4, stream(), x, rw,
+                           terms, d, ne, nw, eps, xn, gpb);
         hipLaunchKernelGGL(k_route_select, dim3(N), dim3(64), 0, stream(), terms, ngroups, ne, K, bias, idx, w,
                            probs);
         GH_LAUNCHED("k_route_terms/select");
