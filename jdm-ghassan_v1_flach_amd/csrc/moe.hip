@@ -32,8 +32,9 @@ __device__ __forceinline__ void route_finish(float* sp, const float* __restrict_
                              int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs,
                              int* sel_lds = nullptr) {
 #pragma clang fp contract(off)
-    // one wave of the block runs this (K <= 8, ne <= 64)
-    __shared__ int rf_sel[8];
+    // one wave per token (K <= 8, ne <= 64, at most 16 waves per block)
+    __shared__ int rf_sel_all[16][8];
+    int* rf_sel = rf_sel_all[threadIdx.x >> 6];
     const int lane = threadIdx.x & 63;
     const float lg = lane < ne ? sp[lane] : -INFINITY;
     const float mx = wave_max(lg);  // order-free
@@ -302,6 +303,89 @@ __global__ void __launch_bounds__(64) k_route_select(const float* __restrict__ t
     route_finish(sp, bias, ne, K, t, idx, wout, probs);
 }
 
+// Router of many tokens (prefill), no norm, in two kernels.
+// k_route_logits: block (expert slice j, token tile i) keeps the router rows
+// of experts 16j..16j+15 in LDS for the whole K range (rows padded by one
+// float4, so the 16 rows a wave reads fall in distinct banks) and computes
+// their logits for 32 tokens: lane (token t = l / 16, expert e = l % 16) of
+// wave w runs the chain of token 32i + 4w + t, expert 16j + e: the
+// reference's group term ((x0 w0 + x1 w1) + x2 w2) + x3 w3
+// (core/moe_cpu.cpp:76-83) added in group order -- the same arithmetic as
+// k_route. Activations stream from global (4 tokens per wave, prefetched a
+// batch of groups ahead). k_route_finish then softmaxes and selects per
+// token (one wave each).
+constexpr int RL_E = 16, RL_T = 32, RL_B = 8;  // experts per block, tokens per block, groups per batch
+__global__ void __launch_bounds__(512) k_route_logits(const float* __restrict__ x, const float* __restrict__ rw,
+                                                      float* __restrict__ logits, int N, int d, int ne) {
+#pragma clang fp contract(off)
+    extern __shared__ float4 rl_w[];  // [RL_E][ngroups + 1]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ngroups = d / 4, rs = ngroups + 1;
+    const int e0 = blockIdx.x * RL_E;
+    const float4* rw4 = (const float4*)rw;
+    for (int q = tid; q < RL_E * ngroups; q += 512) {
+        const int r = q / ngroups, g = q - r * ngroups;
+        const int e = min(e0 + r, ne - 1);
+        rl_w[r * rs + g] = rw4[(size_t)e * ngroups + g];
+    }
+    const int el = lane & 15, tl = lane >> 4;
+    const int t = blockIdx.y * RL_T + wave * 4 + tl;
+    const float4* xr = (const float4*)x + (size_t)min(t, N - 1) * ngroups;
+    const float4* wr = rl_w + el * rs;
+    float4 xa[RL_B], xb[RL_B];
+#pragma unroll
+    for (int j = 0; j < RL_B; ++j) xa[j] = j < ngroups ? xr[j] : float4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    float s = 0.0f;
+    int g = 0;
+    auto batch = [&](const float4 (&xv)[RL_B], int gb) {
+        float term[RL_B];
+#pragma unroll
+        for (int j = 0; j < RL_B; ++j) {
+            const float4 w4 = wr[gb + j];
+            const float p0 = xv[j].x * w4.x, p1 = xv[j].y * w4.y, p2 = xv[j].z * w4.z, p3 = xv[j].w * w4.w;
+            term[j] = ((p0 + p1) + p2) + p3;
+        }
+#pragma unroll
+        for (int j = 0; j < RL_B; ++j) s += term[j];
+    };
+    for (; g + 2 * RL_B <= ngroups; g += 2 * RL_B) {
+#pragma unroll
+        for (int j = 0; j < RL_B; ++j) xb[j] = xr[g + RL_B + j];
+        batch(xa, g);
+        if (g + 3 * RL_B <= ngroups) {
+#pragma unroll
+            for (int j = 0; j < RL_B; ++j) xa[j] = xr[g + 2 * RL_B + j];
+        }
+        batch(xb, g + RL_B);
+    }
+    if (g + RL_B <= ngroups) {  // xa holds groups g..g+RL_B-1
+        batch(xa, g);
+        g += RL_B;
+    }
+    for (; g < ngroups; ++g) {  // the last < RL_B groups
+        const float4 xv = xr[g], w4 = wr[g];
+        const float p0 = xv.x * w4.x, p1 = xv.y * w4.y, p2 = xv.z * w4.z, p3 = xv.w * w4.w;
+        s += ((p0 + p1) + p2) + p3;
+    }
+    if (t < N && e0 + el < ne) logits[(size_t)t * ne + e0 + el] = s;
+}
+
+__global__ void __launch_bounds__(256) k_route_finish(const float* __restrict__ logits, const float* __restrict__ bias,
+                                                      float* __restrict__ probs, int32_t* __restrict__ idx,
+                                                      float* __restrict__ wout, int N, int ne, int K) {
+    __shared__ float sp_all[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= N) return;  // whole wave (route_finish is wave-local)
+    float* sp = sp_all[wave];
+    if (lane < ne) sp[lane] = logits[(size_t)t * ne + lane];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    route_finish(sp, bias, ne, K, t, idx, wout, probs);
+}
+
 // router launch: one block per token, or the two-kernel form for a large
 // router matrix and few tokens
 static int launch_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w,
@@ -315,6 +399,24 @@ static int launch_route(const float* x, const float* rw, const float* bias, floa
         hipLaunchKernelGGL(k_route_select, dim3(N), dim3(64), 0, stream(), terms, ngroups, ne, K, bias, idx, w,
                            probs);
         GH_LAUNCHED("k_route_terms/select");
+        return GH_OK;
+    }
+    const size_t rl_lds = (size_t)RL_E * (d / 4 + 1) * 16;
+    if (N > 8 && !nw && ne <= 64 && K <= 8 && d % 4 == 0 && rl_lds <= 160 * 1024) {
+        static bool configured = false;
+        if (!configured) {
+            const hipError_t e = hipFuncSetAttribute((const void*)k_route_logits,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            if (e != hipSuccess) return fail(GH_EHIP, "k_route_logits LDS attribute: %s", hipGetErrorString(e));
+            configured = true;
+        }
+        float* lg = (float*)workspace(WS_MOE_TERMS, (size_t)N * ne * 4);
+        if (!lg) return fail(GH_ENOMEM, "moe route: workspace");
+        hipLaunchKernelGGL(k_route_logits, dim3(cdiv(ne, RL_E), cdiv(N, RL_T)), dim3(512), rl_lds, stream(), x, rw,
+                           lg, N, d, ne);
+        hipLaunchKernelGGL(k_route_finish, dim3(cdiv(N, 4)), dim3(256), 0, stream(), lg, bias, probs, idx, w, N, ne,
+                           K);
+        GH_LAUNCHED("k_route_logits/finish");
         return GH_OK;
     }
     hipLaunchKernelGGL(k_route, dim3(N), dim3(256), route_lds(d, ne, N), stream(), x, rw, bias, probs, idx, w, d, ne,
