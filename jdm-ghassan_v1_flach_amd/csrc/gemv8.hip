@@ -1,0 +1,172 @@
+// Q4_K GEMV for 2..8 tokens (batched decode): y[t][n] = sum_k x[t][k] w[n][k],
+// linear_forward_q4 (core/ops.cpp:360-408) at M <= 8.
+//
+// The weights are dequantised to fp16 in registers (the reference's CPU path
+// rounds every dequantised weight to fp16, core/ops.cpp:304-338) and
+// multiplied on the matrix cores as a dense 16-row GEMM: A row 2t + e is
+// token t's activation part e (x = hi + lo, two fp16 numbers, so the products
+// keep ~22 bits of each activation), so one v_mfma_f32_16x16x32_f16 per
+// 32-value sub-block covers all 8 tokens of 16 weight rows. Lane (n, g) holds
+// B = 8 weights of row n (values 8g..8g+7 of the sub-block) and receives
+// D[4g..4g+3][n] = the hi and lo parts of tokens 2g and 2g+1.
+//
+// Work split: a tile is 16 rows; wave w of a block owns super-blocks
+// SBW w .. SBW w + SBW - 1 of every tile (its A operands stay in registers
+// for the whole launch); blocks are persistent and walk tiles b, b + G, ...
+// with the next tile's bytes requested before the current one is decoded.
+// Per tile the waves' partial sums meet in LDS and are added in wave order.
+// Weight values: (1024 + q) is made an fp16 number by one v_and_or_b32 per
+// pair of codes, then q d sc - dmin m = (1024 + q) s + nb with s = d sc,
+// nb = -(1024 s + dmin m), rounded to fp16.
+#include <stdlib.h>
+
+#include "gemm_tile.h"
+
+namespace gh {
+
+typedef float g8_f4 __attribute__((ext_vector_type(4)));
+
+struct G8Raw {  // one super-block of one row, this lane's part: header + 4 x 8 bytes
+    uint4 hd;
+    uint2 q[4];
+};
+
+template <int SBW>
+__global__ void __launch_bounds__(512) k_gemv8_q4k(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                    float* __restrict__ y, int M, int K, int N, size_t rowb) {
+    __shared__ float red[2][8][8][16];  // [buf][wave][token][row]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, WB = blockDim.x >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int ntiles = (N + 15) >> 4;
+    // ---- A operands of this wave's super-blocks: row n16 = token n16/2, part n16%2;
+    // values 32 j + 8 g + {0,2,1,3,4,6,5,7} (the order the codes come out of a dword)
+    f16x8 A[SBW][8];
+    {
+        const int t = n16 >> 1, part = n16 & 1;
+        const bool live = t < M;
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+            const int k0 = (wave * SBW + s) * 256 + 8 * g;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (live) {
+                    const float4* p = (const float4*)(x + (size_t)t * K + k0 + 32 * j);
+                    v0 = p[0];
+                    v1 = p[1];
+                }
+                const float v[8] = {v0.x, v0.z, v0.y, v0.w, v1.x, v1.z, v1.y, v1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 hi = (_Float16)v[e];
+                    A[s][j][e] = part ? (_Float16)(v[e] - (float)hi) : hi;
+                }
+            }
+        }
+    }
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    auto load = [&](int tile, G8Raw (&r)[SBW]) {
+        int n = tile * 16 + n16;
+        n = n < N ? n : N - 1;
+        const uint8_t* row = W + (size_t)n * rowb;
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+            const uint8_t* sb = row + (size_t)(wave * SBW + s) * 144;
+            r[s].hd = *(const uint4*)sb;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) r[s].q[p] = *(const uint2*)(sb + 16 + 32 * p + 8 * g);
+        }
+    };
+    G8Raw ra[SBW], rb[SBW];
+    int tile = blockIdx.x;
+    if (tile < ntiles) load(tile, ra);
+    int buf = 0;
+    auto run = [&](int tl, G8Raw (&cur)[SBW], G8Raw (&nxt)[SBW]) {
+        if (tl + (int)gridDim.x < ntiles) load(tl + gridDim.x, nxt);
+        g8_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+            const uint4 hd = cur[s].hd;
+            const float d = f16_to_f32((uint16_t)(hd.x & 0xFFFF)), dm = f16_to_f32((uint16_t)(hd.x >> 16));
+            const uint32_t sc4[3] = {hd.y, hd.z, hd.w};
+            auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                int scv, mv;
+                if (j < 4) {
+                    scv = scb(j) & 63;
+                    mv = scb(j + 4) & 63;
+                } else {
+                    scv = (scb(j + 4) & 0xF) | ((scb(j - 4) >> 6) << 4);
+                    mv = (scb(j + 4) >> 4) | ((scb(j) >> 6) << 4);
+                }
+                const float sc = d * (float)scv, nb = -fmaf(1024.f, sc, dm * (float)mv);
+                const int p = j >> 1, sh = 4 * (j & 1);  // sub-block 2p: low nibbles, 2p+1: high
+                const uint32_t u0 = cur[s].q[p].x >> sh, u1 = cur[s].q[p].y >> sh;
+                const uint32_t c[4] = {gq_and_or(u0, 0x000F000Fu, magic), gq_and_or(u0 >> 8, 0x000F000Fu, magic),
+                                       gq_and_or(u1, 0x000F000Fu, magic), gq_and_or(u1 >> 8, 0x000F000Fu, magic)};
+                f16x8 b;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    b[2 * i] = (_Float16)fmaf(gq_lo(c[i]), sc, nb);
+                    b[2 * i + 1] = (_Float16)fmaf(gq_hi(c[i]), sc, nb);
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[s][j], b, acc, 0, 0, 0);
+            }
+        }
+        // tokens 2g, 2g+1 of row n16: hi + lo parts
+        red[buf][wave][2 * g][n16] = acc[0] + acc[1];
+        red[buf][wave][2 * g + 1][n16] = acc[2] + acc[3];
+        __syncthreads();
+        for (int i = tid; i < 128; i += blockDim.x) {  // a one-wave block has 64 threads for 128 sums
+            const int t = i >> 4, nn = i & 15, n = tl * 16 + nn;
+            float v = 0.f;
+            for (int w = 0; w < WB; ++w) v += red[buf][w][t][nn];
+            if (t < M && n < N) y[(size_t)t * N + n] = v;
+        }
+        buf ^= 1;
+    };
+    while (tile < ntiles) {
+        run(tile, ra, rb);
+        tile += gridDim.x;
+        if (tile >= ntiles) break;
+        run(tile, rb, ra);
+        tile += gridDim.x;
+    }
+}
+
+template <int SBW>
+static int g8_launch(const float* x, const void* w, float* y, int M, int K, int N) {
+    const int WB = K / (256 * SBW);
+    static int per_cu[17];
+    if (!per_cu[WB]) {
+        int nb = 0;
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv8_q4k<SBW>, 64 * WB, 0);
+        per_cu[WB] = e == hipSuccess && nb > 0 ? nb : 1;
+    }
+    const int ntiles = (N + 15) / 16;
+    const int slots = per_cu[WB] * num_cus();
+    hipLaunchKernelGGL(k_gemv8_q4k<SBW>, dim3(ntiles < slots ? ntiles : slots), dim3(64 * WB), 0, stream(), x,
+                       (const uint8_t*)w, y, M, K, N, row_bytes(3, K));
+    GH_LAUNCHED("k_gemv8_q4k");
+    return GH_OK;
+}
+
+// Returns 1 if handled: Q4_K, 2 <= M <= 8, K a multiple of 256 up to 4096.
+int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
+    static const int enabled = [] {
+        const char* e = getenv("GH_GEMV8");
+        return e ? atoi(e) : 1;
+    }();
+    if (!enabled || kind != 3 || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
+    const int nsb = K / 256;
+    // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands and two tiles of
+    // weight bytes stay in registers)
+    if (nsb <= 8) *rc = g8_launch<1>(x, w, y, M, K, N);
+    else if (nsb % 2 == 0 && nsb <= 16) *rc = g8_launch<2>(x, w, y, M, K, N);
+    else return 0;
+    return 1;
+}
+
+}  // namespace gh

@@ -1046,7 +1046,10 @@ static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N,
 // Returns 1 if handled (Q4_K / Q8_0, 1 <= M <= 8, K a multiple of 256).
 // Token groups whose activations do not fit LDS together are run as
 // separate launches over the same weights.
+int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc);  // gemv8.hip
+
 int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
+    if (gemv8_dispatch(x, w, y, M, K, N, kind, rc)) return 1;
     static const int enabled = env_int("GH_GEMV_MFMA", 1);
     static const int dma = env_int("GH_GEMV_DMA", 1);  // 0 off, else the variant of gemv_q4k_i8
     if (enabled && dma && M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
