@@ -85,31 +85,15 @@ constexpr int ROUTE_RB = 8;  // float4 weight loads per thread per batch
 // (normalised) row stays in sx [d] (LDS) and is also written to xn when
 // given. term: LDS [ne][GW + 1]. sel_lds (LDS [K], optional) receives the
 // selected experts; idx / wout / probs (global) may be null.
-__device__ __forceinline__ void route_token(const float* __restrict__ x, const float* __restrict__ rw, const float* __restrict__ bias,
-                            float* __restrict__ probs, int32_t* __restrict__ idx, float* __restrict__ wout, int d,
-                            int ne, int K, const float* __restrict__ nw, float eps, float* __restrict__ xn, int GW,
-                            int t, float* sx, float* term, int* sel_lds) {
-#pragma clang fp contract(off)
-    const int ngroups = d / 4, ts = GW + 1;
-    __shared__ float sp[64];
+// Token row t of x into sx [d] (LDS), RMS-normalised when nw is given
+// (elementwise.hip k_rmsnorm arithmetic: double sum of squares) and written
+// to xn when given. A block of 256 threads; every caller gets bit-identical
+// values (the same loads, sums and order).
+__device__ __forceinline__ void route_norm(const float* __restrict__ x, int t, int d, const float* __restrict__ nw,
+                                           float eps, float* __restrict__ xn, float* sx) {
     __shared__ double dred[4];
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, ngroups = d / 4;
     const float4* xt = (const float4*)(x + (size_t)t * d);
-    const float4* rw4 = (const float4*)rw;
-    auto widx = [&](int q, int g0, int gw) {  // pair q of a window -> float4 index in rw
-        const int e = q / gw;
-        return e * ngroups + g0 + (q - e * gw);
-    };
-    // first batch of router weights, requested with the activations
-    float4 wreg[ROUTE_RB];
-    {
-        const int gw = min(GW, ngroups);
-#pragma unroll
-        for (int b = 0; b < ROUTE_RB; ++b) {
-            const int q = tid + b * 256;
-            if (q < ne * gw) wreg[b] = rw4[widx(q, 0, gw)];
-        }
-    }
     double ss = 0.0;
     for (int g = tid; g < ngroups; g += 256) {
         const float4 v = xt[g];
@@ -130,6 +114,32 @@ __device__ __forceinline__ void route_token(const float* __restrict__ x, const f
         }
     }
     __syncthreads();
+}
+
+__device__ __forceinline__ void route_token(const float* __restrict__ x, const float* __restrict__ rw, const float* __restrict__ bias,
+                            float* __restrict__ probs, int32_t* __restrict__ idx, float* __restrict__ wout, int d,
+                            int ne, int K, const float* __restrict__ nw, float eps, float* __restrict__ xn, int GW,
+                            int t, float* sx, float* term, int* sel_lds) {
+#pragma clang fp contract(off)
+    const int ngroups = d / 4, ts = GW + 1;
+    __shared__ float sp[64];
+    const int tid = threadIdx.x;
+    const float4* rw4 = (const float4*)rw;
+    auto widx = [&](int q, int g0, int gw) {  // pair q of a window -> float4 index in rw
+        const int e = q / gw;
+        return e * ngroups + g0 + (q - e * gw);
+    };
+    // first batch of router weights, requested with the activations
+    float4 wreg[ROUTE_RB];
+    {
+        const int gw = min(GW, ngroups);
+#pragma unroll
+        for (int b = 0; b < ROUTE_RB; ++b) {
+            const int q = tid + b * 256;
+            if (q < ne * gw) wreg[b] = rw4[widx(q, 0, gw)];
+        }
+    }
+    route_norm(x, t, d, nw, eps, xn, sx);
     float s = 0.0f;  // lane e < ne owns logit e
     for (int g0 = 0; g0 < ngroups; g0 += GW) {
         const int gw = min(GW, ngroups - g0), np = ne * gw;
@@ -558,14 +568,34 @@ struct GemvJobs {
     int ne, gw;
     int32_t* ridx;
     float* rwout;
+    // gate/up of EVERY expert (small expert sets): activations [N][ne][rows_r]; the down
+    // kernel then gathers the rows of the selected experts (0: rows in slot order)
+    int gather_ne;
 };
 
-template <int KIND, bool DUAL, bool ROUTE = false>
+// ALLEXP (small expert sets, decode): jobs 0..N*ne-1 are (token j/ne, expert
+// j%ne) for every expert, N*ne.. the shared experts, and the last N rows of
+// blocks route token j (block x = 0 only, writing idx / w): the routing runs
+// beside the GEMVs instead of in front of them, and the down kernel gathers
+// the selected experts' activations.
+template <int KIND, bool DUAL, bool ROUTE = false, bool ALLEXP = false>
 __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
-    const int job = blockIdx.y;
-    const bool shared = job >= J.S;
+    int job = blockIdx.y;
+    if constexpr (ALLEXP) {
+        const int nall = J.N * J.ne;  // J.N = tokens here (shared experts required)
+        if (job >= nall + J.N) {
+            if (blockIdx.x != 0) return;
+            extern __shared__ float msm_r[];
+            const int token = job - nall - J.N;
+            route_token(J.rx, J.rw, J.rbias, nullptr, J.ridx, J.rwout, J.d, J.ne, J.K, J.rnw, J.reps, nullptr, J.gw,
+                        token, msm_r, msm_r + J.d, nullptr);
+            return;
+        }
+    }
+    const bool shared = ALLEXP ? job >= J.N * J.ne : job >= J.S;
     extern __shared__ float msm[];  // ROUTE: token row [d] | router terms
     __shared__ int ssel[8];
+    if (ALLEXP && shared) job = J.S + (job - J.N * J.ne);  // shared jobs keep their usual numbering
     const int rows = shared ? J.rows_s : J.rows_r;
     const int kin = shared ? J.kin_s : J.kin_r;
     const size_t rowb = shared ? J.rowb_s : J.rowb_r;
@@ -573,6 +603,11 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     int LPR = 64;
     while (LPR > 1 && LPR > T) LPR >>= 1;
     const int RP = 64 / LPR;
+    if (ALLEXP) {
+        if (blockIdx.x * 4 * RP >= rows) return;
+        extern __shared__ float msm_n[];
+        route_norm(J.rx, shared ? job - J.S : job / J.ne, J.d, J.rnw, J.reps, nullptr, msm_n);
+    }
     if (ROUTE) {
         if (blockIdx.x * 4 * RP >= rows) return;  // no rows here (block 0, the writer, always has some)
         // every block routes its token (identical arithmetic, so all agree); the normalised row
@@ -591,12 +626,13 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     const uint8_t *Wa, *Wb = nullptr;
     if (shared) {
         const int t = job - J.S;
-        xin = ROUTE ? msm : (DUAL ? J.x + (size_t)t * J.d : J.in_s + (size_t)t * kin);
+        xin = (ROUTE || ALLEXP) ? msm : (DUAL ? J.x + (size_t)t * J.d : J.in_s + (size_t)t * kin);
         Wa = J.sa;
         if (DUAL) Wb = J.sb;
     } else {
-        const int e = ROUTE ? ssel[job % J.K] : J.idx[job];
-        xin = ROUTE ? msm : (DUAL ? J.x + (size_t)(job / J.K) * J.d : J.x + (size_t)job * kin);
+        const int e = ALLEXP ? job % J.ne : ROUTE ? ssel[job % J.K] : J.idx[job];
+        const int tok = ALLEXP ? job / J.ne : job / J.K;
+        xin = (ROUTE || ALLEXP) ? msm : (DUAL ? J.x + (size_t)tok * J.d : J.x + (size_t)job * kin);
         Wa = J.wa + (size_t)e * J.estride;
         if (DUAL) Wb = J.wb + (size_t)e * J.estride;
     }
@@ -660,10 +696,18 @@ __global__ void __launch_bounds__(256) k_moe_down_combine(GemvJobs J, const floa
     const int sh_len = has_sh ? J.kin_s : 0;
     {
         const float4* src_s = (const float4*)(J.in_s + (size_t)tok * J.kin_s);
-        const float4* src_r = (const float4*)(J.x + (size_t)tok * K * J.kin_r);
-        const int n4s = sh_len / 4, n4 = n4s + K * J.kin_r / 4;
-        for (int i = threadIdx.x; i < n4; i += 256)
-            ((float4*)dc_act)[i] = i < n4s ? src_s[i] : src_r[i - n4s];
+        const int kq = J.kin_r / 4;
+        const int n4s = sh_len / 4, n4 = n4s + K * kq;
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            if (i < n4s) {
+                ((float4*)dc_act)[i] = src_s[i];
+            } else {
+                // routed k: its slot's row, or (all experts computed) the row of its expert
+                const int q = i - n4s, kk = q / kq, o = q - kk * kq;
+                const size_t r = J.gather_ne ? (size_t)tok * J.gather_ne + J.idx[tok * K + kk] : (size_t)tok * K + kk;
+                ((float4*)dc_act)[i] = ((const float4*)(J.x + r * J.kin_r))[o];
+            }
+        }
     }
     auto load_job = [&](int j, uint32_t (*w)[DW]) {
         const bool shared = j < 0;
@@ -1173,7 +1217,7 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     const size_t rowb_SH = KIND == 4 ? (size_t)SH * 2 : row_bytes(KIND, SH);
     char* r = (char*)workspace(WS_MOE_ROUTE, (size_t)S * 8);
     float* xn = (float*)workspace(WS_MOE_XG, (size_t)N * d * 4);
-    float* act = (float*)workspace(WS_MOE_ACT, (size_t)S * E * 4);
+    float* act = (float*)workspace(WS_MOE_ACT, (size_t)N * (ne > K ? ne : K) * E * 4);
     float* sh_act = (float*)workspace(WS_MOE_SHARED, (size_t)N * ((size_t)SH + d) * 4);
     if (!r || !xn || !act || !sh_act) return fail(GH_ENOMEM, "moe: workspace");
     int32_t* idx = (int32_t*)r;
@@ -1182,6 +1226,13 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     const int gw = route_window(d, ne, N);
     const size_t rlds = route_lds(d, ne, N);
     const bool fused_route = K <= 8 && gw >= d / 4 && rlds <= 32 * 1024 && (size_t)ne * d <= 16384;
+    // small expert sets: every expert's gate/up is computed (at most a few MB of weights) so the
+    // routing runs beside the GEMVs instead of in front of them
+    static const int allexp_on = [] {
+        const char* e = getenv("GH_MOE_ALLEXP");
+        return e ? atoi(e) : 1;
+    }();
+    const bool allexp = allexp_on && fused_route && has_sh && ne > K && (size_t)ne * E * d <= ((size_t)4 << 20);
     if (!fused_route) {
         const int rc = launch_route(xres, rw, bias, nullptr, idx, w, N, d, ne, K, nw, eps, xn);
         if (rc) return rc;
@@ -1199,7 +1250,12 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     };
     const int maxrows = has_sh ? (E > SH ? E : SH) : E;
     const dim3 g1(cdiv(maxrows, rows_per_block(d)), S + J.N);
-    if (fused_route) {
+    if (allexp) {
+        J.rx = xres; J.rw = rw; J.rbias = bias; J.rnw = nw; J.reps = eps; J.ne = ne; J.gw = gw;
+        J.ridx = idx; J.rwout = w;
+        const dim3 ga(g1.x, N * ne + N + N);  // every expert, the shared experts, the routers
+        hipLaunchKernelGGL((k_moe_gemv<KIND, true, false, true>), ga, dim3(256), rlds, stream(), J);
+    } else if (fused_route) {
         J.rx = xres; J.rw = rw; J.rbias = bias; J.rnw = nw; J.reps = eps; J.ne = ne; J.gw = gw;
         J.ridx = idx; J.rwout = w;
         hipLaunchKernelGGL((k_moe_gemv<KIND, true, true>), g1, dim3(256), rlds, stream(), J);
@@ -1208,6 +1264,7 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     }
     GH_LAUNCHED("k_moe_gemv(gate/up)");
     GemvJobs D{};
+    D.gather_ne = allexp ? ne : 0;
     D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
     D.wa = (const uint8_t*)downs; D.estride = (size_t)d * rowb_E; D.sa = (const uint8_t*)sh_d;
     D.rows_r = d; D.rows_s = d; D.kin_r = E; D.kin_s = SH; D.rowb_r = rowb_E; D.rowb_s = rowb_SH;
