@@ -135,7 +135,8 @@ def kernel_suite(gh):
                                10 if M > 8 else 200)
             tag = f"c2_{kname}_M{M}_{N}x{K}"
             if M <= 8:
-                kern = "k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else "k_gemv_mfma"
+                kern = ("k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else
+                        "k_gemv8_q4k" if (kind == 3 and 2 <= M <= 8 and K <= 4096) else "k_gemv_mfma")
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
                 res[tag] = entry("k_to_f16+k_gemm_q4", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
