@@ -762,6 +762,97 @@ __global__ void __launch_bounds__(256) k_moe_down_combine(GemvJobs J, const floa
     }
 }
 
+// Down projections with the jobs side by side: block = (16 output rows,
+// token), wave 0 = the shared expert, wave 1 + k = routed slot k. Every wave
+// requests its own weight bytes as soon as it knows its expert (the shared
+// wave at once), multiplies 16 rows x its job's K range (4 lanes per row,
+// DP_TPL tasks per lane at most), and leaves its 16 row results in LDS; the
+// block then merges them in the combine order (shared first, then k = 0..K-1,
+// core/moe_cpu.cpp:265-287) and adds the sum to the residual row.
+// Activations in LDS: shared [kin_s] | routed k [kin_r] (or, after the
+// all-expert gate/up, the selected experts' rows).
+constexpr int DP_RB = 16, DP_LPR = 4, DP_TPL = 4;
+template <int KIND>
+__global__ void __launch_bounds__(576) k_moe_down_par(GemvJobs J, const float* __restrict__ wroute,
+                                                      float* __restrict__ xres, int accumulate) {
+    constexpr int DW = Task<KIND>::DW;
+    extern __shared__ float dp_act[];
+    __shared__ float dp_res[9][DP_RB];
+    const int tok = blockIdx.y, K = J.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % DP_LPR, rloc = lane / DP_LPR;
+    const int rows = J.rows_r;
+    const int row = blockIdx.x * DP_RB + rloc;
+    const int rr = row < rows ? row : rows - 1;
+    const bool shared = wave == 0;
+    const int k = wave - 1;
+    const int e = shared ? 0 : J.idx[tok * K + k];
+    const int T = (shared ? J.kin_s : J.kin_r) / 64;
+    const size_t rowb = shared ? J.rowb_s : J.rowb_r;
+    const uint8_t* base = (shared ? J.sa : J.wa + (size_t)e * J.estride) + (size_t)rr * rowb;
+    uint32_t w[DP_TPL][DW];
+#pragma unroll
+    for (int q = 0; q < DP_TPL; ++q) {
+        const int t = sub + q * DP_LPR;
+        if (t < T) load_task<KIND>(base, t, w[q]);
+    }
+    {
+        const float4* src_s = (const float4*)(J.in_s + (size_t)tok * J.kin_s);
+        const int kq = J.kin_r / 4;
+        const int n4s = J.kin_s / 4, n4 = n4s + K * kq;
+        for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+            if (i < n4s) {
+                ((float4*)dp_act)[i] = src_s[i];
+            } else {
+                const int q = i - n4s, kk = q / kq, o = q - kk * kq;
+                const size_t r = J.gather_ne ? (size_t)tok * J.gather_ne + J.idx[tok * K + kk] : (size_t)tok * K + kk;
+                ((float4*)dp_act)[i] = ((const float4*)(J.x + r * J.kin_r))[o];
+            }
+        }
+    }
+    __syncthreads();
+    const float* xin = shared ? dp_act : dp_act + J.kin_s + (size_t)k * J.kin_r;
+    float ga = 0.f;
+#pragma unroll
+    for (int q = 0; q < DP_TPL; ++q) {
+        const int t = sub + q * DP_LPR;
+        if (t < T) {
+            float xv[64];
+            const float4* xp = (const float4*)(xin + (size_t)t * 64);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float4 v = xp[i];
+                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            }
+            float xs[2];
+            task_xsum<KIND>(xv, xs);
+            ga += task_dot<KIND>(w[q], xv, xs, t);
+        }
+    }
+    ga = group_sum(ga, DP_LPR);
+    if (sub == 0) dp_res[wave][rloc] = ga;
+    __syncthreads();
+    if (threadIdx.x < DP_RB) {
+        const int r = blockIdx.x * DP_RB + threadIdx.x;
+        float acc = dp_res[0][threadIdx.x];
+        for (int kk = 0; kk < K; ++kk) acc += wroute[tok * K + kk] * dp_res[1 + kk][threadIdx.x];
+        if (r < rows) {
+            float* o = xres + (size_t)tok * rows + r;
+            *o = accumulate ? *o + acc : acc;
+        }
+    }
+}
+
+template <int KIND>
+static bool down_par_fits(bool has_sh, int K, int E, int SH) {
+    static const int on = [] {
+        const char* e = getenv("GH_MOE_DOWN_PAR");
+        return e ? atoi(e) : 1;
+    }();
+    return on && KIND != 4 && has_sh && K <= 8 && E % 64 == 0 && SH % 64 == 0 && E / 64 <= DP_LPR * DP_TPL &&
+           SH / 64 <= DP_LPR * DP_TPL;
+}
+
 // lanes per row of the fused down kernel: the smallest job's task count
 // (capped at 64), raised until every job fits DC_TPJ tasks per lane
 static int down_lpr(int E, int SH, bool has_sh) {
@@ -1110,8 +1201,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             GH_LAUNCHED("k_moe_combine");
             return GH_OK;
         }
-        hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w_route,
-                           out, LPR, 0);
+        if (down_par_fits<KIND>(has_sh, K, E, SH)) {
+            hipLaunchKernelGGL((k_moe_down_par<KIND>), dim3(cdiv(d, DP_RB), N), dim3(64 * (K + 1)), lds, stream(), D,
+                               w_route, out, 0);
+        } else {
+            hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w_route,
+                               out, LPR, 0);
+        }
         GH_LAUNCHED("k_moe_down_combine");
         return GH_OK;
     }
@@ -1272,8 +1368,13 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     const int LPR = down_lpr(E, SH, has_sh);
     const int rpb = 4 * (64 / LPR);
     const size_t lds = ((has_sh ? (size_t)SH : 0) + (size_t)K * E) * 4;
-    hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w, xres, LPR,
-                       1);
+    if (down_par_fits<KIND>(has_sh, K, E, SH)) {
+        hipLaunchKernelGGL((k_moe_down_par<KIND>), dim3(cdiv(d, DP_RB), N), dim3(64 * (K + 1)), lds, stream(), D, w,
+                           xres, 1);
+    } else {
+        hipLaunchKernelGGL((k_moe_down_combine<KIND>), dim3(cdiv(d, rpb), N), dim3(256), lds, stream(), D, w, xres,
+                           LPR, 1);
+    }
     GH_LAUNCHED("k_moe_down_combine");
     return GH_OK;
 }
