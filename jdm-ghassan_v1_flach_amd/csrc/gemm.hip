@@ -22,6 +22,8 @@
 
 namespace gh {
 
+int launch_add_to(float* y, const float* t, int64_t n);
+
 template <int KIND>
 __global__ void __launch_bounds__(256) k_gemm_q(const float* __restrict__ X, const uint8_t* __restrict__ W,
                                                 float* __restrict__ Y, int M, int K, int N, size_t rowb) {
@@ -138,7 +140,7 @@ __global__ void k_to_f16(const float* __restrict__ x, uint16_t* __restrict__ y, 
 
 template <int KIND>
 __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb) {
+                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb, int Ts) {
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDS_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -169,17 +171,19 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int T = K / BK;
+    // K steps [tb, te) of split blockIdx.y; splits write partial tiles at Y + split * M * N
+    const int tb = blockIdx.y * Ts, te = min(K / BK, tb + Ts);
+    Y += (size_t)blockIdx.y * M * N;
     uint32_t magic = 0x64006400u;
     asm volatile("" : "+v"(magic));
 
     gh_u32x4v xa[4];
     WLoad<KIND> wl;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + ac);
-    wl.load(wrow, 0, lh);
+    for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + (size_t)tb * BK + ac);
+    wl.load(wrow, tb, lh);
     int buf = 0;
-    for (int t = 0; t < T; ++t, buf ^= 1) {
+    for (int t = tb; t < te; ++t, buf ^= 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             gh_u32x4v v = xa[i];
@@ -198,7 +202,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__
             }
         }
         __syncthreads();
-        if (t + 1 < T) {
+        if (t + 1 < te) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) xa[i] = *(const gh_u32x4v*)(xrows[i] + (size_t)(t + 1) * BK + ac);
             wl.load(wrow, t + 1, lh);
@@ -233,6 +237,16 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__
                 if (row < M) Y[(size_t)row * N + col] = acc[i][j][e];
             }
         }
+}
+
+// y = sum of the S split partials, in split order (deterministic); with
+// `accumulate` the sum is added to y (the residual add of the caller).
+__global__ void k_splitk_sum(const float* __restrict__ part, float* __restrict__ y, int64_t n, int S, int accumulate) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int s = 1; s < S; ++s) v += part[(size_t)s * n + i];
+        y[i] = accumulate ? y[i] + v : v;
+    }
 }
 
 // ---------------------------------------------------------------- v4
@@ -530,13 +544,37 @@ int launch_to_f16(const float* x, uint16_t* y, int64_t n) {
     return GH_OK;
 }
 
+__global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] += t[i];
+}
+
+// y = x W^T, or y += x W^T with `accumulate` (the split-K sum adds in place; the other paths
+// write a temporary that one more launch adds)
 template <int KIND>
-static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {
+static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate) {
     uint16_t* x16 = (uint16_t*)workspace(WS_GEMM_X, (size_t)M * K * 2);
     if (!x16) return fail(GH_ENOMEM, "gemm: workspace");
     const int64_t n4 = (int64_t)M * K / 4;
     hipLaunchKernelGGL(k_to_f16, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 8192)), dim3(256), 0, stream(), x,
                        x16, n4);
+    float* yout = y;  // where the product goes; with accumulate outside the split-K path: a temporary
+    auto finish_acc = [&]() -> int {
+        if (yout == y) return GH_OK;
+        const int64_t n = (int64_t)M * N;
+        hipLaunchKernelGGL(k_add_to, dim3((unsigned)std::min<int64_t>(cdiv64(n, 256), 2048)), dim3(256), 0, stream(), y,
+                           yout, n);
+        GH_LAUNCHED("k_add_to");
+        return GH_OK;
+    };
+    {
+        const int blocks = cdiv(M, BM) * cdiv(N, BN), T = K / BK;
+        const bool will_split = 2 * blocks <= num_cus() && T >= 4;
+        if (accumulate && !will_split) {
+            yout = (float*)workspace(WS_GEMM_ACC, (size_t)M * N * 4);
+            if (!yout) return fail(GH_ENOMEM, "gemm: workspace");
+        }
+    }
     if constexpr (KIND == 2 || KIND == 3) {
         static const int v4 = [] {
             const char* e = getenv("GH_GEMM_V4");
@@ -545,7 +583,7 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
         const int tiles = cdiv(M, G4M) * cdiv(N, G4N), T = K / 64;
         // 256x256 tiles once they fill the chip (split K in two when that is needed to fill it)
         const int split = tiles >= num_cus() ? 1 : (2 * tiles >= num_cus() && T % 4 == 0) ? 2 : 0;
-        if (v4 && K % 256 == 0 && split && (split == 1 || ((size_t)M * N % 4 == 0 && ((uintptr_t)y & 15) == 0))) {
+        if (v4 && K % 256 == 0 && split && (split == 1 || ((size_t)M * N % 4 == 0 && ((uintptr_t)yout & 15) == 0))) {
             static bool configured = false;
             if (!configured) {
                 const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4<KIND>,
@@ -556,22 +594,40 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
             if (split > 1) {
                 const int64_t n4 = (int64_t)M * N / 4;
                 hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 4096)), dim3(256), 0,
-                                   stream(), y, n4);
+                                   stream(), yout, n4);
             }
             hipLaunchKernelGGL(k_gemm_q4<KIND>, dim3(tiles, split), dim3(256), G4_LDS, stream(), x16,
-                               (const uint8_t*)w, y, M, K, N, rowb, T / split);
+                               (const uint8_t*)w, yout, M, K, N, rowb, T / split);
             GH_LAUNCHED("k_gemm_q4");
-            return GH_OK;
+            return finish_acc();
         }
     }
-    const int blocks = cdiv(M, BM) * cdiv(N, BN);
-    hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, (const uint8_t*)w, y, M, K, N,
-                       rowb);
+    const int blocks = cdiv(M, BM) * cdiv(N, BN), T = K / BK;
+    // few tiles (small M): split K so more blocks share the sequential K walk, partials summed in order
+    int S = 1;
+    if (2 * blocks <= num_cus() && T >= 4) {
+        S = std::min(T / 2, std::max(1, num_cus() / blocks));
+        S = cdiv(T, cdiv(T, S));
+    }
+    if (S > 1) {
+        const int Ts = cdiv(T, S);
+        float* part = (float*)workspace(WS_GEMM_PART, (size_t)S * M * N * 4);
+        if (!part) return fail(GH_ENOMEM, "gemm: split-K workspace");
+        hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks, S), dim3(256), 0, stream(), x16, (const uint8_t*)w, part, M,
+                           K, N, rowb, Ts);
+        const int64_t n = (int64_t)M * N;
+        hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)std::min<int64_t>(cdiv64(n, 256), 2048)), dim3(256), 0,
+                           stream(), part, y, n, S, accumulate);
+        GH_LAUNCHED("k_gemm_q2 (split K)");
+        return GH_OK;
+    }
+    hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, (const uint8_t*)w, yout, M, K, N,
+                       rowb, T);
     GH_LAUNCHED("k_gemm_q2");
-    return GH_OK;
+    return finish_acc();
 }
 
-int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int accumulate) {
     const int blocks = cdiv(M, BM) * cdiv(N, BN);
     size_t rowb = kind == 4 ? (size_t)K * 2 : kind == 5 ? (size_t)K * 4 : row_bytes(kind, K);
     const dim3 g(blocks), b(256);
@@ -581,21 +637,33 @@ int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, 
     }();
     if (v2 && (kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
         switch (kind) {
-            case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb);
-            case 3: return gemm2_launch<3>(x, w, y, M, K, N, rowb);
-            default: return gemm2_launch<4>(x, w, y, M, K, N, rowb);
+            case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb, accumulate);
+            case 3: return gemm2_launch<3>(x, w, y, M, K, N, rowb, accumulate);
+            default: return gemm2_launch<4>(x, w, y, M, K, N, rowb, accumulate);
         }
     }
+    float* yo = y;
+    if (accumulate) {
+        yo = (float*)workspace(WS_GEMM_ACC, (size_t)M * N * 4);
+        if (!yo) return fail(GH_ENOMEM, "gemm: workspace");
+    }
     switch (kind) {
-        case 0: hipLaunchKernelGGL(k_gemm_q<0>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
-        case 1: hipLaunchKernelGGL(k_gemm_q<1>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
-        case 2: hipLaunchKernelGGL(k_gemm_q<2>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
-        case 3: hipLaunchKernelGGL(k_gemm_q<3>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
-        case 4: hipLaunchKernelGGL(k_gemm_q<4>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
-        case 5: hipLaunchKernelGGL(k_gemm_q<5>, g, b, 0, stream(), x, (const uint8_t*)w, y, M, K, N, rowb); break;
+        case 0: hipLaunchKernelGGL(k_gemm_q<0>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
+        case 1: hipLaunchKernelGGL(k_gemm_q<1>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
+        case 2: hipLaunchKernelGGL(k_gemm_q<2>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
+        case 3: hipLaunchKernelGGL(k_gemm_q<3>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
+        case 4: hipLaunchKernelGGL(k_gemm_q<4>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
+        case 5: hipLaunchKernelGGL(k_gemm_q<5>, g, b, 0, stream(), x, (const uint8_t*)w, yo, M, K, N, rowb); break;
         default: return fail(GH_EINVAL, "gemm: bad kind %d", kind);
     }
     GH_LAUNCHED("k_gemm_q");
+    return accumulate ? launch_add_to(y, yo, (int64_t)M * N) : GH_OK;
+}
+
+int launch_add_to(float* y, const float* t, int64_t n) {
+    hipLaunchKernelGGL(k_add_to, dim3((unsigned)std::min<int64_t>(cdiv64(n, 256), 2048)), dim3(256), 0, stream(), y, t,
+                       n);
+    GH_LAUNCHED("k_add_to");
     return GH_OK;
 }
 

@@ -231,5 +231,7 @@ enum WsSlot {
     WS_MOE_XG = 32,     // gathered rows for the grouped prefill GEMM
     WS_MOE_H = 33,
     WS_MOE_TERMS = 34,  // router group terms (large routers, few tokens)
+    WS_GEMM_PART = 35,  // split-K partial tiles of the small-M prefill GEMM
+    WS_GEMM_ACC = 36,   // product before an accumulating add (paths without an in-place sum)
 };
 }  // namespace gh

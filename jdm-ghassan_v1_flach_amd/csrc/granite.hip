@@ -38,7 +38,8 @@ int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, f
 int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
                        const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
                        float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
-                       int n_heads, int d_head, int d_state, int k, float eps, int kind);
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate);
+int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
 
 // decode control block (device ints)
 enum { CTL_TOKEN = 0, CTL_LEN = 1, CTL_START = 2, CTL_PINNED = 3, CTL_CAP = 4, CTL_SLOT = 5, CTL_STEP = 6, CTL_N = 8 };
@@ -507,11 +508,12 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
                 for (int t = 0; t < P; ++t) GHC(mamba_step(g, l, g->xb + (size_t)t * d, g->pr + (size_t)t * d));
             } else {
                 const std::string mp = pre + "mamba.";
+                // the residual add is folded into out_proj (x += ...)
                 GHC(mamba_forward_impl(g->xb, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
                                        g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"),
                                        g->F(mp + "D"), g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->ssm[l],
-                                       g->conv[l], g->pr, P, d, g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck,
-                                       g->eps, g->qkind));
+                                       g->conv[l], g->x, P, d, g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck,
+                                       g->eps, g->qkind, true));
             }
         } else {
             GHC(linear_any(g->xb, g->W(pre + "wq"), g->q, P, d, g->qd, g->qkind));
@@ -520,9 +522,9 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
             GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
             GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
             GHC(attention_prefill(g->q, g->k, g->v, g->att, 1, P, g->H, g->KV, g->hd, g->scale, 0));
-            GHC(linear_any(g->att, g->W(pre + "wo"), g->pr, P, g->qd, d, g->qkind));
+            GHC(linear_acc(g->att, g->W(pre + "wo"), g->x, P, g->qd, d, g->qkind));  // x += attn W_o^T
         }
-        GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        if (g->lt[l] == 0 && mamba_mode == 0) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, P, d, g->eps));
         GHC(moe_layer(g, l, g->xb, g->pr, P));
         GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));

@@ -23,6 +23,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
+int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
 
 __device__ __forceinline__ float softplus_ref(float v) {
     // core/mamba_cpu.cpp:139-140 (identity above 20)
@@ -514,7 +515,7 @@ __global__ void k_save_window(const float* __restrict__ proj, int proj_ld, int c
 int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
                        const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
                        float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
-                       int n_heads, int d_head, int d_state, int k, float eps, int kind) {
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate) {
     GH_REQUIRE(conv_dim - d_inner == 2 * d_state, "mamba: inconsistent conv_dim / d_state (n_groups must be 1)");
     GH_REQUIRE(n_heads * d_head == d_inner, "mamba: n_heads * d_head != d_inner");
     const int proj = d_inner + conv_dim + n_heads;
@@ -539,7 +540,8 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
     hipLaunchKernelGGL(k_gated_norm, dim3(T), dim3(256), 0, stream(), yb, d_inner, pr, proj, norm_w, normed, d_inner,
                        eps);
     GH_LAUNCHED("k_gated_norm");
-    return linear_any(normed, w_out, out, T, d_inner, d, kind);
+    return accumulate ? linear_acc(normed, w_out, out, T, d_inner, d, kind)
+                      : linear_any(normed, w_out, out, T, d_inner, d, kind);
 }
 
 // Single-token Mamba-2 layer as three launches: (1) [RMSNorm] + in_proj
@@ -615,7 +617,7 @@ int gh_mamba2_forward_half(const float* x, const void* w_in, const float* conv_w
     for (int b = 0; b < B; ++b) {
         int rc = mamba_forward_impl(x + (size_t)b * T * d, w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w, w_out,
                                     state + (size_t)b * n_heads * d_head * d_state, nullptr, out + (size_t)b * T * d,
-                                    T, d, d_inner, conv_dim, n_heads, d_head, d_state, k, eps, kind);
+                                    T, d, d_inner, conv_dim, n_heads, d_head, d_state, k, eps, kind, false);
         if (rc) return rc;
     }
     return GH_OK;

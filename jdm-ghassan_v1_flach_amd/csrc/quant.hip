@@ -266,7 +266,8 @@ int gemv_dispatch(const float* x, const void* w, float* y, int M, int K, int N, 
     return fail(GH_EINVAL, "gemv: bad kind %d", kind);
 }
 
-int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // gemm.hip
+int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int accumulate);  // gemm.hip
+int launch_add_to(float* y, const float* t, int64_t n);  // gemm.hip
 
 static bool g_fused_q4 = true;
 static const int kQuantSlots = 16;
@@ -286,7 +287,19 @@ int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int
     if (rc) return rc;
     if (M == 0 || N == 0) return GH_OK;
     if (M <= 8) return gemv_dispatch(x, w, y, M, K, N, kind);
-    return gemm_dispatch(x, w, y, M, K, N, kind);
+    return gemm_dispatch(x, w, y, M, K, N, kind, 0);
+}
+
+// y += x W^T (the residual add of a sublayer folded into its output projection)
+int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind) {
+    int rc = check_linear(x, w, y, M, K, N, kind);
+    if (rc) return rc;
+    if (M == 0 || N == 0) return GH_OK;
+    if (M > 8) return gemm_dispatch(x, w, y, M, K, N, kind, 1);
+    float* t = (float*)workspace(WS_GEMM_ACC, (size_t)M * N * 4);
+    if (!t) return fail(GH_ENOMEM, "linear: workspace");
+    rc = gemv_dispatch(x, w, t, M, K, N, kind);
+    return rc ? rc : launch_add_to(y, t, (int64_t)M * N);
 }
 
 int dequant_launch(const void* packed, int kind, int64_t n, void* out, bool to_f16) {
