@@ -798,12 +798,20 @@ __global__ void __launch_bounds__(256) k_kv_f16(const float* __restrict__ k, con
         sv[r][c4] = vv.x; sv[r][c4 + 1] = vv.y; sv[r][c4 + 2] = vv.z; sv[r][c4 + 3] = vv.w;
     }
     __syncthreads();
+    // V^T rows keep each 16-key group in MFMA k-slot order: slot s holds key
+    // 8((s & 7) >> 2) + 4(s >> 3) + (s & 3), the key the P operand carries in slot s (P comes
+    // from the S accumulator, whose lane holds keys 4h + i and 8 + 4h + i), so one 16-byte read
+    // of V^T is the B operand of the P.V MFMA
     _Float16* vd = Vt16 + ((size_t)b * KV + kvh) * HD * Tp + t0;
     for (int e = threadIdx.x; e < HD * (PF_BK / 8); e += 256) {
         const int c = e / (PF_BK / 8), r8 = (e % (PF_BK / 8)) * 8;
         f16x8 h8;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) h8[i] = (_Float16)sv[r8 + i][c];
+        for (int i = 0; i < 8; ++i) {
+            const int sl = (r8 & 15) + i;  // slot within the 16-key group
+            const int key = (r8 & ~15) + 8 * ((sl & 7) >> 2) + 4 * (sl >> 3) + (sl & 3);
+            h8[i] = (_Float16)sv[key][c];
+        }
         *(f16x8*)(vd + (size_t)c * Tp + r8) = h8;
     }
 }
@@ -824,6 +832,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
     constexpr int KPT = PF_BK * HD / 8 / 256;  // 16-byte pieces per thread (K), same for V^T
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][PF_BK * KS];
     __shared__ __attribute__((aligned(16))) _Float16 sVt[2][HD * VS];
+    __shared__ __attribute__((aligned(16))) float salpha[4][32];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const int nqt = cdiv(T, PF_BQ);
@@ -951,23 +960,28 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
         const bool moved = m_new != m_run;
         m_run = m_new;
         if (__ballot(moved)) {  // some row maximum moved: rescale (alpha = 1 for the others)
+            // the alphas of the wave's 32 rows through LDS: a lane needs rows 8j + 4hf + 0..3
+            if (hf == 0) salpha[wave][lane & 31] = alpha;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float ar = __shfl(alpha, 8 * (e >> 2) + 4 * hf + (e & 3), 64);
+            for (int j = 0; j < 4; ++j) {
+                const float4 a4 = *(const float4*)&salpha[wave][8 * j + 4 * hf];
+                const float ar[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
-                for (int c = 0; c < HD / 32; ++c) oacc[c][e] *= ar;
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int c = 0; c < HD / 32; ++c) oacc[c][4 * j + i] *= ar[i];
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int kb = 32 * (u >> 1) + 16 * (u & 1) + 4 * hf;
 #pragma unroll
             for (int c = 0; c < HD / 32; ++c) {
-                const _Float16* vrow = cV + (32 * c + (lane & 31)) * VS;
-                f16x8 vb8;
-                const f16x4 lo = *(const f16x4*)(vrow + kb), hi = *(const f16x4*)(vrow + kb + 8);
-                vb8[0] = lo[0]; vb8[1] = lo[1]; vb8[2] = lo[2]; vb8[3] = lo[3];
-                vb8[4] = hi[0]; vb8[5] = hi[1]; vb8[6] = hi[2]; vb8[7] = hi[3];
+                const f16x8 vb8 = *(const f16x8*)(cV + (32 * c + (lane & 31)) * VS + 16 * u + 8 * hf);
                 oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
             }
         }
