@@ -871,9 +871,12 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
     for (int s = 0; s < HD / 16; ++s) {
         if (qj < T) {
             const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
+            // q pre-multiplied by scale * log2(e): the scores come out of the MFMA in log2 units
             const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
-            qreg[s][0] = (_Float16)a0.x; qreg[s][1] = (_Float16)a0.y; qreg[s][2] = (_Float16)a0.z; qreg[s][3] = (_Float16)a0.w;
-            qreg[s][4] = (_Float16)a1.x; qreg[s][5] = (_Float16)a1.y; qreg[s][6] = (_Float16)a1.z; qreg[s][7] = (_Float16)a1.w;
+            const float c = scale * 1.4426950408889634f;
+            qreg[s][0] = (_Float16)(a0.x * c); qreg[s][1] = (_Float16)(a0.y * c); qreg[s][2] = (_Float16)(a0.z * c);
+            qreg[s][3] = (_Float16)(a0.w * c); qreg[s][4] = (_Float16)(a1.x * c); qreg[s][5] = (_Float16)(a1.y * c);
+            qreg[s][6] = (_Float16)(a1.z * c); qreg[s][7] = (_Float16)(a1.w * c);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
@@ -884,7 +887,6 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
     for (int c = 0; c < HD / 32; ++c)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
-    const float sl2 = scale * 1.4426950408889634f;  // scores in log2 units
     float m_run = -INFINITY, l_run = 0.f;
 
     int buf = 0;
@@ -919,7 +921,6 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
         }
         // masks only where the tile crosses the diagonal, the sequence end or the window
         const bool edge = (k0 + PF_BK > q0) || (k0 + PF_BK > T) || (window > 0 && k0 <= q0 + 31 - window + 1);
-        float tmax = -INFINITY;
         if (edge) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -927,34 +928,36 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
                 for (int e = 0; e < 16; ++e) {
                     const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
                     const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
-                    const float sv = vis ? st[t][e] * sl2 : -INFINITY;
-                    st[t][e] = sv;
-                    tmax = fmaxf(tmax, sv);
-                }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float sv = st[t][e] * sl2;
-                    st[t][e] = sv;
-                    tmax = fmaxf(tmax, sv);
+                    if (!vis) st[t][e] = -INFINITY;
                 }
         }
+        // row maximum over the lane's 32 keys as a tree (no 32-long dependent chain)
+        float mx[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx[e] = fmaxf(st[0][e], st[1][e]);
+#pragma unroll
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+            for (int e = 0; e < w; ++e) mx[e] = fmaxf(mx[e], mx[e + w]);
+        float tmax = mx[0];
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float m_new = fmaxf(m_run, tmax);
         const float msub = (m_new == -INFINITY) ? 0.f : m_new;  // fully masked row: exp2(-inf) = 0
         const float alpha = __builtin_amdgcn_exp2f(m_run - msub);
-        float psum = 0.f;
         f16x8 pa[4];
+        float ps[16];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int e = 0; e < 16; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(st[0][e] - msub), p1 = __builtin_amdgcn_exp2f(st[1][e] - msub);
+            pa[e >> 3][e & 7] = (_Float16)p0;
+            pa[2 + (e >> 3)][e & 7] = (_Float16)p1;
+            ps[e] = p0 + p1;
+        }
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = __builtin_amdgcn_exp2f(st[t][e] - msub);
-                psum += p;
-                pa[2 * t + (e >> 3)][e & 7] = (_Float16)p;
-            }
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+            for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
+        float psum = ps[0];
         psum += __shfl_xor(psum, 32, 64);
         l_run = l_run * alpha + psum;
         const bool moved = m_new != m_run;
