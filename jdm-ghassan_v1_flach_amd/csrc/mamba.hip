@@ -295,17 +295,25 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
 
     // ---- inter-chunk term: (e^(cum_t) C_t) S_in^T
     const float* Sc = Sin + ((size_t)c * H + h) * P * N;
+    // every C / S_in piece of the block is requested before the first one is converted (one
+    // memory round trip instead of one per loop step)
+    constexpr int CPT = 64 * N / 4 / 256;  // float4 pieces per thread (4 or 8)
+    float4 cv[CPT], sv[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
+        cv[j] = tt + r < len ? *(const float4*)(Cm + (size_t)(t0 + tt + r) * ldc + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        sv[j] = ((const float4*)Sc)[e];  // P * N / 4 == 64 * N / 4
+    }
     __syncthreads();
-    for (int e = tid; e < 64 * N / 4; e += 256) {
-        const int r = (4 * e) / N, cc = (4 * e) % N;
-        const bool ok = tt + r < len;
-        const float4 v = ok ? *(const float4*)(Cm + (size_t)(t0 + tt + r) * ldc + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float sc = ok ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
-        f16x4 hv;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
+        const float sc = tt + r < len ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
+        const float4 v = cv[j], w = sv[j];
+        f16x4 hv, hw;
         hv[0] = (_Float16)(v.x * sc); hv[1] = (_Float16)(v.y * sc); hv[2] = (_Float16)(v.z * sc); hv[3] = (_Float16)(v.w * sc);
         *(f16x4*)(sC + r * SN + cc) = hv;
-        const float4 w = ((const float4*)Sc)[e];  // P * N / 4 == 64 * N / 4
-        f16x4 hw;
         hw[0] = (_Float16)w.x; hw[1] = (_Float16)w.y; hw[2] = (_Float16)w.z; hw[3] = (_Float16)w.w;
         *(f16x4*)(sS + r * SN + cc) = hw;
     }
@@ -317,26 +325,70 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
         const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
     }
-    // ---- intra-chunk term over tau tiles up to the last row of this block
+    // ---- intra-chunk term over tau tiles up to the last row of this block. The next tile's
+    // operands (cum / dt of its positions, the X rows, this block's G rows) are loaded into
+    // registers while the current tile is multiplied: no global round trip inside the loop.
     const int kend = min(len, tt + 64);
     const int ntk = (kend + TK - 1) / TK;
+    constexpr int XR = 4;  // X^T staging: thread = (4 columns xq, rows 4 xg .. 4 xg + 3)
+    const int xq = tid % 16, xg = tid / 16;
+    float4 px[XR], pg[4];
+    float pcum = 0.f, pdt = 0.f;
+    auto prefetch = [&](int kk) {
+        const int k0 = ((kk + h) % ntk) * TK;
+        if (tid < TK) {
+            const int tau = k0 + tid;
+            pcum = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
+            pdt = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int r = xg * XR + i;
+            px[i] = r < len - k0 ? *(const float4*)(xs + (size_t)(t0 + k0 + r) * ldx + h * P + 4 * xq)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = tid + 256 * j, r = e >> 4, q = (e & 15) * 4;
+            const int t = tt + r;
+            pg[j] = t < len ? *(const float4*)(G + ((size_t)c * L + t) * L + k0 + q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    prefetch(0);
     for (int kk = 0; kk < ntk; ++kk) {
         const int k0 = ((kk + h) % ntk) * TK;
         __syncthreads();  // previous tile (or the inter-chunk operands) consumed
         if (tid < TK) {
-            const int tau = k0 + tid;
-            scum[tid] = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
-            sdt[tid] = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
+            scum[tid] = pcum;
+            sdt[tid] = pdt;
         }
-        stage_t64<P, S, false>(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0, nullptr, sXt);
+        {
+            typedef _Float16 hrun __attribute__((ext_vector_type(XR)));
+            hrun h0, h1, h2, h3;
+#pragma unroll
+            for (int i = 0; i < XR; ++i) {
+                h0[i] = (_Float16)px[i].x;
+                h1[i] = (_Float16)px[i].y;
+                h2[i] = (_Float16)px[i].z;
+                h3[i] = (_Float16)px[i].w;
+            }
+            _Float16* d = sXt + (4 * xq) * S + xg * XR;
+            *(hrun*)d = h0;
+            *(hrun*)(d + S) = h1;
+            *(hrun*)(d + 2 * S) = h2;
+            *(hrun*)(d + 3 * S) = h3;
+        }
+        float4 gcur[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gcur[j] = pg[j];
         __syncthreads();
+        if (kk + 1 < ntk) prefetch(kk + 1);
         // A[t][tau] = G e^(cum_t - cum_tau) dt_tau for tau <= t (both inside the chunk), fp16
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = tid + 256 * j, r = e >> 4, q = (e & 15) * 4;
             const int t = tt + r;
-            const float4 g4 = t < len ? *(const float4*)(G + ((size_t)c * L + t) * L + k0 + q) : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float gv[4] = {g4.x, g4.y, g4.z, g4.w};
+            const float gv[4] = {gcur[j].x, gcur[j].y, gcur[j].z, gcur[j].w};
             f16x4 hv;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
