@@ -162,6 +162,41 @@ __device__ __forceinline__ void stage_t64(const float* __restrict__ src, int ld,
     *(hrun*)(d + 3 * S) = h3;
 }
 
+// stage_t64 in two halves: the loads (into registers, issued early) and the
+// transposed fp16 stores (optionally scaled per row by sw from LDS).
+template <int W>
+struct Stage64 {
+    static constexpr int Q = W / 4, G = 256 / Q, R = 64 / G;
+    float4 v[R];
+    __device__ __forceinline__ void load(const float* __restrict__ src, int ld, int nvalid) {
+        const int cq = threadIdx.x % Q, g = threadIdx.x / Q;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int r = g * R + i;
+            v[i] = r < nvalid ? *(const float4*)(src + (size_t)r * ld + 4 * cq) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    template <int S>
+    __device__ __forceinline__ void store(_Float16* dst, const float* sw) const {
+        const int cq = threadIdx.x % Q, g = threadIdx.x / Q;
+        typedef _Float16 hrun __attribute__((ext_vector_type(R)));
+        hrun h0, h1, h2, h3;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const float w = sw ? sw[g * R + i] : 1.0f;
+            h0[i] = (_Float16)(v[i].x * w);
+            h1[i] = (_Float16)(v[i].y * w);
+            h2[i] = (_Float16)(v[i].z * w);
+            h3[i] = (_Float16)(v[i].w * w);
+        }
+        _Float16* d = dst + (4 * cq) * S + g * R;
+        *(hrun*)d = h0;
+        *(hrun*)(d + S) = h1;
+        *(hrun*)(d + 2 * S) = h2;
+        *(hrun*)(d + 3 * S) = h3;
+    }
+};
+
 template <int N>
 __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict__ xs, int ldx,
                                                          const float* __restrict__ Bm, int ldb,
@@ -186,18 +221,31 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict
     // the B rows of a chunk are the same for every head: head h starts at tile h mod ntk, so the
     // blocks of one chunk do not all read the same lines at once (that serialises them)
     const int ntk = (len + TK - 1) / TK;
-    for (int kk = 0; kk < ntk; ++kk) {
+    // the next tile's cum / dt, X rows and B rows are loaded into registers while the current
+    // tile is multiplied (no global round trip inside the loop)
+    Stage64<P> rx;
+    Stage64<N> rb;
+    float pc = 0.f, pd = 0.f;
+    auto prefetch = [&](int kk) {
         const int k0 = ((kk + h) % ntk) * TK;
-        __syncthreads();
         if (threadIdx.x < TK) {
             const int tau = k0 + threadIdx.x;
-            sw[threadIdx.x] = tau < len ? expf(cend - cum[(size_t)(t0 + tau) * H + h]) * dt[(size_t)(t0 + tau) * H + h]
-                                        : 0.f;
+            pc = tau < len ? cum[(size_t)(t0 + tau) * H + h] : 0.f;
+            pd = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
         }
+        rx.load(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0);
+        rb.load(Bm + (size_t)(t0 + k0) * ldb, ldb, len - k0);
+    };
+    prefetch(0);
+    for (int kk = 0; kk < ntk; ++kk) {
+        const int k0 = ((kk + h) % ntk) * TK;
+        __syncthreads();  // the previous tile's operands are consumed
+        if (threadIdx.x < TK) sw[threadIdx.x] = k0 + (int)threadIdx.x < len ? expf(cend - pc) * pd : 0.f;
         __syncthreads();
-        stage_t64<P, S, true>(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0, sw, sX);
-        stage_t64<N, S, false>(Bm + (size_t)(t0 + k0) * ldb, ldb, len - k0, nullptr, sB);
+        rx.template store<S>(sX, sw);
+        rb.template store<S>(sB, nullptr);
         __syncthreads();
+        if (kk + 1 < ntk) prefetch(kk + 1);
 #pragma unroll
         for (int ks = 0; ks < TK / 16; ++ks) {
             const int ko = ks * 16 + 8 * (lane >> 5);
