@@ -59,12 +59,22 @@ __global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in
     const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int t0 = c * L, len = min(L, T - t0);
     const float A = A_in ? A_in[h] : -expf(a_log[h]);
-    float carry = 0.f;
-    for (int base = 0; base < len; base += 64) {
+    // the raw dt of all positions (up to 4 per lane) are requested before the first scan step
+    float raws[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 64 * j + lane;
+        raws[j] = i < len ? dt_in[(size_t)(t0 + i) * dt_ld + h] : 0.f;
+    }
+    float carry = 0.f;  // L <= 256 (ssd_run checks it): at most 4 steps
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int base = 64 * j;
+        if (base >= len) break;
         const int i = base + lane;
         float dt = 0.f, a = 0.f;
         if (i < len) {
-            const float raw = dt_in[(size_t)(t0 + i) * dt_ld + h];
+            const float raw = raws[j];
             dt = dt_bias ? softplus_ref(raw + dt_bias[h]) : raw;
             a = A * dt;
         }
