@@ -728,9 +728,13 @@ static size_t gd_lds_bytes(int K, int SBW, int NB) {
            2 * GD_S * WB * 64 * 4;
 }
 
-template <int SBW, int NB>
+// FUSED: the activation vector is formed by a norm prologue (RMSNORM / GATED,
+// the arithmetic of gm_prologue) straight into the staging area instead of
+// being copied, and every output goes through gm_epilogue (STORE / ADD / CONV).
+template <int SBW, int NB, bool FUSED = false>
 __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
-                                                           float* __restrict__ y, int K, int N, size_t rowb) {
+                                                           float* __restrict__ y, int K, int N, size_t rowb,
+                                                           GmFuse f) {
     using C = GdCfg<SBW>;
     constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL;
     extern __shared__ __attribute__((aligned(16))) uint4 gd_lds[];
@@ -747,9 +751,29 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     float* sxs = ssc + (K >> 5);                            // [K / 32] sums of x
     float4* sred = (float4*)(sxs + (K >> 5));               // [2][GD_S][WB][16] (4 lane groups each)
     // x: piece tid + j * blockDim.x (contiguous per wave instruction)
+    const bool pro = FUSED && f.pro != GM_PRO_NONE;
+    float4 pv[SBW], pw[SBW];
+    if (!pro) {
 #pragma unroll
-    for (int j = 0; j < SBW; ++j)
-        lds_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, lds_addr(&sx[wave * 64 + j * blockDim.x]));
+        for (int j = 0; j < SBW; ++j)
+            lds_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, lds_addr(&sx[wave * 64 + j * blockDim.x]));
+    } else {
+        // prologue operands requested now; the values are formed while the first tile streams in
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const int idx = tid + j * blockDim.x;
+            pv[j] = ((const float4*)x)[idx];
+            pw[j] = ((const float4*)f.pw)[idx];
+            if (f.pro == GM_PRO_GATED) {
+                const float4 z = ((const float4*)f.pz)[idx];
+                // mamba.hip k_gated_norm: v = y * silu(z)
+                pv[j].x = pv[j].x * (z.x / (1.0f + expf(-z.x)));
+                pv[j].y = pv[j].y * (z.y / (1.0f + expf(-z.y)));
+                pv[j].z = pv[j].z * (z.z / (1.0f + expf(-z.z)));
+                pv[j].w = pv[j].w * (z.w / (1.0f + expf(-z.w)));
+            }
+        }
+    }
     // column `wave` of a tile -> ring slice; piece q = PR r + j of row r
     uint32_t voff[PPL];
 #pragma unroll
@@ -779,6 +803,29 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     // only the first tile now: the memory system returns it sooner when the other tiles of the
     // ring are requested after the conversion of x (the ring is always filled, so every wait is exact)
     dma(t0 < ntiles ? t0 : ntiles - 1, 0);
+    if (pro) {
+        // elementwise.hip k_rmsnorm / mamba.hip k_gated_norm: double sum of squares, x * inv * w
+        __shared__ double gd_red[16];
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < SBW; ++j)
+            ss += (double)pv[j].x * pv[j].x + (double)pv[j].y * pv[j].y + (double)pv[j].z * pv[j].z +
+                  (double)pv[j].w * pv[j].w;
+        const double tot = gm_block_sum_dpp(ss, gd_red);
+        float inv;
+        if (f.pro == GM_PRO_GATED) {
+            inv = 1.0f / sqrtf((float)(tot / (double)K) + f.eps);
+        } else {
+            const double invd = 1.0 / sqrt(tot / (double)K + (double)f.eps);
+            inv = isfinite(invd) ? (float)invd : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const int idx = tid + j * blockDim.x;
+            sx[idx] = make_float4(pv[j].x * inv * pw[j].x, pv[j].y * inv * pw[j].y, pv[j].z * inv * pw[j].z,
+                                  pv[j].w * inv * pw[j].w);
+        }
+    }
     // ---- x -> three int8 parts per value; scale, x sum and part sums per 32 values (8 threads each)
     lds_dma_wait<PPL>(1);  // x landed (the first tile in flight)
     lds_barrier();
@@ -915,7 +962,10 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
                 v += __shfl_xor(v, 4, 64);
                 v += __shfl_xor(v, 8, 64);
                 const int n = (tile - (slot - tl) * G) * 16 + row;
-                if (w == 0 && n < N) y[n] = v;
+                if (w == 0 && n < N) {
+                    if constexpr (FUSED) gm_epilogue(y, n, n, v, f, GmEpiPre{}, false);
+                    else y[n] = v;
+                }
             }
         }
         b = b + 1 == NB ? 0 : b + 1;
@@ -1011,13 +1061,13 @@ static int gm_kind(const float* x, const void* w, float* y, int M, int K, int N)
     return gm_ss<KIND, 4>(x, w, y, M, K, N);
 }
 
-template <int SBW, int NB>
-static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N) {
+template <int SBW, int NB, bool FUSED = false>
+static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, const GmFuse& f = GmFuse{}) {
     static int configured = 0;
     static int per_cu[17];  // resident blocks per CU by K / (256 SBW)
     const size_t lds = gd_lds_bytes(K, SBW, NB);
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB, FUSED>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)gd_lds_bytes(4096, SBW, NB));
         if (e != hipSuccess) return fail(GH_EHIP, "k_gemv_q4k_i8 LDS attribute: %s", hipGetErrorString(e));
         configured = 1;
@@ -1025,14 +1075,14 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N) {
     const int wb = K / (256 * SBW);
     if (!per_cu[wb]) {
         int nb = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB>, 64 * wb, lds);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED>, 64 * wb, lds);
         per_cu[wb] = e == hipSuccess && nb > 0 ? nb : 1;
     }
     const int ntiles = (N + 15) / 16;
     const int slots = per_cu[wb] * num_cus();
     const int blocks = ntiles < slots ? ntiles : slots;
-    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K, N,
-                       row_bytes(3, K));
+    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K, N,
+                       row_bytes(3, K), f);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
 }
@@ -1075,6 +1125,12 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
 
 int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, const GmFuse& f) {
     if ((kind != 2 && kind != 3) || K % 256 != 0) return fail(GH_EUNSUPPORTED, "gemv_fused: kind %d K=%d", kind, K);
+    static const int i8_fused = env_int("GH_GEMV_I8_FUSED", 1);
+    if (i8_fused && kind == 3 && K <= 4096 && !f.w1 && f.pro != GM_PRO_ATTN && f.epi != GM_EPI_QKV &&
+        (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
+        // norm prologue / residual or conv epilogue on the int8-MFMA streaming GEMV
+        return gd_launch<1, 2, true>(x, (const uint8_t*)w, y, K, N, f);
+    }
     if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
     if (f.pro == GM_PRO_ATTN && (f.splits > 64 || f.H * f.hd != K))
         return fail(GH_EUNSUPPORTED, "gemv_fused: attention merge of %d splits", f.splits);
