@@ -784,6 +784,11 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     auto dma = [&](int tile, int b) {
         uint4* dst = ring + ((size_t)b * WB + wave) * NP;
         const uint8_t* base = W + (size_t)tile * 16 * rowb;
+        if (FUSED && f.w1) {  // weight segments (16-row aligned): rows [n0, n0+n1) from w1, then w2
+            const int r0 = tile * 16;
+            if (r0 >= f.n0 + f.n1) base = (const uint8_t*)f.w2 + (size_t)(r0 - f.n0 - f.n1) * rowb;
+            else if (r0 >= f.n0) base = (const uint8_t*)f.w1 + (size_t)(r0 - f.n0) * rowb;
+        }
         if (tile * 16 + 16 <= N) {
 #pragma unroll
             for (int i = 0; i < PPL; ++i)
@@ -1126,9 +1131,10 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
 int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, const GmFuse& f) {
     if ((kind != 2 && kind != 3) || K % 256 != 0) return fail(GH_EUNSUPPORTED, "gemv_fused: kind %d K=%d", kind, K);
     static const int i8_fused = env_int("GH_GEMV_I8_FUSED", 1);
-    if (i8_fused && kind == 3 && K <= 4096 && !f.w1 && f.pro != GM_PRO_ATTN && f.epi != GM_EPI_QKV &&
+    if (i8_fused && kind == 3 && K <= 4096 && f.pro != GM_PRO_ATTN && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
         (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
-        // norm prologue / residual or conv epilogue on the int8-MFMA streaming GEMV
+        // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
+        // streaming GEMV
         return gd_launch<1, 2, true>(x, (const uint8_t*)w, y, K, N, f);
     }
     if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
