@@ -104,6 +104,11 @@ int gh_argmax_token(const float* logits, int V, int32_t* out_host);
 /* Device-resident variant for graph-captured decode: writes the id to a
  * device int. No reference counterpart (the reference copies it back). */
 int gh_argmax_token_dev(const float* logits, int V, int32_t* out_dev);
+/* The tail of a decode step in one launch: final rmsnorm (core/ops.h:134) of x[d],
+ * the tied fp16 lm head (model/model.cpp:1087-1160, logits[V] written) and
+ * argmax_token (core/ops.h:400) into a device int. d % 8 == 0, d <= 2048. */
+int gh_lm_head_greedy_dev(const float* x, const float* norm_w, float eps, const uint16_t* tab_f16, float* logits,
+                          int d, int V, int32_t* out_dev);
 
 /* ----------------------------------------------------------------- Mamba-2 */
 /* core/ops.h:256-269 mamba2_forward_half: one Mamba-2 layer over B x T

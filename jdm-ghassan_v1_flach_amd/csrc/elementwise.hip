@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(1024) k_argmax(const float* __restrict__ l, in
     {
         // the wave's best as an unsigned key (value in an order-preserving form, then ~index so
         // the lower index wins ties; 0 = none) reduced on the DPP path into lane 63
-        const uint32_t u = __builtin_bit_cast(uint32_t, bv);
+        const uint32_t u = __builtin_bit_cast(uint32_t, bv == 0.f ? 0.f : bv);  // -0 ties with +0
         uint32_t hi = bi >= 0 ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
         uint32_t lo = bi >= 0 ? ~(uint32_t)bi : 0u;
         auto step = [&](uint32_t oh, uint32_t ol) {

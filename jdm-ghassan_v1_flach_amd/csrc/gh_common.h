@@ -233,5 +233,6 @@ enum WsSlot {
     WS_MOE_TERMS = 34,  // router group terms (large routers, few tokens)
     WS_GEMM_PART = 35,  // split-K partial tiles of the small-M prefill GEMM
     WS_GEMM_ACC = 36,   // product before an accumulating add (paths without an in-place sum)
+    WS_HEAD_CTL = 37,   // argmax key / counter block of a standalone lm-head + greedy call
 };
 }  // namespace gh

@@ -42,7 +42,12 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
 int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
 
 // decode control block (device ints)
-enum { CTL_TOKEN = 0, CTL_LEN = 1, CTL_START = 2, CTL_PINNED = 3, CTL_CAP = 4, CTL_SLOT = 5, CTL_STEP = 6, CTL_N = 8 };
+// ctl[CTL_AMAX..+1]: a 64-bit running argmax key (8-byte aligned), ctl[CTL_AMAX_CNT]: blocks
+// done, ctl[CTL_AMAX_NEG0]: logit 0 is -inf; all zero between launches of k_head_argmax.
+enum {
+    CTL_TOKEN = 0, CTL_LEN = 1, CTL_START = 2, CTL_PINNED = 3, CTL_CAP = 4, CTL_SLOT = 5, CTL_STEP = 6,
+    CTL_AMAX = 8, CTL_AMAX_CNT = 10, CTL_AMAX_NEG0 = 11, CTL_N = 12
+};
 
 // KVCache::allocate_slot (inference/kv_cache.h:74-92) on the device.
 __global__ void k_alloc_slot(int32_t* ctl) {
@@ -102,6 +107,169 @@ __global__ void k_step_begin(int32_t* ctl, const uint16_t* __restrict__ tab, flo
         x[i] = (id < 0 || id >= vocab) ? 0.f : f16_to_f32(tab[(size_t)id * dim + i]);
 }
 
+
+// Argmax key of logit v at index i, ordered like core/math_cpu.cpp:710-723
+// (first finite maximum, strict '>', so the lower index wins ties; -0 counts
+// as +0, they compare equal there): a finite value becomes an order-preserving
+// unsigned number (>= 0x00800000) above ~i. +inf gets 0 above ~i, so the largest
+// key is a finite maximum if there is one, else the first +inf; NaN and -inf
+// get 0 = "none".
+__device__ __forceinline__ uint64_t amax_key(float v, int i) {
+    const uint32_t lo = ~(uint32_t)i;
+    if (v == __builtin_inff()) return lo;
+    if (!isfinite(v)) return 0;
+    const uint32_t u = __builtin_bit_cast(uint32_t, v == 0.f ? 0.f : v);
+    const uint32_t hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// End of a decode step in one launch: final RMSNorm (k_rmsnorm's arithmetic,
+// so the normalised row is bit-identical), the tied fp16 lm head
+// (model/model.cpp:1087-1160) and, with `argmax`, the greedy pick recorded as
+// k_argmax + k_record_token do. Block b owns rows 16b..16b+15, wave w four of
+// them; lane l holds 8-value pieces l, l + 64, ... of x and of each row. Every
+// block recomputes the norm (d floats from L2) while its weight rows stream in.
+// The blocks' best keys meet in a 64-bit atomicMax; the block whose count
+// arrives last takes the key, resets it and the counter, and writes the token.
+// Device-scope atomics are ordered by waiting for each one's return before the
+// next is issued (no cache write-back fence: the logits themselves are not
+// read back). With no finite logit the reference's serial scan returns the
+// first +inf when l[0] is -inf and 0 otherwise; the block of row 0 reports
+// whether l[0] is -inf through ctl[CTL_AMAX_NEG0].
+template <int CHM>
+__global__ void __launch_bounds__(256) k_head_argmax(const float* __restrict__ x, const float* __restrict__ nw,
+                                                     float eps, const uint16_t* __restrict__ tab,
+                                                     float* __restrict__ logits, int d, int V, int32_t* ctl,
+                                                     int32_t* ids, int cap, int argmax) {
+    constexpr int RPW = 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = d >> 3;
+    const int row0 = (blockIdx.x * 4 + wave) * RPW;
+    // every load issued before the first wait: x pieces + norm weights, weight rows, x for the sum
+    float4 xv[CHM][2], nv[CHM][2];
+    uint4 wr[RPW][CHM];
+#pragma unroll
+    for (int i = 0; i < CHM; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nch) {
+            xv[i][0] = ((const float4*)x)[2 * c];
+            xv[i][1] = ((const float4*)x)[2 * c + 1];
+            nv[i][0] = ((const float4*)nw)[2 * c];
+            nv[i][1] = ((const float4*)nw)[2 * c + 1];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int n = row0 + r < V ? row0 + r : V - 1;
+        const uint4* wrow = (const uint4*)(tab + (size_t)n * d);
+#pragma unroll
+        for (int i = 0; i < CHM; ++i) {
+            const int c = lane + 64 * i;
+            if (c < nch) wr[r][i] = wrow[c];
+        }
+    }
+    float xs[CHM * 2];
+#pragma unroll
+    for (int j = 0; j < CHM * 2; ++j)
+        if (tid + 256 * j < d) xs[j] = x[tid + 256 * j];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < CHM * 2; ++j)
+        if (tid + 256 * j < d) ss += (double)xs[j] * xs[j];
+    __shared__ double red[4];
+    __shared__ uint64_t skey[4];
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // LDS only: the weight loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const double invd = 1.0 / sqrt(tot / (double)d + (double)eps);
+    const float inv = isfinite(invd) ? (float)invd : 0.0f;
+    float xn[CHM][8];
+#pragma unroll
+    for (int i = 0; i < CHM; ++i) {
+        const float a[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                            xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+        const float b[8] = {nv[i][0].x, nv[i][0].y, nv[i][0].z, nv[i][0].w,
+                            nv[i][1].x, nv[i][1].y, nv[i][1].z, nv[i][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xn[i][e] = a[e] * inv * b[e];
+    }
+    uint64_t best = 0;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < CHM; ++i) {
+            if (lane + 64 * i < nch) {
+                const uint32_t wd[4] = {wr[r][i].x, wr[r][i].y, wr[r][i].z, wr[r][i].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc = fmaf(xn[i][2 * e], f16_to_f32((uint16_t)(wd[e] & 0xFFFF)), acc);
+                    acc = fmaf(xn[i][2 * e + 1], f16_to_f32((uint16_t)(wd[e] >> 16)), acc);
+                }
+            }
+        }
+        acc = wave_total63(acc);
+        const int n = row0 + r;
+        if (lane == 63 && n < V) {
+            logits[n] = acc;
+            const uint64_t k = amax_key(acc, n);
+            best = k > best ? k : best;
+            if (argmax && n == 0 && acc == -__builtin_inff()) {
+                (void)__hip_atomic_fetch_or(ctl + CTL_AMAX_NEG0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): performed before the block's count
+            }
+        }
+    }
+    if (!argmax) return;
+    if (lane == 63) skey[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t k = skey[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) k = skey[w] > k ? skey[w] : k;
+        unsigned long long* keyp = (unsigned long long*)(ctl + CTL_AMAX);
+        unsigned int* cntp = (unsigned int*)(ctl + CTL_AMAX_CNT);
+        if (k) {
+            (void)__hip_atomic_fetch_max(keyp, (unsigned long long)k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        if (__hip_atomic_fetch_add(cntp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
+            const uint64_t fin = __hip_atomic_exchange(keyp, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int neg0 = __hip_atomic_exchange(ctl + CTL_AMAX_NEG0, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            (void)__hip_atomic_exchange(cntp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int bi = 0;
+            if (fin >> 32) bi = (int)~(uint32_t)fin;                // finite maximum
+            else if (fin && neg0) bi = (int)~(uint32_t)fin;        // no finite value: first +inf after l[0] = -inf
+            ctl[CTL_TOKEN] = bi;
+            if (ids) {
+                const int s = ctl[CTL_STEP];
+                if (s < cap) ids[s] = bi;
+                ctl[CTL_STEP] = s + 1;
+            }
+        }
+    }
+}
+
+// Returns 1 if launched (fp16 table, d a multiple of 8 up to 2048, 16-byte aligned rows).
+static int launch_head_argmax(const float* x, const float* nw, float eps, const uint16_t* tab, float* logits, int d,
+                              int V, int32_t* ctl, int32_t* ids, int cap, bool argmax) {
+    static const int enabled = [] {
+        const char* e = getenv("GH_HEAD_FUSED");
+        return e ? atoi(e) : 1;
+    }();
+    if (!enabled || d % 8 || d > 2048 || (((uintptr_t)x | (uintptr_t)nw | (uintptr_t)tab) & 15)) return 0;
+    const dim3 grid((V + 15) / 16), blk(256);
+    if (d <= 512)
+        hipLaunchKernelGGL(k_head_argmax<1>, grid, blk, 0, stream(), x, nw, eps, tab, logits, d, V, ctl, ids, cap, argmax);
+    else if (d <= 1024)
+        hipLaunchKernelGGL(k_head_argmax<2>, grid, blk, 0, stream(), x, nw, eps, tab, logits, d, V, ctl, ids, cap, argmax);
+    else
+        hipLaunchKernelGGL(k_head_argmax<4>, grid, blk, 0, stream(), x, nw, eps, tab, logits, d, V, ctl, ids, cap, argmax);
+    GH_LAUNCHED("k_head_argmax");
+    return 1;
+}
 }  // namespace gh
 
 using namespace gh;
@@ -297,6 +465,11 @@ static int decode_step_fused(gh_granite* g, bool argmax) {
                              g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"), g->W(pre + "moe_sh_down"), 1, d, g->E,
                              g->ne, g->K, g->SH, g->qkind));
     }
+    if (launch_head_argmax(g->x, g->F("final_norm"), g->eps, (const uint16_t*)g->W("tok_embeddings"), g->logits, d,
+                           g->V, g->ctl, g->gen_ids, g->max_ctx, argmax)) {
+        GH_LAUNCHED("decode_step");
+        return GH_OK;
+    }
     GHC(gh_rmsnorm_forward(g->x, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
     GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
     if (argmax)
@@ -315,6 +488,20 @@ static int decode_step(gh_granite* g, bool argmax) {
 }
 
 extern "C" {
+
+// Final norm + tied fp16 lm head + greedy id in one launch (the tail of a
+// decode step), for callers outside a model; the id goes to a device int.
+int gh_lm_head_greedy_dev(const float* x, const float* norm_w, float eps, const uint16_t* tab, float* logits, int d,
+                          int V, int32_t* out_dev) {
+    GH_REQUIRE(x && norm_w && tab && logits && out_dev && d > 0 && V > 0, "lm_head_greedy: bad arguments");
+    int32_t* ctl = (int32_t*)workspace(WS_HEAD_CTL, CTL_N * 4);
+    if (!ctl) return fail(GH_ENOMEM, "lm_head_greedy: workspace");
+    GH_HIP(hipMemsetAsync(ctl, 0, CTL_N * 4, stream()));
+    if (!launch_head_argmax(x, norm_w, eps, tab, logits, d, V, ctl, nullptr, 0, true))
+        return fail(GH_EUNSUPPORTED, "lm_head_greedy: d=%d (needs d %% 8 == 0, d <= 2048, 16-byte aligned rows)", d);
+    GH_HIP(hipMemcpyAsync(out_dev, ctl + CTL_TOKEN, 4, hipMemcpyDeviceToDevice, stream()));
+    return GH_OK;
+}
 
 int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_granite** out) {
     GH_REQUIRE(cfg && fcfg && out, "granite_create: null argument");
@@ -484,7 +671,7 @@ int gh_granite_reset(gh_granite* g) {
         else sbytes += (size_t)2 * g->max_ctx * g->kvd * 2;
     }
     GH_HIP(hipMemsetAsync(g->state_buf, 0, sbytes, stream()));
-    const int32_t ctl[CTL_N] = {0, 0, 0, g->pinned_cfg, g->max_ctx, 0, 0, 0};
+    const int32_t ctl[CTL_N] = {0, 0, 0, g->pinned_cfg, g->max_ctx, 0, 0, 0, 0, 0, 0, 0};
     GH_HIP(hipMemcpyAsync(g->ctl, ctl, sizeof ctl, hipMemcpyHostToDevice, stream()));
     GH_HIP(hipStreamSynchronize(stream()));
     g->host_len = 0;
