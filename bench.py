@@ -229,6 +229,20 @@ def kernel_suite(gh):
             res[tag] = entry("moe route+permute+group gemm x2+shared+combine", ms,
                              bytes_=ne5 * expert_bytes + 3 * SH5 * d5 * 144 // 256, flops=fl, bound="mfma")
         del bufs, out
+    # ---------------- sampling ops of the decode loop (next-row scope: top-K, penalties)
+    for V, K in ((4096, 40), (100352, 40), (262144, 128)):
+        lg = gh.Buf.from_array(gh.rng_normal(9, V))
+        tv, ti = gh.Buf.zeros(K, np.float32), gh.Buf.zeros(K, np.int32)
+        ms = time_launches(gh, lambda: gh.call("gh_topk_select", lg.p, V, K, tv.p, ti.p), 50)
+        res[f"topk_V{V}_K{K}"] = entry("k_topk_pass (1-3 passes)", ms, bytes_=V * 4)
+        del lg, tv, ti
+    V, n = 100352, 2048
+    lg = gh.Buf.from_array(gh.rng_normal(10, V))
+    hist = (np.arange(n, dtype=np.int32) * 7919) % V
+    hp = hist.ctypes.data_as(C.c_void_p)
+    ms = time_launches(gh, lambda: gh.call("gh_apply_rep_penalties", lg.p, V, hp, n, gh.fl(1.1), gh.fl(0.1),
+                                           gh.fl(0.1)), 50)
+    res[f"rep_penalties_V{V}_hist{n}"] = entry("H2D history + k_rep_penalties", ms, bytes_=n * 4 * 3 + n * 8)
     return res
 
 

@@ -104,6 +104,15 @@ int gh_argmax_token(const float* logits, int V, int32_t* out_host);
 /* Device-resident variant for graph-captured decode: writes the id to a
  * device int. No reference counterpart (the reference copies it back). */
 int gh_argmax_token_dev(const float* logits, int V, int32_t* out_dev);
+/* core/ops.h:397 topk_select (device logits / outputs): the K largest logits, larger value first,
+ * lower index first among equal values (core/math_cpu.cpp:695-707); NaN ranks below -inf.
+ * Limits of the CUDA branch (cuda/kernels.cu:1474-1476): 1 <= K <= 128, K <= V <= 262144. */
+int gh_topk_select(const float* logits, int V, int K, float* out_vals, int32_t* out_ids);
+/* core/ops.h:402 apply_rep_penalties: logits on the device, hist a HOST array of hist_n ids
+ * (as Generator passes its history, inference/generator.cpp:1042); semantics of
+ * core/math_cpu.cpp:725-752. */
+int gh_apply_rep_penalties(float* logits, int V, const int32_t* hist, int hist_n, float rep, float freq,
+                           float pres);
 /* The tail of a decode step in one launch: final rmsnorm (core/ops.h:134) of x[d],
  * the tied fp16 lm head (model/model.cpp:1087-1160, logits[V] written) and
  * argmax_token (core/ops.h:400) into a device int. d % 8 == 0, d <= 2048. */

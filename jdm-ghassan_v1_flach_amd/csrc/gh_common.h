@@ -234,5 +234,7 @@ enum WsSlot {
     WS_GEMM_PART = 35,  // split-K partial tiles of the small-M prefill GEMM
     WS_GEMM_ACC = 36,   // product before an accumulating add (paths without an in-place sum)
     WS_HEAD_CTL = 37,   // argmax key / counter block of a standalone lm-head + greedy call
+    WS_TOPK = 38,       // top-K survivors of each 4096-logit chunk
+    WS_PEN_HIST = 39,   // device copy of the penalty history
 };
 }  // namespace gh

@@ -22,6 +22,9 @@
 //   linear_forward_q4 (Q4_K) ... pinned through the dequant closed form + the
 //                                same serial dot as kinds 0-2.
 //   rmsnorm/swiglu/softmax/argmax/embedding ... pinned: golden outputs.
+//   topk_select, apply_rep_penalties ........... pinned: golden outputs of
+//                                the compiled ops:: CPU functions + numpy
+//                                lexsort / per-token counting in tests.
 //   attention_forward_ex, attention_decode_ring_fp16 ... pinned: golden.
 //   paged bf16 decode .......... pinned: equals the ring kernel on widened
 //                                values (test) -- an extension.
@@ -441,6 +444,41 @@ void softmax_row(float* x, int n) {
 }
 
 // core/math_cpu.cpp:710-723
+// core/math_cpu.cpp:695-707: the K largest logits, larger value first, lower
+// index first among equal values (here: a full sort by that key, then the
+// first K, which is the same set and order for any input without NaN).
+void topk_select(const float* l, int V, int K, float* vals, i32* ids) {
+    std::vector<int> order((size_t)V);
+    for (int i = 0; i < V; ++i) order[(size_t)i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return l[a] > l[b]; });
+    for (int k = 0; k < K; ++k) {
+        ids[k] = order[(size_t)k];
+        vals[k] = l[order[(size_t)k]];
+    }
+}
+
+// core/math_cpu.cpp:725-752: every distinct in-range token of the history, seen
+// n times, gets the repetition transform once (divide positive logits by rep,
+// multiply the others), then minus freq * n, then minus pres. Counting here is
+// a dense per-token table rather than a sort.
+void apply_rep_penalties(float* l, int V, const i32* hist, int n, float rep, float freq, float pres) {
+    if (n <= 0 || V <= 0) return;
+    const bool use_rep = rep > 0.0f && rep != 1.0f, use_freq = freq != 0.0f, use_pres = pres != 0.0f;
+    if (!use_rep && !use_freq && !use_pres) return;
+    std::vector<int> cnt((size_t)V, 0);
+    for (int i = 0; i < n; ++i)
+        if (hist[i] >= 0 && hist[i] < V) ++cnt[(size_t)hist[i]];
+    for (int t = 0; t < V; ++t) {
+        const int c = cnt[(size_t)t];
+        if (!c) continue;
+        float v = l[t];
+        if (use_rep) v = v > 0.0f ? v / rep : v * rep;
+        if (use_freq) v -= freq * (float)c;
+        if (use_pres) v -= pres;
+        l[t] = v;
+    }
+}
+
 i32 argmax(const float* l, int V) {
     int best = -1;
     float bv = -std::numeric_limits<float>::infinity();
@@ -760,6 +798,14 @@ void orc_swiglu_forward(const float* g, const float* u, float* out, int64_t n) {
 }
 void orc_softmax_row(float* x, int n) { softmax_row(x, n); }
 int32_t orc_argmax_token(const float* l, int V) { return argmax(l, V); }
+int orc_topk_select(const float* l, int V, int K, float* vals, int32_t* ids) {
+    if (V <= 0 || K < 1 || K > V) return 1;
+    topk_select(l, V, K, vals, ids);
+    return 0;
+}
+void orc_apply_rep_penalties(float* l, int V, const int32_t* hist, int n, float rep, float freq, float pres) {
+    apply_rep_penalties(l, V, hist, n, rep, freq, pres);
+}
 // core/math_cpu.cpp:227-241
 void orc_embedding_forward_half(const int32_t* ids, const uint16_t* table, float* out, int64_t ntok, int dim, int vocab) {
     for (i64 t = 0; t < ntok; ++t) {

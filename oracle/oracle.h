@@ -41,6 +41,9 @@ void orc_rmsnorm_forward(const float* x, const float* w, float* out, float* rrms
 void orc_swiglu_forward(const float* g, const float* u, float* out, int64_t n);
 void orc_softmax_row(float* x, int n);
 int32_t orc_argmax_token(const float* logits, int V);
+int  orc_topk_select(const float* logits, int V, int K, float* out_vals, int32_t* out_ids);
+void orc_apply_rep_penalties(float* logits, int V, const int32_t* hist, int hist_n, float rep, float freq,
+                             float pres);
 void orc_embedding_forward_half(const int32_t* ids, const uint16_t* table, float* out,
                                 int64_t ntok, int dim, int vocab);
 

@@ -91,6 +91,12 @@ void ref_swiglu_forward(const float* g, const float* u, float* out, i64 n) {
 }
 void ref_softmax_row(float* x, int n) { cpu::softmax_row(x, n); }
 i32 ref_argmax_token(const float* l, int V) { return ops::argmax_token(Device::CPU, l, V); }
+void ref_topk_select(const float* l, int V, int K, float* vals, i32* ids) {
+    ops::topk_select(Device::CPU, l, V, K, vals, ids);
+}
+void ref_apply_rep_penalties(float* l, int V, const i32* hist, int n, float rep, float freq, float pres) {
+    ops::apply_rep_penalties(Device::CPU, l, V, hist, n, rep, freq, pres);
+}
 void ref_embedding_forward_half(const i32* ids, const u16* table, float* out, i64 ntok, int dim, int vocab) {
     ops::embedding_forward_half(Device::CPU, ids, table, out, ntok, dim, vocab);
 }

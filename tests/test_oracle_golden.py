@@ -315,3 +315,50 @@ def test_granite_greedy_golden():
     ids, margins = O.granite_generate(O.oracle().orc_granite_generate, O.C1, 2, w, g["prompt"], 8)
     assert np.array_equal(ids, g["ids"][:8])
     assert np.array_equal(bits(margins), bits(g["margins"][:8]))
+
+
+def _orc_topk(lg, K):
+    vals = np.zeros(K, np.float32)
+    ids = np.zeros(K, np.int32)
+    assert O.oracle().orc_topk_select(P(lg), len(lg), K, P(vals), P(ids)) == 0
+    return vals, ids
+
+
+@pytest.mark.parametrize("tag", ["a", "b", "c"])
+def test_topk_select_golden(tag):
+    g = golden("sampling")
+    lg, K = g[f"tk{tag}_x"], int(g[f"tk{tag}_k"])
+    vals, ids = _orc_topk(lg, K)
+    assert np.array_equal(ids, g[f"tk{tag}_ids"])
+    assert np.array_equal(bits(vals), bits(g[f"tk{tag}_vals"]))
+    # an independent order: numpy lexsort by (value descending, index ascending)
+    order = np.lexsort((np.arange(len(lg)), -lg.astype(np.float64)))[:K]
+    assert np.array_equal(ids, order)
+
+
+@pytest.mark.parametrize("tag", ["a", "b", "c", "d", "e"])
+def test_rep_penalties_golden(tag):
+    g = golden("sampling")
+    rep, freq, pres = [float(v) for v in g[f"rp{tag}_p"]]
+    hist = g["rp_hist"]
+    o = g[f"rp{tag}_x"].copy()
+    O.oracle().orc_apply_rep_penalties(P(o), len(o), P(hist), len(hist), O.f(rep), O.f(freq), O.f(pres))
+    assert np.array_equal(bits(o), bits(g[f"rp{tag}_out"]))
+
+
+def test_rep_penalties_closed_forms():
+    V = 64
+    x = O.rng_normal(75, V, 0, 2)
+    x[3] = 1.5
+    x[4] = -1.5
+    hist = np.array([3, 3, 3, 4, 70, -2], np.int32)  # 3 seen 3 times, 4 once, the rest out of range
+    o = x.copy()
+    O.oracle().orc_apply_rep_penalties(P(o), V, P(hist), len(hist), O.f(2.0), O.f(0.5), O.f(0.25))
+    assert o[3] == np.float32(np.float32(1.5 / 2.0) - np.float32(1.5)) - np.float32(0.25)
+    assert o[4] == np.float32(np.float32(-1.5 * 2.0) - np.float32(0.5)) - np.float32(0.25)
+    rest = np.ones(V, bool)
+    rest[[3, 4]] = False
+    assert np.array_equal(bits(o[rest]), bits(x[rest]))
+    o = x.copy()  # neutral settings leave the logits alone
+    O.oracle().orc_apply_rep_penalties(P(o), V, P(hist), len(hist), O.f(1.0), O.f(0.0), O.f(0.0))
+    assert np.array_equal(bits(o), bits(x))
