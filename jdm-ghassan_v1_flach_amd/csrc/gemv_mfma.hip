@@ -728,9 +728,13 @@ static size_t gd_lds_bytes(int K, int SBW, int NB) {
            2 * GD_S * WB * 64 * 4;
 }
 
-// FUSED: the activation vector is formed by a norm prologue (RMSNORM / GATED,
-// the arithmetic of gm_prologue) straight into the staging area instead of
-// being copied, and every output goes through gm_epilogue (STORE / ADD / CONV).
+constexpr int GD_ATT_MAX = 1024;  // heads x splits of the attention-merge prologue
+constexpr int GD_ATT_PT = 8;      // (max, sum) pairs per thread: GD_ATT_MAX / 128 threads
+
+// FUSED: the activation vector is formed by a prologue (RMSNORM / GATED / the
+// attention merge, the arithmetic of gm_prologue) straight into the staging
+// area instead of being copied, and every output goes through gm_epilogue
+// (STORE / ADD / CONV / QKV).
 template <int SBW, int NB, bool FUSED = false>
 __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                            float* __restrict__ y, int K, int N, size_t rowb,
@@ -752,8 +756,30 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     float4* sred = (float4*)(sxs + (K >> 5));               // [2][GD_S][WB][16] (4 lane groups each)
     // x: piece tid + j * blockDim.x (contiguous per wave instruction)
     const bool pro = FUSED && f.pro != GM_PRO_NONE;
+    const bool att = FUSED && f.pro == GM_PRO_ATTN;
     float4 pv[SBW], pw[SBW];
-    if (!pro) {
+    float4 ov[SBW][GM_SPR];  // attention merge: this thread's partials of its first GM_SPR splits
+    float2 mlr[GD_ATT_PT];   // attention merge: (max, sum) pairs tid, tid + blockDim.x, ...
+    if (att) {
+        // attention.hip k_attn_combine for all heads: every operand requested before the first tile
+        const int S = f.splits, HS = f.H * f.splits;
+#pragma unroll
+        for (int i = 0; i < GD_ATT_PT; ++i) {
+            const int q = tid + i * blockDim.x;
+            if (q < HS) {
+                const int h = q / S, sp = q - h * S;
+                mlr[i] = *(const float2*)(f.ml + (((size_t)(h / f.G) * S + sp) * f.G + h % f.G) * 2);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const int c = 4 * (tid + j * blockDim.x), h = c / f.hd, cc = c - h * f.hd;
+            const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * f.hd + cc;
+#pragma unroll
+            for (int sp = 0; sp < GM_SPR; ++sp)
+                if (sp < S) ov[j][sp] = *(const float4*)(op + (size_t)sp * f.G * f.hd);
+        }
+    } else if (!pro) {
 #pragma unroll
         for (int j = 0; j < SBW; ++j)
             lds_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, lds_addr(&sx[wave * 64 + j * blockDim.x]));
@@ -808,7 +834,65 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     // only the first tile now: the memory system returns it sooner when the other tiles of the
     // ring are requested after the conversion of x (the ring is always filled, so every wait is exact)
     dma(t0 < ntiles ? t0 : ntiles - 1, 0);
-    if (pro) {
+    if (att) {
+        __shared__ float gd_att[2 * GD_ATT_MAX + 64];  // [H][S] max then split weight, [H][S] sums, [H] 1/L
+        const int H = f.H, S = f.splits, HS = H * S;
+        float* sm = gd_att;
+        float* sl = gd_att + HS;
+        float* sinv = gd_att + 2 * HS;
+#pragma unroll
+        for (int i = 0; i < GD_ATT_PT; ++i) {
+            const int q = tid + i * blockDim.x;
+            if (q < HS) {
+                sm[q] = mlr[i].x;
+                sl[q] = mlr[i].y;
+            }
+        }
+        __syncthreads();
+        if (tid < H) {
+            float Mx = -INFINITY;
+            for (int sp = 0; sp < S; ++sp)
+                if (sl[tid * S + sp] > 0.f) Mx = fmaxf(Mx, sm[tid * S + sp]);
+            float L = 0.f;
+            for (int sp = 0; sp < S; ++sp) {
+                const float l = sl[tid * S + sp];
+                const float w = l > 0.f ? expf(sm[tid * S + sp] - Mx) : 0.f;
+                sm[tid * S + sp] = w;
+                L += w * l;
+            }
+            sinv[tid] = L > 0.f ? 1.0f / L : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+            const int idx = tid + j * blockDim.x, c = 4 * idx, h = c / f.hd, cc = c - h * f.hd;
+            const float* op = f.o_part + ((size_t)(h / f.G) * S * f.G + h % f.G) * f.hd + cc;
+            float a[4] = {0.f, 0.f, 0.f, 0.f};
+            // splits in order; an empty split (weight 0) has no partials written and is skipped
+#pragma unroll
+            for (int sp = 0; sp < GM_SPR; ++sp) {
+                const float w = sp < S ? sm[h * S + sp] : 0.f;
+                if (w != 0.f) {
+                    a[0] += w * ov[j][sp].x;
+                    a[1] += w * ov[j][sp].y;
+                    a[2] += w * ov[j][sp].z;
+                    a[3] += w * ov[j][sp].w;
+                }
+            }
+            for (int sp = GM_SPR; sp < S; ++sp) {
+                const float w = sm[h * S + sp];
+                if (w != 0.f) {
+                    const float4 o4 = *(const float4*)(op + (size_t)sp * f.G * f.hd);
+                    a[0] += w * o4.x;
+                    a[1] += w * o4.y;
+                    a[2] += w * o4.z;
+                    a[3] += w * o4.w;
+                }
+            }
+            const float iv = sinv[h];
+            sx[idx] = make_float4(a[0] * iv, a[1] * iv, a[2] * iv, a[3] * iv);
+        }
+    } else if (pro) {
         // elementwise.hip k_rmsnorm / mamba.hip k_gated_norm: double sum of squares, x * inv * w
         __shared__ double gd_red[16];
         double ss = 0.0;
@@ -1131,7 +1215,10 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
 int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, const GmFuse& f) {
     if ((kind != 2 && kind != 3) || K % 256 != 0) return fail(GH_EUNSUPPORTED, "gemv_fused: kind %d K=%d", kind, K);
     static const int i8_fused = env_int("GH_GEMV_I8_FUSED", 1);
-    if (i8_fused && kind == 3 && K <= 4096 && f.pro != GM_PRO_ATTN && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
+    const bool att_ok = f.pro != GM_PRO_ATTN || (f.H * f.hd == K && f.hd % 4 == 0 && f.H <= 64 &&
+                                                 f.H * f.splits <= GD_ATT_PT * (K / 256) * 64 &&
+                                                 f.H * f.splits <= GD_ATT_MAX && (((uintptr_t)f.o_part) & 15) == 0);
+    if (i8_fused && kind == 3 && K <= 4096 && att_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
         (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
         // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
         // streaming GEMV

@@ -109,3 +109,20 @@ def test_q4k_model_runs_and_matches_oracle(gh):
         compare(ids, r_ids, r_m)
     finally:
         m.close()
+
+
+def test_q4k_model_long_context(gh):
+    """Q4_K, two attention layers of the c1 shape over a 700-token prompt: the
+    decode attention splits the context into more chunks than the merge
+    prologue of the output projection keeps in registers."""
+    c = dict(O.C1)
+    c.update(L=2, layer_types=[1, 1])
+    m = Granite(gh, c, 3, max_ctx=1024)
+    try:
+        prompt = O.rng_below(2, 700, 4096)
+        ids, _ = m.generate(prompt, 10, 1, True)
+        w = O.granite_weights(c, 3)
+        r_ids, r_m = O.granite_generate(O.oracle().orc_granite_generate, c, 3, w, prompt, 10, max_ctx=1024)
+        compare(ids, r_ids, r_m)
+    finally:
+        m.close()
