@@ -243,7 +243,43 @@ def kernel_suite(gh):
     ms = time_launches(gh, lambda: gh.call("gh_apply_rep_penalties", lg.p, V, hp, n, gh.fl(1.1), gh.fl(0.1),
                                            gh.fl(0.1)), 50)
     res[f"rep_penalties_V{V}_hist{n}"] = entry("H2D history + k_rep_penalties", ms, bytes_=n * 4 * 3 + n * 8)
+    # ---------------- GGUF: packed Q4_K blocks of the c2 matrix from a mapped file into HBM
+    res["gguf_read_packed_c2_q4k"] = gguf_load_case(gh)
     return res
+
+
+def gguf_load_case(gh):
+    """Writes the c2 14336x4096 Q4_K matrix to a GGUF file under the system temp
+    folder and times gh_gguf_read_packed into device memory (host page cache -> HBM)."""
+    import tempfile
+    lib = gh.load()
+    N, K = 14336, 4096
+    w = gh.quantize(3, gh.rng_normal(2, N * K, 0, 0.02))
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        names = (C.c_char_p * 1)(b"layers.0.moe_sh_up")
+        types = (C.c_uint32 * 1)(12)
+        nd = (C.c_int * 1)(2)
+        dims = (C.c_uint64 * 8)(K, N)
+        data = (C.c_void_p * 1)(w.ctypes.data)
+        gh.check(lib.gh_gguf_write(path.encode(), 1, names, types, nd, dims, data, 0, None, None, None))
+        h = C.c_void_p()
+        gh.check(lib.gh_gguf_open(path.encode(), C.byref(h)))
+        dev = gh.Buf.zeros(w.nbytes, np.uint8)
+        read = lambda: gh.check(lib.gh_gguf_read_packed(h, b"layers.0.moe_sh_up", 3, dev.p, 1, C.c_size_t(w.nbytes)))
+        read()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            read()
+        ms = (time.perf_counter() - t0) / 5 * 1e3
+        lib.gh_gguf_close(h)
+        e = entry("gguf_read_packed (mapped file -> hipMemcpy, PCIe)", ms, bytes_=w.nbytes)
+        e["bound"] = "pcie"
+        e.pop("frac", None)
+        return e
+    finally:
+        os.unlink(path)
 
 
 def cpu_baseline(prompt, n_prefill=16, n_new=6):

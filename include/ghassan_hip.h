@@ -179,6 +179,37 @@ int gh_moe_route(const float* x, const float* router_w, const float* router_bias
  * grouped [N*K], offsets [ne+1] (device). */
 int gh_moe_permute(const int32_t* idx, int64_t N, int K, int ne, int32_t* grouped, int32_t* offsets);
 
+/* ------------------------------------------------------------------ GGUF */
+/* format/gguf_codec.h:150-205 GGUFReader (open / tensors / find_tensor / get_* /
+ * read_tensor_quant / read_tensor_f32), widened: GGML Q4_K (type 12) is accepted
+ * next to F32, F16, Q4_0, Q4_1 and Q8_0, and packed blocks go from the mapped
+ * file straight into device memory (dst_dev = GH_DEV_GPU) or host memory.
+ * Errors use the reference's "gguf_format: ..." messages. */
+typedef struct gh_gguf gh_gguf;
+int gh_gguf_open(const char* path, gh_gguf** out);
+int gh_gguf_close(gh_gguf* f);
+int64_t gh_gguf_tensor_count(const gh_gguf* f);
+/* dims8: up to 8 dimensions, innermost (row length) first, as stored. */
+int gh_gguf_tensor_info(const gh_gguf* f, int64_t i, const char** name, uint32_t* ggml_type, int* ndims,
+                        uint64_t* dims8, uint64_t* nbytes);
+/* index of a tensor by the backend (= reference internal) name, or by the
+ * llama.cpp alias GGUFReader::find_weight also tries (gguf_codec.cpp:1216-1258); -1 if absent */
+int64_t gh_gguf_find_tensor(const gh_gguf* f, const char* name);
+int gh_gguf_get_u64(const gh_gguf* f, const char* key, uint64_t* out);
+int gh_gguf_get_f32(const gh_gguf* f, const char* key, float* out);
+int gh_gguf_get_str(const gh_gguf* f, const char* key, char* buf, size_t cap);
+/* read_tensor_quant (gguf_codec.cpp:1450-1501): kind 0 Q4_0, 1 Q4_1, 2 Q8_0, 3 Q4_K. A file
+ * tensor of that GGML type is copied verbatim; an F32/F16 one is quantised on the host. */
+int gh_gguf_read_packed(const gh_gguf* f, const char* name, int kind, void* dst, int dst_dev, size_t cap_bytes);
+/* read_tensor_f32 for F32 / F16 tensors; read_f16: the same as fp16 (F16 verbatim). */
+int gh_gguf_read_f32(const gh_gguf* f, const char* name, float* dst, int dst_dev, size_t cap_elems);
+int gh_gguf_read_f16(const gh_gguf* f, const char* name, uint16_t* dst, int dst_dev, size_t cap_elems);
+/* GGUFWriter (gguf_codec.h:64-130) for already-packed host data: GGUF v3, types as above,
+ * metadata scalars (GGUF value types 0-7, 10-12) or strings (8), general.alignment honoured. */
+int gh_gguf_write(const char* path, int n_tensors, const char* const* names, const uint32_t* ggml_types,
+                  const int* ndims, const uint64_t* dims8, const void* const* data, int n_kv,
+                  const char* const* keys, const uint32_t* kv_types, const void* const* kv_values);
+
 /* -------------------------------------------------- host codec / synthetic */
 /* quantization/quantize.cpp:322-341 quantize (host pointers): kinds 0-2 as
  * the reference; kind 3 (Q4_K) our own quantizer. n % block == 0 except Q8_0. */
@@ -207,6 +238,11 @@ int gh_granite_param_count(gh_granite* g);
 int gh_granite_param_name(gh_granite* g, int i, const char** name, size_t* nbytes);
 int gh_granite_get_param(gh_granite* g, const char* name, void* host, size_t nbytes);
 int gh_granite_reset(gh_granite* g);
+/* load_model_from_gguf (gguf_codec.cpp:1507-1564) for a created model: every
+ * parameter by its name (or llama.cpp alias) from the file, packed weights in
+ * the model's kind (verbatim when the file holds that kind, including Q4_K),
+ * fp16 / fp32 vectors decoded. Shapes must match the model's configuration. */
+int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f);
 /* Generator::prefill + first logits (inference/generator.cpp:917-983).
  * logits_host may be NULL. mamba_mode: 0 token-by-token state updates
  * (the reference's order), 1 chunked SSD scan. */

@@ -632,6 +632,26 @@ int gh_granite_set_param(gh_granite* g, const char* name, const void* host, size
     return GH_OK;
 }
 
+int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f) {
+    GH_REQUIRE(g && f, "granite_load_gguf: null argument");
+    for (const Param& p : g->params) {
+        const int64_t ti = gh_gguf_find_tensor(f, p.name.c_str());
+        GH_REQUIRE(ti >= 0, "granite_load_gguf: tensor not found: %s", p.name.c_str());
+        int nd = 0;
+        uint64_t dims[8], nb = 0;
+        GHC(gh_gguf_tensor_info(f, ti, nullptr, nullptr, &nd, dims, &nb));
+        uint64_t numel = 1;
+        for (int i = 0; i < nd; ++i) numel *= dims[i];
+        GH_REQUIRE(numel == (uint64_t)p.numel, "granite_load_gguf: %s has %llu values, the model needs %lld",
+                   p.name.c_str(), (unsigned long long)numel, (long long)p.numel);
+        void* dst = g->wbuf + p.off;
+        if (p.storage == 0) GHC(gh_gguf_read_packed(f, p.name.c_str(), g->qkind, dst, GH_DEV_GPU, p.nbytes));
+        else if (p.storage == 1) GHC(gh_gguf_read_f16(f, p.name.c_str(), (uint16_t*)dst, GH_DEV_GPU, (size_t)p.numel));
+        else GHC(gh_gguf_read_f32(f, p.name.c_str(), (float*)dst, GH_DEV_GPU, (size_t)p.numel));
+    }
+    return GH_OK;
+}
+
 int gh_granite_get_param(gh_granite* g, const char* name, void* host, size_t nbytes) {
     GH_REQUIRE(g && name && host, "granite_get_param: null argument");
     auto it = g->by_name.find(name);

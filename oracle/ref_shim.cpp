@@ -16,6 +16,7 @@
 #include "core/dtype.h"
 #include "quantization/quantize.h"
 #include "model/model.h"
+#include "format/gguf_codec.h"
 #define private public
 #include "inference/generator.h"
 #undef private
@@ -257,4 +258,42 @@ int ref_granite_param_table(const i32* cfg, const float* fcfg, int max_ctx, char
     return i;
 }
 
+
+// GGUF through the reference's own writer and reader (format/gguf_codec.cpp):
+// three tensors of the given f32 values -- F32 [r0][64], Q8_0 [r1][64] and
+// F16 [r2][64] -- plus a few metadata keys.
+int ref_gguf_write(const char* path, const float* a, int r0, const float* b, int r1, const float* c, int r2) {
+    auto mk = [](const float* v, int rows) {
+        Tensor t({(i64)rows, 64}, DType::F32, Device::CPU);
+        std::memcpy(t.data_ptr(), v, sizeof(float) * (size_t)rows * 64);
+        return t;
+    };
+    GGUFWriter w(path);
+    w.set_arch("ghassan");
+    w.set_hidden_size(64);
+    w.set_num_layers(2);
+    w.set_rms_eps(1e-5f);
+    w.add_tensor("layers.0.attn_norm", mk(a, r0), GGMLType::F32);
+    w.add_tensor("layers.0.wq", mk(b, r1), GGMLType::Q8_0);
+    w.add_tensor("tok_embeddings", mk(c, r2), GGMLType::F16);
+    w.write();
+    return 0;
+}
+// packed bytes of a Q8_0 tensor as the reference's loader returns them
+long ref_gguf_read_q8(const char* path, const char* name, void* out, long cap) {
+    GGUFReader r;
+    if (!r.open(path)) return -1;
+    Tensor t = r.read_tensor_quant(name, DType::Q8_0);
+    if ((long)t.nbytes() > cap) return -2;
+    std::memcpy(out, t.data_ptr(), t.nbytes());
+    return (long)t.nbytes();
+}
+long ref_gguf_read_f32(const char* path, const char* name, float* out, long cap) {
+    GGUFReader r;
+    if (!r.open(path)) return -1;
+    Tensor t = r.read_tensor_f32(name);
+    if ((long)t.numel() > cap) return -2;
+    std::memcpy(out, t.data_ptr(), sizeof(float) * (size_t)t.numel());
+    return (long)t.numel();
+}
 }  // extern "C"
