@@ -563,13 +563,23 @@ static bool dec_v2() {
     return v2;
 }
 
+// shortest run of positions per split (env GH_ATTN_CHUNK_MIN, a multiple of 64)
+int attn_chunk_min() {
+    static const int v = [] {
+        const char* e = getenv("GH_ATTN_CHUNK_MIN");
+        const int c = e ? atoi(e) : 64;
+        return c >= 64 ? c / 64 * 64 : 64;
+    }();
+    return v;
+}
+
 static int pick_chunk(int len, int blocks_other, int cap = DEC_CHUNK_MAX) {
     // enough blocks to fill the chip, runs of 64..512 positions
     const int target = 2 * num_cus();
     int per = cdiv(target, blocks_other > 0 ? blocks_other : 1);
     int chunk = cdiv(len > 0 ? len : 1, per > 0 ? per : 1);
     chunk = (chunk + 63) / 64 * 64;
-    if (chunk < 128) chunk = 128;
+    if (chunk < attn_chunk_min()) chunk = attn_chunk_min();
     if (chunk > cap) chunk = cap;
     return chunk;
 }

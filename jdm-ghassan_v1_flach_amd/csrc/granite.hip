@@ -411,12 +411,15 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
 // [merge+wo+residual]), per MoE 3 ([norm+route], gate/up, [down+combine+
 // residual]); begin, lm head and argmax+record around them. Returns
 // GH_EUNSUPPORTED before launching anything if a shape does not fit.
+namespace gh {
+int attn_chunk_min();
+}
 static bool fused_supported(const gh_granite* g) {
     const int k = g->qkind;
     if (k != 2 && k != 3) return false;
     if (g->d % 256 || g->di % 256 || g->qd % 256 || g->qd % 16 || g->kvd % 16) return false;
     if (g->mds != 64 && g->mds != 128) return false;
-    const int chunk_min = 128;
+    const int chunk_min = attn_chunk_min();
     if ((g->max_ctx + chunk_min - 1) / chunk_min > 64) return false;  // attention merge in the wo prologue
     return true;
 }
