@@ -41,7 +41,34 @@ struct GmFuse {
     const float* conv_b = nullptr;
     float* conv_win = nullptr;
     int c0 = 0, cdim = 0, ck = 0;
+    // start of a decode step folded into the first layer's norm prologue: the activation is the
+    // fp16 embedding row of token bctl[0] (zero if out of range), block 0 also stores it to
+    // emb_out and takes the step's cache slot (decode_alloc_slot). Only the int8 Q4_K path.
+    const uint16_t* emb = nullptr;
+    float* emb_out = nullptr;
+    int32_t* bctl = nullptr;
+    int vocab = 0;
 };
+
+// The decode control block: [0] token, [1] cache length, [2] ring start, [3] pinned prefix,
+// [4] capacity, [5] slot of the new token. A slot of the ring cache with a pinned prefix
+// (inference/kv_cache.h:75-92): append while there is room, else overwrite the oldest
+// unpinned position and advance the ring start. One thread.
+__device__ inline void decode_alloc_slot(int32_t* ctl) {
+    const int cap = ctl[4], pin = ctl[3];
+    int len = ctl[1], start = ctl[2], slot;
+    if (len < cap) {
+        slot = len;
+        if (len >= pin) slot = pin + ((start + (len - pin)) % (cap - pin));
+        ++len;
+    } else {
+        slot = pin + (start % (cap - pin));
+        start = (start + 1) % (cap - pin);
+    }
+    ctl[1] = len;
+    ctl[2] = start;
+    ctl[5] = slot;
+}
 
 // y = f(x) . W^T for ONE token, K-quant (kind 3) or Q8_0 (kind 2) weights,
 // K a multiple of 256. Returns GH_EUNSUPPORTED if the shape is not handled.

@@ -785,10 +785,23 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             lds_dma16s(x, (uint32_t)(tid + j * blockDim.x) * 16u, lds_addr(&sx[wave * 64 + j * blockDim.x]));
     } else {
         // prologue operands requested now; the values are formed while the first tile streams in
+        const bool emb = FUSED && f.emb != nullptr;
+        const int tok = emb ? f.bctl[0] : 0;
+        const bool tok_ok = tok >= 0 && tok < f.vocab;
 #pragma unroll
         for (int j = 0; j < SBW; ++j) {
             const int idx = tid + j * blockDim.x;
-            pv[j] = ((const float4*)x)[idx];
+            if (emb) {  // elementwise.hip k_embed_half: the token's fp16 row (zero out of range)
+                pv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (tok_ok) {
+                    const uint2 h = ((const uint2*)(f.emb + (size_t)tok * K))[idx];
+                    pv[j] = make_float4(f16_to_f32((uint16_t)(h.x & 0xFFFF)), f16_to_f32((uint16_t)(h.x >> 16)),
+                                        f16_to_f32((uint16_t)(h.y & 0xFFFF)), f16_to_f32((uint16_t)(h.y >> 16)));
+                }
+                if (blockIdx.x == 0) ((float4*)f.emb_out)[idx] = pv[j];
+            } else {
+                pv[j] = ((const float4*)x)[idx];
+            }
             pw[j] = ((const float4*)f.pw)[idx];
             if (f.pro == GM_PRO_GATED) {
                 const float4 z = ((const float4*)f.pz)[idx];
@@ -800,6 +813,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             }
         }
     }
+    if (FUSED && f.emb != nullptr && blockIdx.x == 0 && tid == 0) decode_alloc_slot(f.bctl);
     // column `wave` of a tile -> ring slice; piece q = PR r + j of row r
     uint32_t voff[PPL];
 #pragma unroll
@@ -1218,12 +1232,15 @@ int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, 
     const bool att_ok = f.pro != GM_PRO_ATTN || (f.H * f.hd == K && f.hd % 4 == 0 && f.H <= 64 &&
                                                  f.H * f.splits <= GD_ATT_PT * (K / 256) * 64 &&
                                                  f.H * f.splits <= GD_ATT_MAX && (((uintptr_t)f.o_part) & 15) == 0);
-    if (i8_fused && kind == 3 && K <= 4096 && att_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
+    const bool emb_ok = !f.emb || (f.pro == GM_PRO_RMSNORM && f.bctl && f.emb_out && f.vocab > 0 &&
+                                   (((uintptr_t)f.emb | (uintptr_t)f.emb_out) & 15) == 0);
+    if (i8_fused && kind == 3 && K <= 4096 && att_ok && emb_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
         (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
         // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
         // streaming GEMV
         return gd_launch<1, 2, true>(x, (const uint8_t*)w, y, K, N, f);
     }
+    if (f.emb) return GH_EUNSUPPORTED;  // the folded step start exists on the int8 path only (no launch made)
     if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
     if (f.pro == GM_PRO_ATTN && (f.splits > 64 || f.H * f.hd != K))
         return fail(GH_EUNSUPPORTED, "gemv_fused: attention merge of %d splits", f.splits);

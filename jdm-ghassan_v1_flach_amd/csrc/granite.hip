@@ -27,7 +27,7 @@ int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void
                      const float* conv_b, const float* dt_bias, const float* a_log, const float* D,
                      const float* norm_w, const void* w_out, float* conv_state, float* ssm_state, float* out,
                      bool add, int d, int d_inner, int conv_dim, int n_heads, int d_head, int d_state, int k,
-                     float eps, int kind);
+                     float eps, int kind, const GmFuse* begin = nullptr);
 int moe_decode_fused(float* xres, const float* nw, float eps, const float* rw, const float* bias, const void* gates,
                      const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, int N,
                      int d, int E, int ne, int K, int SH, int qkind);
@@ -48,23 +48,11 @@ enum {
     CTL_TOKEN = 0, CTL_LEN = 1, CTL_START = 2, CTL_PINNED = 3, CTL_CAP = 4, CTL_SLOT = 5, CTL_STEP = 6,
     CTL_AMAX = 8, CTL_AMAX_CNT = 10, CTL_AMAX_NEG0 = 11, CTL_N = 12
 };
+static_assert(CTL_TOKEN == 0 && CTL_LEN == 1 && CTL_START == 2 && CTL_PINNED == 3 && CTL_CAP == 4 && CTL_SLOT == 5,
+              "decode_alloc_slot (gemv_fuse.h) indexes the control block by these positions");
 
 // KVCache::allocate_slot (inference/kv_cache.h:74-92) on the device.
-__global__ void k_alloc_slot(int32_t* ctl) {
-    const int cap = ctl[CTL_CAP], pin = ctl[CTL_PINNED];
-    int len = ctl[CTL_LEN], start = ctl[CTL_START], slot;
-    if (len < cap) {
-        slot = len;
-        if (len >= pin) slot = pin + ((start + (len - pin)) % (cap - pin));
-        ++len;
-    } else {
-        slot = pin + (start % (cap - pin));
-        start = (start + 1) % (cap - pin);
-    }
-    ctl[CTL_LEN] = len;
-    ctl[CTL_START] = start;
-    ctl[CTL_SLOT] = slot;
-}
+__global__ void k_alloc_slot(int32_t* ctl) { decode_alloc_slot(ctl); }
 
 // K/V of one token -> fp16 cache rows at the slot chosen by k_alloc_slot.
 __global__ void k_store_kv(const float* __restrict__ k, const float* __restrict__ v, uint16_t* __restrict__ kc,
@@ -87,21 +75,7 @@ __global__ void k_record_token(int32_t* ctl, int32_t* ids, int cap) {
 // and its embedding row (elementwise.hip k_embed_half) in one launch.
 __global__ void k_step_begin(int32_t* ctl, const uint16_t* __restrict__ tab, float* __restrict__ x, int dim,
                              int vocab) {
-    if (threadIdx.x == 0) {
-        const int cap = ctl[CTL_CAP], pin = ctl[CTL_PINNED];
-        int len = ctl[CTL_LEN], start = ctl[CTL_START], slot;
-        if (len < cap) {
-            slot = len;
-            if (len >= pin) slot = pin + ((start + (len - pin)) % (cap - pin));
-            ++len;
-        } else {
-            slot = pin + (start % (cap - pin));
-            start = (start + 1) % (cap - pin);
-        }
-        ctl[CTL_LEN] = len;
-        ctl[CTL_START] = start;
-        ctl[CTL_SLOT] = slot;
-    }
+    if (threadIdx.x == 0) decode_alloc_slot(ctl);
     const int id = ctl[CTL_TOKEN];
     for (int i = threadIdx.x; i < dim; i += blockDim.x)
         x[i] = (id < 0 || id >= vocab) ? 0.f : f16_to_f32(tab[(size_t)id * dim + i]);
@@ -426,18 +400,50 @@ static bool fused_supported(const gh_granite* g) {
 
 static int decode_step_fused(gh_granite* g, bool argmax) {
     const int d = g->d;
-    hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(256), 0, stream(), g->ctl, (const uint16_t*)g->W("tok_embeddings"),
-                       g->x, d, g->V);
-    GH_LAUNCHED("k_step_begin");
+    static const int fold_begin = [] {
+        const char* e = getenv("GH_BEGIN_FUSED");
+        return e ? atoi(e) : 1;
+    }();
+    // the step's start (slot + embedding row) runs inside layer 0's first GEMV when its path
+    // takes it; otherwise (GH_EUNSUPPORTED before any launch) as k_step_begin
+    GmFuse begin;
+    begin.emb = (const uint16_t*)g->W("tok_embeddings");
+    begin.emb_out = g->x;
+    begin.bctl = g->ctl;
+    begin.vocab = g->V;
+    bool begun = !fold_begin;
+    auto launch_begin = [&]() -> int {
+        hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(256), 0, stream(), g->ctl, begin.emb, g->x, d, g->V);
+        GH_LAUNCHED("k_step_begin");
+        begun = true;
+        return GH_OK;
+    };
+    if (begun) GHC(launch_begin());
     for (int l = 0; l < g->L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
         if (g->lt[l] == 0) {
             const std::string mp = pre + "mamba.";
-            GHC(mamba_step_fused(g->x, g->F(pre + "attn_norm"), g->eps, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
-                                 g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"), g->F(mp + "D"),
-                                 g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->conv[l], g->ssm[l], g->x, true, d,
-                                 g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck, g->eps, g->qkind));
+            auto run = [&](const GmFuse* b) {
+                return mamba_step_fused(g->x, g->F(pre + "attn_norm"), g->eps, g->W(mp + "in_proj"),
+                                        g->F(mp + "conv1d.weight"), g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"),
+                                        g->F(mp + "A_log"), g->F(mp + "D"), g->F(mp + "norm.weight"),
+                                        g->W(mp + "out_proj"), g->conv[l], g->ssm[l], g->x, true, d, g->di,
+                                        g->conv_dim, g->mh, g->mdh, g->mds, g->ck, g->eps, g->qkind, b);
+            };
+            if (!begun) {
+                const int rc = run(&begin);
+                if (rc == GH_OK) {
+                    begun = true;
+                } else {
+                    if (rc != GH_EUNSUPPORTED) return rc;
+                    GHC(launch_begin());
+                    GHC(run(nullptr));
+                }
+            } else {
+                GHC(run(nullptr));
+            }
         } else {
+            if (!begun) GHC(launch_begin());
             GmFuse f1;
             f1.pro = GM_PRO_RMSNORM;
             f1.pw = g->F(pre + "attn_norm");

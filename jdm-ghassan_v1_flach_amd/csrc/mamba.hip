@@ -662,9 +662,10 @@ int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void
                      const float* conv_b, const float* dt_bias, const float* a_log, const float* D,
                      const float* norm_w, const void* w_out, float* conv_state, float* ssm_state, float* out,
                      bool add, int d, int d_inner, int conv_dim, int n_heads, int d_head, int d_state, int k,
-                     float eps, int kind) {
+                     float eps, int kind, const GmFuse* begin) {
     if ((kind != 2 && kind != 3) || d % 256 || d_inner % 256 || (d_state != 64 && d_state != 128))
         return GH_EUNSUPPORTED;
+    if (begin && !nw) return GH_EUNSUPPORTED;  // the step's start rides on the norm prologue
     const int proj = d_inner + conv_dim + n_heads;
     float* pr = (float*)workspace(WS_MAMBA_PROJ, (size_t)proj * 4);
     float* yb = (float*)workspace(WS_MAMBA_Y, (size_t)d_inner * 4 * 2);
@@ -680,6 +681,12 @@ int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void
     f1.c0 = d_inner;
     f1.cdim = conv_dim;
     f1.ck = k;
+    if (begin) {
+        f1.emb = begin->emb;
+        f1.emb_out = begin->emb_out;
+        f1.bctl = begin->bctl;
+        f1.vocab = begin->vocab;
+    }
     int rc = gemv_fused(x, w_in, pr, d, proj, kind, f1);
     if (rc) return rc;
     const float* xbc = pr + d_inner;  // conv output, in place of the raw xBC
@@ -747,7 +754,7 @@ int gh_mamba2_step_half(const float* x, const void* w_in, const float* conv_w, c
     {
         const int rc = mamba_step_fused(x, nullptr, 0.f, w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w, w_out,
                                         conv_state, ssm_state, out, false, d, d_inner, conv_dim, n_heads, d_head,
-                                        d_state, k, eps, kind);
+                                        d_state, k, eps, kind, nullptr);
         if (rc != GH_EUNSUPPORTED) return rc;
     }
     const int proj = d_inner + conv_dim + n_heads;
