@@ -412,7 +412,13 @@ static int launch_route(const float* x, const float* rw, const float* bias, floa
         return GH_OK;
     }
     const size_t rl_lds = (size_t)RL_E * (d / 4 + 1) * 16;
-    if (N > 8 && !nw && ne <= 64 && K <= 8 && d % 4 == 0 && rl_lds <= 160 * 1024) {
+    // below 16 experts (c1: 8) a 16-expert slice leaves half the lanes idle and a 128-token
+    // prefill fills 4 blocks; one block per token (k_route) is faster there (c1 prefill +5 %)
+    static const int rl_min_ne = [] {
+        const char* e = getenv("GH_RL_MIN_NE");
+        return e ? atoi(e) : 16;
+    }();
+    if (N > 8 && !nw && ne <= 64 && ne >= rl_min_ne && K <= 8 && d % 4 == 0 && rl_lds <= 160 * 1024) {
         static bool configured = false;
         if (!configured) {
             const hipError_t e = hipFuncSetAttribute((const void*)k_route_logits,
