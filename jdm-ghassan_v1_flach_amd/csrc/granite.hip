@@ -387,6 +387,7 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
 // GH_EUNSUPPORTED before launching anything if a shape does not fit.
 namespace gh {
 int attn_chunk_min();
+float** moe_accumulate_slot();
 }
 static bool fused_supported(const gh_granite* g) {
     const int k = g->qkind;
@@ -742,8 +743,14 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
         }
         if (g->lt[l] == 0 && mamba_mode == 0) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, P, d, g->eps));
-        GHC(moe_layer(g, l, g->xb, g->pr, P));
-        GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        // x += moe(x): added by the combine launch when the path has one, else here
+        float** acc = moe_accumulate_slot();
+        *acc = g->x;
+        const int mrc = moe_layer(g, l, g->xb, g->pr, P);
+        const bool pending = *acc != nullptr;
+        *acc = nullptr;
+        if (mrc) return mrc;
+        if (pending) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
     }
     // cache length P, ring start 0 (KVCache::set_length)
     const int32_t lenstart[2] = {P, 0};

@@ -874,7 +874,7 @@ static int down_lpr(int E, int SH, bool has_sh) {
 // in slot order).
 __global__ void k_moe_combine(const float* __restrict__ ysh, const float* __restrict__ y,
                               const int32_t* __restrict__ pos, const float* __restrict__ w, float* __restrict__ out,
-                              int N, int K, int d) {
+                              int N, int K, int d, int accumulate) {
     const int t = blockIdx.x;
     for (int j = threadIdx.x; j < d; j += blockDim.x) {
         float acc = ysh ? ysh[(size_t)t * d + j] : 0.f;
@@ -883,8 +883,20 @@ __global__ void k_moe_combine(const float* __restrict__ ysh, const float* __rest
             const int r = pos ? pos[s] : s;
             acc += w[s] * y[(size_t)r * d + j];
         }
-        out[(size_t)t * d + j] = acc;
+        // accumulate: the residual add x + moe(x) of the caller, the same single addition
+        out[(size_t)t * d + j] = accumulate ? out[(size_t)t * d + j] + acc : acc;
     }
+}
+
+// A caller's residual stream to add the combined output into, taken by the
+// next k_moe_combine launch (which then writes there instead of `out`); a path
+// without that launch leaves it set and the caller adds `out` itself.
+static float* g_moe_acc_dst = nullptr;
+float** moe_accumulate_slot() { return &g_moe_acc_dst; }
+static void combine_target(float*& out, int& acc) {
+    acc = g_moe_acc_dst != nullptr;
+    if (acc) out = g_moe_acc_dst;
+    g_moe_acc_dst = nullptr;
 }
 
 // ===================================================== prefill: grouped GEMM
@@ -1202,8 +1214,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             const int rpb2 = rows_per_block(E) < rows_per_block(SH) ? rows_per_block(E) : rows_per_block(SH);
             hipLaunchKernelGGL((k_moe_gemv<KIND, false>), dim3(cdiv(d, rpb2), S + D.N), dim3(256), 0, stream(), D);
             GH_LAUNCHED("k_moe_gemv(down)");
-            hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, nullptr,
-                               w_route, out, N, K, d);
+            {
+                float* cdst = out;
+                int cacc = 0;
+                combine_target(cdst, cacc);
+                hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr,
+                                   nullptr, w_route, cdst, N, K, d, cacc);
+            }
             GH_LAUNCHED("k_moe_combine");
             return GH_OK;
         }
@@ -1264,8 +1281,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
             GH_LAUNCHED("k_moe_group_gemm2(shared)");
         }
-        hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
-                           out, N, K, d);
+        {
+            float* cdst = out;
+            int cacc = 0;
+            combine_target(cdst, cacc);
+            hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos,
+                               w_route, cdst, N, K, d, cacc);
+        }
         GH_LAUNCHED("k_moe_combine");
         return GH_OK;
     }
@@ -1299,8 +1321,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         hipLaunchKernelGGL((k_moe_group_gemm<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
         GH_LAUNCHED("k_moe_group_gemm(shared)");
     }
-    hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
-                       out, N, K, d);
+    {
+        float* cdst = out;
+        int cacc = 0;
+        combine_target(cdst, cacc);
+        hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
+                           cdst, N, K, d, cacc);
+    }
     GH_LAUNCHED("k_moe_combine");
     return GH_OK;
 }
