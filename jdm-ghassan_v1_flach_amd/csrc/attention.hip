@@ -557,21 +557,8 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
     }
 }
 
-// the MFMA decode kernel (head_dim 64 / 128) unless GH_ATTN_DEC_OLD is set
-static bool dec_v2() {
-    static const bool v2 = getenv("GH_ATTN_DEC_OLD") == nullptr;
-    return v2;
-}
-
-// shortest run of positions per split (env GH_ATTN_CHUNK_MIN, a multiple of 64)
-int attn_chunk_min() {
-    static const int v = [] {
-        const char* e = getenv("GH_ATTN_CHUNK_MIN");
-        const int c = e ? atoi(e) : 64;
-        return c >= 64 ? c / 64 * 64 : 64;
-    }();
-    return v;
-}
+// shortest run of positions per split (a multiple of 64)
+int attn_chunk_min() { return 64; }
 
 static int pick_chunk(int len, int blocks_other, int cap = DEC_CHUNK_MAX) {
     // enough blocks to fill the chip, runs of 64..512 positions
@@ -597,7 +584,7 @@ static void launch_dec2(const DecodeArgs& a, dim3 grid) {
 // writes back L2.)
 template <bool PAGED>
 static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
-    const bool v2 = dec_v2() && (hd == 64 || hd == 128) && a.G <= 8;
+    const bool v2 = (hd == 64 || hd == 128) && a.G <= 8;
     a.chunk = pick_chunk(span, a.KV * S, v2 ? DEC2_CHUNK_MAX : DEC_CHUNK_MAX);
     a.splits = cdiv(span > 0 ? span : 1, a.chunk);
     float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
@@ -1074,7 +1061,7 @@ int attn_decode_partials_devctl(const float* q, const uint16_t* kc, const uint16
 
 int attention_prefill(const float* q, const float* k, const float* v, float* out, int B, int T, int H, int KV, int hd,
                       float scale, int window) {
-    if ((hd == 64 || hd == 128) && !getenv("GH_ATTN_PF_OLD")) {
+    if (hd == 64 || hd == 128) {
         const int Tp = cdiv(T, PF_BK) * PF_BK;
         _Float16* kv16 = (_Float16*)workspace(WS_ATTN_KV16, (size_t)B * KV * Tp * hd * 2 * 2);
         if (!kv16) return fail(GH_ENOMEM, "attention prefill: workspace");

@@ -576,14 +576,10 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
         }
     }
     if constexpr (KIND == 2 || KIND == 3) {
-        static const int v4 = [] {
-            const char* e = getenv("GH_GEMM_V4");
-            return e ? atoi(e) : 1;
-        }();
         const int tiles = cdiv(M, G4M) * cdiv(N, G4N), T = K / 64;
         // 256x256 tiles once they fill the chip (split K in two when that is needed to fill it)
         const int split = tiles >= num_cus() ? 1 : (2 * tiles >= num_cus() && T % 4 == 0) ? 2 : 0;
-        if (v4 && K % 256 == 0 && split && (split == 1 || ((size_t)M * N % 4 == 0 && ((uintptr_t)yout & 15) == 0))) {
+        if (K % 256 == 0 && split && (split == 1 || ((size_t)M * N % 4 == 0 && ((uintptr_t)yout & 15) == 0))) {
             static bool configured = false;
             if (!configured) {
                 const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_q4<KIND>,
@@ -631,11 +627,7 @@ int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, 
     const int blocks = cdiv(M, BM) * cdiv(N, BN);
     size_t rowb = kind == 4 ? (size_t)K * 2 : kind == 5 ? (size_t)K * 4 : row_bytes(kind, K);
     const dim3 g(blocks), b(256);
-    static const int v2 = [] {
-        const char* e = getenv("GH_GEMM_V2");
-        return e ? atoi(e) : 1;
-    }();
-    if (v2 && (kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
+    if ((kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
         switch (kind) {
             case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb, accumulate);
             case 3: return gemm2_launch<3>(x, w, y, M, K, N, rowb, accumulate);

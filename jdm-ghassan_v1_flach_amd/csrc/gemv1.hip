@@ -211,26 +211,15 @@ __global__ void __launch_bounds__(256) k_gemv1(const float* __restrict__ x, cons
     }
 }
 
-static int wpc_env() {
-    static const int v = [] {
-        const char* e = getenv("GH_GEMV1_WPC");
-        return e ? atoi(e) : 8;
-    }();
-    return v;
-}
-static int r_env() {
-    static const int v = [] {
-        const char* e = getenv("GH_GEMV1_R");
-        return e ? atoi(e) : 2;
-    }();
-    return v;
-}
+// waves per CU of the persistent grid and rows per lane
+constexpr int GEMV1_WPC = 8;
+constexpr int GEMV1_R = 2;
 
 template <int R>
 static void launch1(const float* x, const void* w, float* y, int K, int N, int kind, int WK) {
     const int GPB = 4 / WK;
     const int ngroups = cdiv(N, R);
-    const int max_blocks = wpc_env() * num_cus() / 4;
+    const int max_blocks = GEMV1_WPC * num_cus() / 4;
     int blocks = cdiv(ngroups, GPB);
     if (blocks > max_blocks) blocks = max_blocks;
     const int iters = cdiv(ngroups, blocks * GPB);
@@ -249,7 +238,7 @@ int gemv1_dispatch(const float* x, const void* w, float* y, int K, int N, int ki
     const int T = K / 64;
     if (T > 256) return 0;
     const int WK = T <= 64 ? 1 : T <= 128 ? 2 : 4;
-    const int r = r_env();
+    const int r = GEMV1_R;
     if (r == 1) launch1<1>(x, w, y, K, N, kind, WK);
     else if (r == 4) launch1<4>(x, w, y, K, N, kind, WK);
     else launch1<2>(x, w, y, K, N, kind, WK);

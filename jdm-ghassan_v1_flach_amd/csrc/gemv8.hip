@@ -155,11 +155,7 @@ static int g8_launch(const float* x, const void* w, float* y, int M, int K, int 
 
 // Returns 1 if handled: Q4_K, 2 <= M <= 8, K a multiple of 256 up to 4096.
 int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
-    static const int enabled = [] {
-        const char* e = getenv("GH_GEMV8");
-        return e ? atoi(e) : 1;
-    }();
-    if (!enabled || kind != 3 || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
+    if (kind != 3 || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
     const int nsb = K / 256;
     // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands and two tiles of
     // weight bytes stay in registers)

@@ -1076,11 +1076,6 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no transfer into LDS outlives the block
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : dflt;
-}
-
 // dynamic LDS budget: 160 KB per workgroup less a reserve for the static
 // arrays of the fusion prologue
 constexpr size_t GM_LDS_MAX = 160 * 1024 - 512;
@@ -1098,8 +1093,7 @@ template <int KIND, int SS>
 static int gm_split(int K, int M, bool pro, int& WB, int& spw) {
     const int nsteps = K / 256 / SS;
     const int wcap = M <= 2 ? 16 : 8;
-    int wmax = env_int("GH_GEMVM_WB", wcap);
-    if (wmax > wcap) wmax = wcap;
+    const int wmax = wcap;
     for (int wb = nsteps < wmax ? nsteps : wmax; wb >= 1; --wb) {
         spw = (nsteps + wb - 1) / wb;
         WB = (nsteps + spw - 1) / spw;
@@ -1122,7 +1116,7 @@ static int gm_launch(const float* x, const void* w, float* y, int M, int K, int 
         attr_set = true;
     }
     const int ntiles = (N + 15) / 16;
-    const int wpc = env_int("GH_GEMVM_WPC", 16);
+    const int wpc = 16;  // waves per CU
     int bpc = wpc / WB;
     if (bpc < 1) bpc = 1;
     const int by_lds = (int)(GM_LDS_MAX / lds);
@@ -1203,15 +1197,11 @@ int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N,
 
 int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
     if (gemv8_dispatch(x, w, y, M, K, N, kind, rc)) return 1;
-    static const int enabled = env_int("GH_GEMV_MFMA", 1);
-    static const int dma = env_int("GH_GEMV_DMA", 1);  // 0 off, else the variant of gemv_q4k_i8
-    if (enabled && dma && M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
-        *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, dma);
+    if (M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
+        *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, 1);
         return 1;
     }
-    static const int q8_m1 = env_int("GH_GEMV_MFMA_Q8M1", 1);
-    if (!enabled || (kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
-    if (kind == 2 && M == 1 && !q8_m1) return 0;
+    if ((kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
     int mc = M;
     while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc, false) : gm_fits<2>(K, mc, false))) --mc;
     if (mc < 1) return 0;
@@ -1228,13 +1218,12 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
 
 int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, const GmFuse& f) {
     if ((kind != 2 && kind != 3) || K % 256 != 0) return fail(GH_EUNSUPPORTED, "gemv_fused: kind %d K=%d", kind, K);
-    static const int i8_fused = env_int("GH_GEMV_I8_FUSED", 1);
     const bool att_ok = f.pro != GM_PRO_ATTN || (f.H * f.hd == K && f.hd % 4 == 0 && f.H <= 64 &&
                                                  f.H * f.splits <= GD_ATT_PT * (K / 256) * 64 &&
                                                  f.H * f.splits <= GD_ATT_MAX && (((uintptr_t)f.o_part) & 15) == 0);
     const bool emb_ok = !f.emb || (f.pro == GM_PRO_RMSNORM && f.bctl && f.emb_out && f.vocab > 0 &&
                                    (((uintptr_t)f.emb | (uintptr_t)f.emb_out) & 15) == 0);
-    if (i8_fused && kind == 3 && K <= 4096 && att_ok && emb_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
+    if (kind == 3 && K <= 4096 && att_ok && emb_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
         (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
         // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
         // streaming GEMV

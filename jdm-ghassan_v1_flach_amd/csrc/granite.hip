@@ -229,11 +229,7 @@ __global__ void __launch_bounds__(256) k_head_argmax(const float* __restrict__ x
 // Returns 1 if launched (fp16 table, d a multiple of 8 up to 2048, 16-byte aligned rows).
 static int launch_head_argmax(const float* x, const float* nw, float eps, const uint16_t* tab, float* logits, int d,
                               int V, int32_t* ctl, int32_t* ids, int cap, bool argmax) {
-    static const int enabled = [] {
-        const char* e = getenv("GH_HEAD_FUSED");
-        return e ? atoi(e) : 1;
-    }();
-    if (!enabled || d % 8 || d > 2048 || (((uintptr_t)x | (uintptr_t)nw | (uintptr_t)tab) & 15)) return 0;
+    if (d % 8 || d > 2048 || (((uintptr_t)x | (uintptr_t)nw | (uintptr_t)tab) & 15)) return 0;
     const dim3 grid((V + 15) / 16), blk(256);
     if (d <= 512)
         hipLaunchKernelGGL(k_head_argmax<1>, grid, blk, 0, stream(), x, nw, eps, tab, logits, d, V, ctl, ids, cap, argmax);
@@ -387,7 +383,10 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
 // GH_EUNSUPPORTED before launching anything if a shape does not fit.
 namespace gh {
 int attn_chunk_min();
-float** moe_accumulate_slot();
+int moe_forward_acc(const float* x, const float* router_w, const float* router_bias, const void* gates,
+                    const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d,
+                    float* out, float* acc_dst, int* added, float* probs_cache, int32_t* idx_cache, float* w_cache,
+                    int64_t N, int d, int E, int ne, int K, int SH, int qkind);
 }
 static bool fused_supported(const gh_granite* g) {
     const int k = g->qkind;
@@ -401,10 +400,6 @@ static bool fused_supported(const gh_granite* g) {
 
 static int decode_step_fused(gh_granite* g, bool argmax) {
     const int d = g->d;
-    static const int fold_begin = [] {
-        const char* e = getenv("GH_BEGIN_FUSED");
-        return e ? atoi(e) : 1;
-    }();
     // the step's start (slot + embedding row) runs inside layer 0's first GEMV when its path
     // takes it; otherwise (GH_EUNSUPPORTED before any launch) as k_step_begin
     GmFuse begin;
@@ -412,14 +407,13 @@ static int decode_step_fused(gh_granite* g, bool argmax) {
     begin.emb_out = g->x;
     begin.bctl = g->ctl;
     begin.vocab = g->V;
-    bool begun = !fold_begin;
+    bool begun = false;
     auto launch_begin = [&]() -> int {
         hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(256), 0, stream(), g->ctl, begin.emb, g->x, d, g->V);
         GH_LAUNCHED("k_step_begin");
         begun = true;
         return GH_OK;
     };
-    if (begun) GHC(launch_begin());
     for (int l = 0; l < g->L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
         if (g->lt[l] == 0) {
@@ -489,11 +483,7 @@ static int decode_step_fused(gh_granite* g, bool argmax) {
 }
 
 static int decode_step(gh_granite* g, bool argmax) {
-    static const int fused = [] {
-        const char* e = getenv("GH_DECODE_FUSED");
-        return e ? atoi(e) : 1;
-    }();
-    if (fused && fused_supported(g)) return decode_step_fused(g, argmax);
+    if (fused_supported(g)) return decode_step_fused(g, argmax);
     return decode_step_dev(g, argmax);
 }
 
@@ -744,13 +734,12 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
         if (g->lt[l] == 0 && mamba_mode == 0) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, P, d, g->eps));
         // x += moe(x): added by the combine launch when the path has one, else here
-        float** acc = moe_accumulate_slot();
-        *acc = g->x;
-        const int mrc = moe_layer(g, l, g->xb, g->pr, P);
-        const bool pending = *acc != nullptr;
-        *acc = nullptr;
-        if (mrc) return mrc;
-        if (pending) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        int added = 0;
+        GHC(moe_forward_acc(g->xb, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
+                            g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"),
+                            g->W(pre + "moe_sh_down"), g->pr, g->x, &added, nullptr, nullptr, nullptr, P, d, g->E,
+                            g->ne, g->K, g->SH, g->qkind));
+        if (!added) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
     }
     // cache length P, ring start 0 (KVCache::set_length)
     const int32_t lenstart[2] = {P, 0};

@@ -704,7 +704,13 @@ int mamba_step_fused(const float* x, const float* nw, float norm_eps, const void
     f3.pw = norm_w;
     f3.eps = eps;
     f3.epi = add ? GM_EPI_ADD : GM_EPI_STORE;
-    return gemv_fused(yb, w_out, out, d_inner, d, kind, f3);
+    rc = gemv_fused(yb, w_out, out, d_inner, d, kind, f3);
+    // GH_EUNSUPPORTED means "nothing launched, take another path" only before the first launch:
+    // here the in_proj has already advanced the conv window and the scan the SSM state
+    if (rc == GH_EUNSUPPORTED)
+        return fail(GH_EINVAL, "mamba step: out_proj (K=%d N=%d kind %d) unsupported after the state advanced",
+                    d_inner, d, kind);
+    return rc;
 }
 
 }  // namespace gh

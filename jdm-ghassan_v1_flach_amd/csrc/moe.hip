@@ -414,11 +414,7 @@ static int launch_route(const float* x, const float* rw, const float* bias, floa
     const size_t rl_lds = (size_t)RL_E * (d / 4 + 1) * 16;
     // below 16 experts (c1: 8) a 16-expert slice leaves half the lanes idle and a 128-token
     // prefill fills 4 blocks; one block per token (k_route) is faster there (c1 prefill +5 %)
-    static const int rl_min_ne = [] {
-        const char* e = getenv("GH_RL_MIN_NE");
-        return e ? atoi(e) : 16;
-    }();
-    if (N > 8 && !nw && ne <= 64 && ne >= rl_min_ne && K <= 8 && d % 4 == 0 && rl_lds <= 160 * 1024) {
+    if (N > 8 && !nw && ne <= 64 && ne >= 16 && K <= 8 && d % 4 == 0 && rl_lds <= 160 * 1024) {
         static bool configured = false;
         if (!configured) {
             const hipError_t e = hipFuncSetAttribute((const void*)k_route_logits,
@@ -851,11 +847,7 @@ __global__ void __launch_bounds__(576) k_moe_down_par(GemvJobs J, const float* _
 
 template <int KIND>
 static bool down_par_fits(bool has_sh, int K, int E, int SH) {
-    static const int on = [] {
-        const char* e = getenv("GH_MOE_DOWN_PAR");
-        return e ? atoi(e) : 1;
-    }();
-    return on && KIND != 4 && has_sh && K <= 8 && E % 64 == 0 && SH % 64 == 0 && E / 64 <= DP_LPR * DP_TPL &&
+    return KIND != 4 && has_sh && K <= 8 && E % 64 == 0 && SH % 64 == 0 && E / 64 <= DP_LPR * DP_TPL &&
            SH / 64 <= DP_LPR * DP_TPL;
 }
 
@@ -888,15 +880,15 @@ __global__ void k_moe_combine(const float* __restrict__ ysh, const float* __rest
     }
 }
 
-// A caller's residual stream to add the combined output into, taken by the
-// next k_moe_combine launch (which then writes there instead of `out`); a path
-// without that launch leaves it set and the caller adds `out` itself.
-static float* g_moe_acc_dst = nullptr;
-float** moe_accumulate_slot() { return &g_moe_acc_dst; }
-static void combine_target(float*& out, int& acc) {
-    acc = g_moe_acc_dst != nullptr;
-    if (acc) out = g_moe_acc_dst;
-    g_moe_acc_dst = nullptr;
+// Target of the ordered combine: the caller's residual stream `acc_dst` when given (the combine
+// then adds into it, and *added records that it did), else `out`. Paths without a combine
+// launch (decode down kernels) leave *added at 0 and the caller adds `out` itself.
+static void combine_target(float* acc_dst, int* added, float*& out, int& acc) {
+    acc = acc_dst != nullptr;
+    if (acc) {
+        out = acc_dst;
+        if (added) *added = 1;
+    }
 }
 
 // ===================================================== prefill: grouped GEMM
@@ -1169,8 +1161,8 @@ __global__ void k_single_group_tiles(int32_t* tiles, int32_t* offs, int N, int b
 
 template <int KIND>
 static int moe_kind(const float* x, const float* w_route, const int32_t* idx, const void* gates, const void* ups,
-                    const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, float* out, int N, int d,
-                    int E, int ne, int K, int SH) {
+                    const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, float* out, float* acc_dst,
+                    int* added, int N, int d, int E, int ne, int K, int SH) {
     const int S = N * K;
     const bool has_sh = sh_g && sh_u && sh_d;
     const size_t rowb_d = KIND == 4 ? (size_t)d * 2 : row_bytes(KIND, d);
@@ -1217,7 +1209,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             {
                 float* cdst = out;
                 int cacc = 0;
-                combine_target(cdst, cacc);
+                combine_target(acc_dst, added, cdst, cacc);
                 hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr,
                                    nullptr, w_route, cdst, N, K, d, cacc);
             }
@@ -1284,7 +1276,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         {
             float* cdst = out;
             int cacc = 0;
-            combine_target(cdst, cacc);
+            combine_target(acc_dst, added, cdst, cacc);
             hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos,
                                w_route, cdst, N, K, d, cacc);
         }
@@ -1324,7 +1316,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
     {
         float* cdst = out;
         int cacc = 0;
-        combine_target(cdst, cacc);
+        combine_target(acc_dst, added, cdst, cacc);
         hipLaunchKernelGGL(k_moe_combine, dim3(N), dim3(256), 0, stream(), has_sh ? sh_y : nullptr, yr, pos, w_route,
                            cdst, N, K, d, cacc);
     }
@@ -1357,11 +1349,7 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     const bool fused_route = K <= 8 && gw >= d / 4 && rlds <= 32 * 1024 && (size_t)ne * d <= 16384;
     // small expert sets: every expert's gate/up is computed (at most a few MB of weights) so the
     // routing runs beside the GEMVs instead of in front of them
-    static const int allexp_on = [] {
-        const char* e = getenv("GH_MOE_ALLEXP");
-        return e ? atoi(e) : 1;
-    }();
-    const bool allexp = allexp_on && fused_route && has_sh && ne > K && (size_t)ne * E * d <= ((size_t)4 << 20);
+    const bool allexp = fused_route && has_sh && ne > K && (size_t)ne * E * d <= ((size_t)4 << 20);
     if (!fused_route) {
         const int rc = launch_route(xres, rw, bias, nullptr, idx, w, N, d, ne, K, nw, eps, xn);
         if (rc) return rc;
@@ -1437,6 +1425,51 @@ int moe_route(const float* x, const float* rw, const float* bias, float* probs, 
 
 using namespace gh;
 
+namespace gh {
+
+// moe_forward_bias_half with an optional residual target: when acc_dst is given and the path
+// ends in the ordered combine, the combined output is added into acc_dst (one addition, as the
+// caller's add_inplace would do) and *added is set; otherwise `out` holds it.
+int moe_forward_acc(const float* x, const float* router_w, const float* router_bias, const void* gates,
+                    const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d,
+                    float* out, float* acc_dst, int* added, float* probs_cache, int32_t* idx_cache, float* w_cache,
+                    int64_t N, int d, int E, int ne, int K, int SH, int qkind) {
+    if (added) *added = 0;
+    if (N <= 0) return GH_OK;
+    // core/moe_cpu.cpp:207-209
+    GH_REQUIRE(K >= 1 && K <= 8, "moe_forward: K must be in [1,8]");
+    GH_REQUIRE(ne > 0 && ne <= 64, "moe_forward: ne out of range");
+    GH_REQUIRE(d > 0 && E > 0, "moe_forward: bad dims");
+    GH_REQUIRE(x && router_w && gates && ups && downs && out, "moe_forward: null pointer");
+    GH_REQUIRE(qkind >= -1 && qkind <= 3, "moe_forward: unknown qkind %d", qkind);
+    const int bv = qkind == 3 ? 256 : 64;
+    const bool has_sh = sh_g && sh_u && sh_d;
+    GH_REQUIRE(d % bv == 0 && E % bv == 0 && (!has_sh || SH % bv == 0),
+               "moe_forward: d=%d, E=%d, SH=%d must be multiples of %d", d, E, SH, bv);
+    GH_REQUIRE(N <= 8192, "moe_forward: at most 8192 tokens per call");
+    const int S = (int)N * K;
+    int32_t* idx = idx_cache;
+    float* w = w_cache;
+    if (!idx || !w) {
+        char* r = (char*)workspace(WS_MOE_ROUTE, (size_t)S * 8);
+        if (!r) return fail(GH_ENOMEM, "moe: workspace");
+        if (!idx) idx = (int32_t*)r;
+        if (!w) w = (float*)(r + (size_t)S * 4);
+    }
+    int rc = moe_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
+    if (rc) return rc;
+    const int n = (int)N;
+    switch (qkind) {
+        case -1: return moe_kind<4>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH);
+        case 0: return moe_kind<0>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH);
+        case 1: return moe_kind<1>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH);
+        case 2: return moe_kind<2>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH);
+        default: return moe_kind<3>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH);
+    }
+}
+
+}  // namespace gh
+
 extern "C" {
 
 int gh_moe_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w, int64_t N,
@@ -1462,36 +1495,8 @@ int gh_moe_forward_bias_half(const float* x, const float* router_w, const float*
     (void)s_gate;
     (void)s_up;
     (void)s_act;
-    if (N <= 0) return GH_OK;
-    // core/moe_cpu.cpp:207-209
-    GH_REQUIRE(K >= 1 && K <= 8, "moe_forward: K must be in [1,8]");
-    GH_REQUIRE(ne > 0 && ne <= 64, "moe_forward: ne out of range");
-    GH_REQUIRE(d > 0 && E > 0, "moe_forward: bad dims");
-    GH_REQUIRE(x && router_w && gates && ups && downs && out, "moe_forward: null pointer");
-    GH_REQUIRE(qkind >= -1 && qkind <= 3, "moe_forward: unknown qkind %d", qkind);
-    const int bv = qkind == 3 ? 256 : 64;
-    const bool has_sh = sh_g && sh_u && sh_d;
-    GH_REQUIRE(d % bv == 0 && E % bv == 0 && (!has_sh || SH % bv == 0),
-               "moe_forward: d=%d, E=%d, SH=%d must be multiples of %d", d, E, SH, bv);
-    GH_REQUIRE(N <= 8192, "moe_forward: at most 8192 tokens per call");
-    const int S = (int)N * K;
-    int32_t* idx = idx_cache;
-    float* w = w_cache;
-    if (!idx || !w) {
-        char* r = (char*)workspace(WS_MOE_ROUTE, (size_t)S * 8);
-        if (!r) return fail(GH_ENOMEM, "moe: workspace");
-        if (!idx) idx = (int32_t*)r;
-        if (!w) w = (float*)(r + (size_t)S * 4);
-    }
-    int rc = moe_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
-    if (rc) return rc;
-    switch (qkind) {
-        case -1: return moe_kind<4>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
-        case 0: return moe_kind<0>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
-        case 1: return moe_kind<1>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
-        case 2: return moe_kind<2>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
-        default: return moe_kind<3>(x, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, (int)N, d, E, ne, K, SH);
-    }
+    return moe_forward_acc(x, router_w, router_bias, gates, ups, downs, sh_g, sh_u, sh_d, out, nullptr, nullptr,
+                           probs_cache, idx_cache, w_cache, N, d, E, ne, K, SH, qkind);
 }
 
 }  // extern "C"

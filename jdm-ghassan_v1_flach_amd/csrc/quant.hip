@@ -197,20 +197,9 @@ __global__ void __launch_bounds__(256) k_gemv(const float* __restrict__ x, const
     }
 }
 
-// tuning knobs (environment, read once): waves per CU of the persistent grid
-// and rows per lane of the single-token GEMV
-static int env_int(const char* n, int dflt) {
-    const char* v = getenv(n);
-    return v ? atoi(v) : dflt;
-}
-static int gemv_wpc() {
-    static const int v = env_int("GH_GEMV_WPC", 8);
-    return v;
-}
-static int gemv_r() {
-    static const int v = env_int("GH_GEMV_R", 2);
-    return v;
-}
+// waves per CU of the persistent grid and rows per lane of the single-token GEMV
+static int gemv_wpc() { return 8; }
+static int gemv_r() { return 2; }
 
 template <int KIND, int MT, int R>
 static int launch_gemv_t(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb) {

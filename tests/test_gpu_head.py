@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import relerr
+from conftest import close
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +46,7 @@ def test_head_greedy_parity(gh, d, V):
     tab = O.f32_to_f16(O.rng_normal(62, V * d, 0, 0.02))
     lg, tok = _head(gh, x, nw, tab, d, V)
     ref = _oracle_logits(x, nw, tab, d, V)
-    assert relerr(lg, ref) <= TOL
+    assert close(lg, ref, TOL)
     assert tok == _argmax(lg)
     top2 = np.sort(ref)[-2:]
     if top2[1] - top2[0] > 1e-3:

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import relerr
+from conftest import close
 
 pytestmark = pytest.mark.gpu
 
@@ -47,7 +47,7 @@ def test_gemv_parity(gh, kind, M, K, N):
     dx, dw = gh.Buf.from_array(x), gh.Buf.from_array(w)
     gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
     ref = O.linear_q(x, w, M, K, N, kind)
-    assert relerr(y.numpy().reshape(M, N), ref) <= GEMV_TOL
+    assert close(y.numpy().reshape(M, N), ref, GEMV_TOL)
 
 
 @pytest.mark.parametrize("kind", [2, 3])
@@ -60,7 +60,7 @@ def test_gemv_c2_full(gh, kind, M, K, N):
     dx, dw = gh.Buf.from_array(x), gh.Buf.from_array(w)
     gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
     ref = O.linear_q(x, w, M, K, N, kind)
-    assert relerr(y.numpy().reshape(M, N), ref) <= GEMV_TOL
+    assert close(y.numpy().reshape(M, N), ref, GEMV_TOL)
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2, 3])
@@ -72,7 +72,7 @@ def test_gemm_parity(gh, kind, M, K, N):
     dx, dw = gh.Buf.from_array(x), gh.Buf.from_array(w)
     gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
     ref = O.linear_q(x, w, M, K, N, kind)
-    assert relerr(y.numpy().reshape(M, N), ref) <= GEMM_TOL
+    assert close(y.numpy().reshape(M, N), ref, GEMM_TOL)
 
 
 @pytest.mark.parametrize("kind", [2, 3])
@@ -91,9 +91,9 @@ def test_gemm_c2_full_rows_match_gemv(gh, kind):
     ys = gh.Buf.zeros(8 * N, np.float32)
     dxs = gh.Buf.from_array(xs)
     gh.call("gh_linear_forward_q4", dxs.p, dw.p, ys.p, 8, K, N, kind)
-    assert relerr(Y[rows], ys.numpy().reshape(8, N)) <= GEMM_TOL
+    assert close(Y[rows], ys.numpy().reshape(8, N), GEMM_TOL)
     ref = O.linear_q(np.ascontiguousarray(xs[:2]), w, 2, K, N, kind)
-    assert relerr(Y[rows[:2]], ref) <= GEMM_TOL
+    assert close(Y[rows[:2]], ref, GEMM_TOL)
 
 
 def test_fp16_and_f32_linear(gh):
@@ -106,10 +106,10 @@ def test_fp16_and_f32_linear(gh):
     gh.call("gh_linear_forward_fp16", dx.p, dwh.p, y.p, M, K, N)
     ref = np.empty(M * N, np.float32)
     O.oracle().orc_linear_forward_fp16(O.P(x), O.P(wh), O.P(ref), M, K, N)
-    assert relerr(y.numpy(), ref) <= GEMV_TOL
+    assert close(y.numpy(), ref, GEMV_TOL)
     gh.call("gh_linear_forward_f32", dx.p, dwf.p, y.p, M, K, N)
     O.oracle().orc_linear_forward_f32(O.P(x), O.P(wf), O.P(ref), M, K, N)
-    assert relerr(y.numpy(), ref) <= GEMV_TOL
+    assert close(y.numpy(), ref, GEMV_TOL)
     Mg = 64
     xg = O.rng_normal(13, Mg * K)
     yg = gh.Buf.zeros(Mg * N, np.float32)
@@ -117,7 +117,7 @@ def test_fp16_and_f32_linear(gh):
     gh.call("gh_linear_forward_fp16", dxg.p, dwh.p, yg.p, Mg, K, N)
     refg = np.empty(Mg * N, np.float32)
     O.oracle().orc_linear_forward_fp16(O.P(xg), O.P(wh), O.P(refg), Mg, K, N)
-    assert relerr(yg.numpy(), refg) <= GEMM_TOL
+    assert close(yg.numpy(), refg, GEMM_TOL)
 
 
 @pytest.mark.parametrize("kind", [2, 3])
@@ -134,7 +134,7 @@ def test_small_m_gemv_every_m(gh, kind, K, N):
         y = gh.Buf.zeros(M * N, np.float32)
         gh.call("gh_linear_forward_q4", dx.p, dw.p, y.p, M, K, N, kind)
         ref = O.linear_q(x, w, M, K, N, kind)
-        assert relerr(y.numpy().reshape(M, N), ref) <= GEMV_TOL, f"M={M}"
+        assert close(y.numpy().reshape(M, N), ref, GEMV_TOL), f"M={M}"
 
 
 @pytest.mark.parametrize("kind", [2, 3])
@@ -154,4 +154,4 @@ def test_small_m_gemv_activation_range(gh, kind):
     ref = O.linear_q(x, w, M, K, N, kind).reshape(M, N)
     got = y.numpy().reshape(M, N)
     for t in range(M):
-        assert relerr(got[t], ref[t]) <= GEMV_TOL, f"token {t}"
+        assert close(got[t], ref[t], GEMV_TOL), f"token {t}"
