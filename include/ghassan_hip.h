@@ -152,6 +152,15 @@ int gh_attention_forward_ex(const float* q, const float* k, const float* v, floa
 int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
                                   int H, int KV, int hd, int ring_start, int pinned_prefix, int cur_len,
                                   int cache_max, float scale, float* scratch, int window);
+/* No counterpart in the reference. attention_decode_ring_fp16 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops): the same kernels
+ * and result, with the split-K partials in a static 4 MiB device array per GPU instead of the
+ * backend's grow-only workspace; it calls no hipMalloc / hipFree. Returns GH_EINVAL when the
+ * partials (H * splits * (hd + 2) floats, splits ~ cur_len / chunk) would exceed 4 MiB.
+ * Calls that overlap on one GPU (several streams or host threads) race on that array. */
+int gh_attention_decode_ring_fp16_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                                          float* out, int H, int KV, int hd, int ring_start, int pinned_prefix,
+                                          int cur_len, int cache_max, float scale, int window);
 /* Extension (no reference counterpart): ragged batched
  * decode over a paged bf16 KV cache. q [S, H, hd]; pages [n_pages, page_size,
  * KV, hd] bf16; page_table [S, max_pages] (device int32); seq_lens [S]

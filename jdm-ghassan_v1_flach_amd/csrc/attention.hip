@@ -582,13 +582,30 @@ static void launch_dec2(const DecodeArgs& a, dim3 grid) {
 // otherwise k_attn_combine merges them into out. (A merge by the last block
 // of each kv head was slower: the device-scope fence every block then needs
 // writes back L2.)
-template <bool PAGED>
-static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out) {
+// Floats of split-K partials (o, then (max, sum) pairs at a 64-float boundary) one decode
+// launch needs; sets a.chunk / a.splits.
+static size_t decode_partial_floats(DecodeArgs& a, int hd, int S, int span, size_t* ml_off) {
     const bool v2 = (hd == 64 || hd == 128) && a.G <= 8;
     a.chunk = pick_chunk(span, a.KV * S, v2 ? DEC2_CHUNK_MAX : DEC_CHUNK_MAX);
     a.splits = cdiv(span > 0 ? span : 1, a.chunk);
-    float* o = (float*)workspace(WS_ATTN_O, (size_t)S * a.KV * a.splits * a.G * hd * 4);
-    float* ml = (float*)workspace(WS_ATTN_ML, (size_t)S * a.KV * a.splits * a.G * 2 * 4);
+    const size_t no = (size_t)S * a.KV * a.splits * a.G * hd;
+    *ml_off = (no + 63) / 64 * 64;
+    return *ml_off + (size_t)S * a.KV * a.splits * a.G * 2;
+}
+
+// ws: caller-provided partials buffer of decode_partial_floats() floats, or null for the
+// backend's grow-only workspace.
+template <bool PAGED>
+static int launch_decode(DecodeArgs& a, int hd, int S, int span, float* out, float* ws = nullptr) {
+    const bool v2 = (hd == 64 || hd == 128) && a.G <= 8;
+    size_t ml_off = 0;
+    const size_t nf = decode_partial_floats(a, hd, S, span, &ml_off);
+    float* o = ws;
+    float* ml = ws ? ws + ml_off : nullptr;
+    if (!ws) {
+        o = (float*)workspace(WS_ATTN_O, ml_off * 4);
+        ml = (float*)workspace(WS_ATTN_ML, (nf - ml_off) * 4);
+    }
     if (!o || !ml) return fail(GH_ENOMEM, "attention decode: workspace");
     a.o_part = o;
     a.ml_part = ml;
@@ -1111,10 +1128,9 @@ int gh_attention_forward_ex(const float* q, const float* k, const float* v, floa
     return attention_prefill(q, k, v, out, B, T, H, KV, hd, scale, window);
 }
 
-int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV,
-                                  int hd, int ring_start, int pinned, int cur_len, int cache_max, float scale,
-                                  float* scratch, int window) {
-    (void)scratch;
+static int ring_decode_args(DecodeArgs& a, const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H,
+                            int KV, int hd, int ring_start, int pinned, int cur_len, int cache_max, float scale,
+                            int window) {
     // core/attn_cpu.cpp:211-222
     GH_REQUIRE(H > 0 && KV > 0 && hd > 0, "attention_decode_ring_fp16: empty shape");
     GH_REQUIRE(H % KV == 0, "attention_decode_ring_fp16: H must be a multiple of KV");
@@ -1128,11 +1144,64 @@ int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kc, const uint
     }
     GH_REQUIRE(H / KV <= DEC_GMAX, "attention_decode_ring_fp16: group size %d > %d", H / KV, DEC_GMAX);
     GH_REQUIRE(q && kc && vc && out, "attention_decode_ring_fp16: null pointer");
-    DecodeArgs a{};
+    a = DecodeArgs{};
     a.q = q; a.k = kc; a.v = vc; a.H = H; a.KV = KV; a.G = H / KV; a.scale = scale;
     a.ring_start = ring_start; a.pinned = pinned; a.cur_len = cur_len; a.cache_max = cache_max;
     a.j0 = (window > 0 && cur_len > window) ? cur_len - window : 0;
+    return GH_OK;
+}
+
+int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H, int KV,
+                                  int hd, int ring_start, int pinned, int cur_len, int cache_max, float scale,
+                                  float* scratch, int window) {
+    (void)scratch;
+    DecodeArgs a;
+    const int rc = ring_decode_args(a, q, kc, vc, out, H, KV, hd, ring_start, pinned, cur_len, cache_max, scale, window);
+    if (rc) return rc;
     return launch_decode<false>(a, hd, 1, cur_len - a.j0, out);
+}
+
+// The allocation-free variant: the split-K partials live in `scratch`, a file-scope device
+// array each GPU holds once for the life of the process. Its device address is looked up per
+// device with hipGetSymbolAddress (the array's name is only a host-side stand-in) on the first
+// call on that device. Every call on a GPU uses the same array: calls that overlap on one GPU
+// (several streams, several host threads) race on it. Nothing in it needs to start at zero:
+// every launch writes all the partials the merge reads.
+constexpr size_t NOALLOC_DEC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) float scratch[NOALLOC_DEC_SCRATCH_BYTES / 4];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static float* g_scratch_dev[NOALLOC_MAX_DEVICES];
+
+static int noalloc_scratch(float** out) {
+    int dev = 0;
+    GH_HIP(hipGetDevice(&dev));
+    GH_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, "attention decode (no-alloc): device %d out of range", dev);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(GH_EHIP, "attention decode (no-alloc): hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_dev[dev] = (float*)p;
+    }
+    *out = g_scratch_dev[dev];
+    return GH_OK;
+}
+
+int gh_attention_decode_ring_fp16_noalloc(const float* q, const uint16_t* kc, const uint16_t* vc, float* out, int H,
+                                          int KV, int hd, int ring_start, int pinned, int cur_len, int cache_max,
+                                          float scale, int window) {
+    DecodeArgs a;
+    int rc = ring_decode_args(a, q, kc, vc, out, H, KV, hd, ring_start, pinned, cur_len, cache_max, scale, window);
+    if (rc) return rc;
+    size_t ml_off = 0;
+    const size_t need = decode_partial_floats(a, hd, 1, cur_len - a.j0, &ml_off) * 4;
+    GH_REQUIRE(need <= NOALLOC_DEC_SCRATCH_BYTES,
+               "attention_decode_ring_fp16_noalloc: %zu bytes of partials (H=%d hd=%d, %d splits) exceed the %zu-byte "
+               "static scratch", need, H, hd, a.splits, NOALLOC_DEC_SCRATCH_BYTES);
+    float* ws = nullptr;
+    rc = noalloc_scratch(&ws);
+    if (rc) return rc;
+    return launch_decode<false>(a, hd, 1, cur_len - a.j0, out, ws);
 }
 
 int gh_attention_decode_paged_bf16(const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* page_table,
