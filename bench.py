@@ -13,14 +13,17 @@ tok/s is reported beside it.
 
 `roofline` is the path's dominant HBM kernel at production shape, the
 single-token Q4_K GEMV of BASELINE config 2 (14336x4096), timed alone over
-repeated launches with HIP events on the backend stream; `traffic` comes from
+repeated launches with HIP events on the backend stream, cold (10 copies of
+the weights in rotation, 331 MB, more than the 256 MB MALL: every launch reads
+HBM; the headline) and warm (the same copy every launch); `traffic` comes from
 the committed rocprofv3 PMC summary of `--probe` (FETCH_SIZE + WRITE_SIZE per
 launch, scaled by what the counters read for a plain copy of known size); `kernels` gives the per-kernel figures for BASELINE configs 2-5 at
 full size. `cpu_baseline` times the CPU oracle (a restatement of the
-reference's CPU path) on a bounded sample of the same workload.
+reference's CPU path) on the same workload on the host's cores.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--eager-decode]
-python bench.py --probe     # 20 launches of the roofline GEMV + 20 plain 64 MiB copies, for PMC runs
+python bench.py --probe     # 20 cold launches of the roofline GEMV + 20 plain 64 MiB copies, for PMC runs
+python bench.py --probe-mfma  # 5 launches of each MFMA-bound kernel (c3 scan, c2 GEMM, c4 prefill), for PMC runs
 """
 import argparse
 import ctypes as C
@@ -122,6 +125,16 @@ def moe_decode_case(gh, d, E, ne, K, SH, kind, N=1, seed=5, skew=False):
     return run, bufs, out
 
 
+def to_f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def to_bf16(x):
+    """fp32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 def kernel_suite(gh):
     res = {}
     # ---------------- c2: quantized GEMV / GEMM, W 14336x4096
@@ -176,16 +189,32 @@ def kernel_suite(gh):
     del b_in, b_out, bv, conv, ssm
     # ---------------- c4: decode attention, L = 1k / 8k / 32k, ragged batch 16, prefill 4096
     Hq, KVh, hd = 32, 8, 128
+    kv_all = gh.rng_normal(4, 2 * 32768 * KVh * hd)  # K then V, N(0,1) (seed 4)
+    k16, v16 = to_f16(kv_all[:32768 * KVh * hd]), to_f16(kv_all[32768 * KVh * hd:])
+    kb16, vb16 = to_bf16(kv_all[:32768 * KVh * hd]), to_bf16(kv_all[32768 * KVh * hd:])
+    q = gh.Buf.from_array(gh.rng_normal(40, Hq * hd))
+    o = gh.Buf.zeros(Hq * hd, np.float32)
+    sc = 1.0 / np.sqrt(hd)
     for L in (1024, 8192, 32768):
-        q = gh.Buf.from_array(gh.rng_normal(4, Hq * hd))
-        kc = gh.Buf(L * KVh * hd * 2)
-        vc = gh.Buf(L * KVh * hd * 2)
-        o = gh.Buf.zeros(Hq * hd, np.float32)
+        n = L * KVh * hd
+        # bf16 cache as configured: the paged entry point with one sequence
+        kp, vp = gh.Buf.from_array(kb16[:n]), gh.Buf.from_array(vb16[:n])
+        npg = L // 64
+        pt = gh.Buf.from_array(np.arange(npg, dtype=np.int32))
+        ln = gh.Buf.from_array(np.array([L], np.int32))
+        ms = time_launches(gh, lambda: gh.call("gh_attention_decode_paged_bf16", q.p, kp.p, vp.p, pt.p, ln.p, 1, npg, 64,
+                                               L, o.p, Hq, KVh, hd, gh.fl(sc)), 100)
+        res[f"c4_decode_bf16_L{L}"] = entry("k_attn_decode2<paged bf16>+k_attn_combine", ms,
+                                            bytes_=n * 2 * 2 + 2 * Hq * hd * 4, flops=4.0 * Hq * hd * L)
+        del kp, vp
+        # the reference's fp16 ring cache (attention_decode_ring_fp16)
+        kc, vc = gh.Buf.from_array(k16[:n]), gh.Buf.from_array(v16[:n])
         ms = time_launches(gh, lambda: gh.call("gh_attention_decode_ring_fp16", q.p, kc.p, vc.p, o.p, Hq, KVh, hd, 0,
-                                               8, L, L, gh.fl(0.0884), None, 0), 100)
-        res[f"c4_decode_L{L}"] = entry("k_attn_decode2+k_attn_combine", ms, bytes_=L * KVh * hd * 2 * 2 + 2 * Hq * hd * 4,
-                                       flops=4.0 * Hq * hd * L)
+                                               8, L, L, gh.fl(sc), None, 0), 100)
+        res[f"c4_decode_L{L}"] = entry("k_attn_decode2+k_attn_combine (fp16 ring)", ms,
+                                       bytes_=n * 2 * 2 + 2 * Hq * hd * 4, flops=4.0 * Hq * hd * L)
         del kc, vc
+    del k16, v16, kb16, vb16, kv_all
     ps = 64
     lens = (512 + gh.rng_below(4, 16, 8192 - 512 + 1)).astype(np.int32)
     max_pages = (int(lens.max()) + ps - 1) // ps
@@ -195,8 +224,10 @@ def kernel_suite(gh):
         for i in range((int(lens[s]) + ps - 1) // ps):
             pt[s, i] = nxt
             nxt += 1
-    kp = gh.Buf(nxt * ps * KVh * hd * 2)
-    vp = gh.Buf(nxt * ps * KVh * hd * 2)
+    kvr = gh.rng_normal(41, 2 * nxt * ps * KVh * hd)  # N(0,1) bf16 pages
+    kp = gh.Buf.from_array(to_bf16(kvr[:nxt * ps * KVh * hd]))
+    vp = gh.Buf.from_array(to_bf16(kvr[nxt * ps * KVh * hd:]))
+    del kvr
     qb = gh.Buf.from_array(gh.rng_normal(5, 16 * Hq * hd))
     dpt, dl = gh.Buf.from_array(pt), gh.Buf.from_array(lens)
     ob = gh.Buf.zeros(16 * Hq * hd, np.float32)
@@ -282,9 +313,10 @@ def gguf_load_case(gh):
         os.unlink(path)
 
 
-def cpu_baseline(prompt, n_prefill=16, n_new=6):
-    """The CPU oracle (restated reference CPU path) on a bounded sample of the
-    same workload: c1 Q4_K, a 16-token prompt prefix and 6 greedy tokens."""
+def cpu_baseline(prompt, n_prefill=PROMPT, n_new=N_NEW):
+    """The CPU oracle (restated reference CPU path) on the same workload: c1
+    Q4_K, the 128-token prompt and 64 greedy tokens (about a minute of CPU
+    time on 16 host threads)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     w = O.granite_weights(O.C1, 3)
@@ -305,17 +337,26 @@ def cpu_baseline(prompt, n_prefill=16, n_new=6):
                       f"prefill {secs[0]:.2f} s, decode {secs[1]:.2f} s"}
 
 
-def roofline_gemv(gh):
-    """The c2 headline GEMV (Q4_K, 14336x4096, M=1): buffers and a launcher."""
+COLD_COPIES = 10  # 10 x 33 MB of weights > the 256 MB Infinity Cache (MALL)
+
+
+def roofline_gemv(gh, copies=1):
+    """The c2 headline GEMV (Q4_K, 14336x4096, M=1): buffers and a launcher.
+    copies > 1: that many distinct copies of the weights (and of x, y), used in
+    rotation, so that every launch reads its weights from HBM rather than from
+    the MALL a previous launch left them in (cold-cache measurement)."""
     K2, N2 = 4096, 14336
     w2 = gh.quantize(3, gh.rng_normal(2, N2 * K2, 0, 0.02))
     x2 = gh.rng_normal(3, K2)
-    bufs = (gh.Buf.from_array(w2), gh.Buf.from_array(x2), gh.Buf.zeros(N2, np.float32))
+    sets = [(gh.Buf.from_array(w2), gh.Buf.from_array(x2), gh.Buf.zeros(N2, np.float32)) for _ in range(copies)]
     nbytes = w2.nbytes + x2.nbytes + N2 * 4
+    it = [0]
 
     def run():
-        gh.call("gh_linear_forward_q4", bufs[1].p, bufs[0].p, bufs[2].p, 1, K2, N2, 3)
-    return run, bufs, nbytes
+        w, x, y = sets[it[0]]
+        it[0] = (it[0] + 1) % copies
+        gh.call("gh_linear_forward_q4", x.p, w.p, y.p, 1, K2, N2, 3)
+    return run, sets, nbytes
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_c2_traffic.txt")
@@ -323,7 +364,7 @@ COPY_FLOATS = 16 << 20  # 64 MiB per side
 
 
 def probe(gh):
-    run, bufs, nbytes = roofline_gemv(gh)
+    run, bufs, nbytes = roofline_gemv(gh, COLD_COPIES)
     for _ in range(20):
         run()
     src = gh.Buf.from_array(np.ones(COPY_FLOATS, np.float32))
@@ -331,7 +372,40 @@ def probe(gh):
     for _ in range(20):
         gh.call("gh_copy", dst.p, src.p, gh.i64(COPY_FLOATS))
     gh.sync()
-    log(f"probe: 20 x roofline GEMV ({nbytes} algorithmic bytes), 20 x k_copy ({COPY_FLOATS * 4} B read + written)")
+    log(f"probe: 20 x roofline GEMV, cold ({COLD_COPIES} weight copies in rotation; {nbytes} algorithmic bytes), "
+        f"20 x k_copy ({COPY_FLOATS * 4} B read + written)")
+
+
+def probe_mfma(gh):
+    """5 launches each of the c3 SSD scan (T=4096), the c2 Q4_K prefill GEMM
+    (M=2048) and the c4 causal prefill attention (T=4096), full size."""
+    T, H, P, N = 4096, 48, 64, 128
+    arrs = [gh.rng_normal(31, T * H * P), gh.rng_normal(32, T * N) / np.float32(np.sqrt(N)),
+            gh.rng_normal(33, T * N) / np.float32(np.sqrt(N)),
+            np.log1p(np.exp(gh.rng_normal(34, T * H, -2.0, 0.5).astype(np.float64))).astype(np.float32),
+            -np.exp(gh.rng_uniform(35, H, 0.0, np.log(16.0))).astype(np.float32), np.ones(H, np.float32)]
+    bufs = [gh.Buf.from_array(a) for a in arrs]
+    st, yb = gh.Buf.zeros(H * P * N, np.float32), gh.Buf.zeros(T * H * P, np.float32)
+    for _ in range(5):
+        gh.call("gh_ssd_scan", *[b.p for b in bufs], st.p, yb.p, T, H, P, N, 256)
+    gh.sync()
+    del bufs, st, yb
+    M, K, Nn = 2048, 4096, 14336
+    dw = gh.Buf.from_array(gh.quantize(3, gh.rng_normal(2, Nn * K, 0, 0.02)))
+    dx, dy = gh.Buf.from_array(gh.rng_normal(3, M * K)), gh.Buf.zeros(M * Nn, np.float32)
+    for _ in range(5):
+        gh.call("gh_linear_forward_q4", dx.p, dw.p, dy.p, M, K, Nn, 3)
+    gh.sync()
+    del dw, dx, dy
+    Tp, Hq, KVh, hd = 4096, 32, 8, 128
+    qf = gh.Buf.from_array(gh.rng_normal(6, Tp * Hq * hd))
+    kf = gh.Buf.from_array(gh.rng_normal(7, Tp * KVh * hd))
+    vf = gh.Buf.from_array(gh.rng_normal(8, Tp * KVh * hd))
+    of = gh.Buf.zeros(Tp * Hq * hd, np.float32)
+    for _ in range(5):
+        gh.call("gh_attention_forward_ex", qf.p, kf.p, vf.p, of.p, None, 1, Tp, Hq, KVh, hd, gh.fl(0.0884), 0, None)
+    gh.sync()
+    log("probe-mfma: 5 x SSD scan c3, 5 x GEMM c2 Q4_K M=2048, 5 x prefill attention c4 T=4096")
 
 
 def read_traffic():
@@ -356,6 +430,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager-decode", action="store_true",
                     help="launch the decode step's kernels one by one instead of replaying the captured graph")
+    ap.add_argument("--probe-mfma", action="store_true",
+                    help="only run the MFMA-bound kernels (c3 SSD scan, c2 prefill GEMM, c4 prefill attention), "
+                         "5 launches each, for rocprofv3 --pmc runs")
     ap.add_argument("--probe", action="store_true",
                     help="only run the roofline GEMV and a plain copy of known size (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -367,6 +444,9 @@ def main():
     gh.load()
     if args.probe:
         probe(gh)
+        return
+    if args.probe_mfma:
+        probe_mfma(gh)
         return
     Model.use_graph = 0 if args.eager_decode else 1
     prompt = gh.rng_below(1, PROMPT, C1["V"])
@@ -410,10 +490,16 @@ def main():
     dw, dx, dy = gh.Buf.from_array(w), gh.Buf.from_array(gh.rng_normal(3, C1["d"])), gh.Buf.zeros(proj, np.float32)
     inproj_ms = time_launches(gh, lambda: gh.call("gh_linear_forward_q4", dx.p, dw.p, dy.p, 1, C1["d"], proj, 3), 500)
 
-    # c2 headline GEMV (Q4_K, 14336x4096, M=1) is the roofline object
-    run2, bufs2, gemv_bytes = roofline_gemv(gh)
+    # c2 headline GEMV (Q4_K, 14336x4096, M=1) is the roofline object: cold (weights from HBM,
+    # the headline) and warm (the same weights every launch, partly served by the MALL)
+    run2, bufs2, gemv_bytes = roofline_gemv(gh, COLD_COPIES)
     gemv_ms = time_launches(gh, run2, 500)
     achieved = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    del bufs2
+    run_w, bufs_w, _ = roofline_gemv(gh, 1)
+    warm_ms = time_launches(gh, run_w, 500)
+    achieved_warm = gemv_bytes / (warm_ms * 1e-3) / 1e9
+    del bufs_w
 
     kernels = {}
     if not args.no_kernels:
@@ -454,7 +540,11 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "k_gemv_q4k_i8 (BASELINE c2: 14336x4096, M=1)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "avg_launch_us": round(gemv_ms * 1e3, 3), "algorithmic_bytes": int(gemv_bytes)},
+                     "avg_launch_us": round(gemv_ms * 1e3, 3), "algorithmic_bytes": int(gemv_bytes),
+                     "cache": f"cold: {COLD_COPIES} weight copies ({COLD_COPIES * gemv_bytes / 1e6:.0f} MB) in rotation",
+                     "frac_cold": round(achieved / HBM_PEAK_GBS, 4),
+                     "achieved_warm": round(achieved_warm, 1), "frac_warm": round(achieved_warm / HBM_PEAK_GBS, 4),
+                     "avg_launch_us_warm": round(warm_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "kernels": kernels,
         "greedy_ids_head": ids_q4k[:8].tolist(),

@@ -272,6 +272,7 @@ struct gh_granite {
     int host_len = 0;  // cache length mirror
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    hipStream_t cap_stream = nullptr;  // the stream the graph was captured on; lives as long as the graph
 
     const void* W(const std::string& n) const {
         auto it = by_name.find(n);
@@ -295,6 +296,10 @@ static void add_param(gh_granite* g, const std::string& name, int64_t numel, int
 static void free_all(gh_granite* g) {
     if (g->graph_exec) (void)hipGraphExecDestroy(g->graph_exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
+    if (g->cap_stream) {
+        (void)hipStreamSynchronize(g->cap_stream);
+        (void)hipStreamDestroy(g->cap_stream);
+    }
     void* ptrs[] = {g->wbuf, g->state_buf, g->x, g->ids, g->ctl, g->gen_ids};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -784,29 +789,29 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
     }
     if (use_graph && done < n_new) {
         if (!g->graph_exec) {
+            // Capture needs a non-null stream. When the backend stream is the null stream, the
+            // capture runs on a stream the model owns and keeps until the graph is destroyed
+            // (gh_granite_destroy), so no captured node can outlive the stream it was recorded on.
             hipStream_t s = stream();
-            bool own = false;
-            if (s == nullptr) {  // capture needs a non-null stream
-                GH_HIP(hipStreamCreate(&s));
-                own = true;
-                GH_HIP(hipDeviceSynchronize());
+            const bool own = s == nullptr;
+            if (own) {
+                if (!g->cap_stream) GH_HIP(hipStreamCreate(&g->cap_stream));
+                s = g->cap_stream;
+                GH_HIP(hipStreamSynchronize(nullptr));  // prior null-stream work before the capture
                 gh_set_stream((void*)s);
             }
             GH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
             int rc = decode_step(g, true);
             hipGraph_t graph = nullptr;
             hipError_t e = hipStreamEndCapture(s, &graph);
-            if (own) {
-                gh_set_stream(nullptr);
+            if (own) gh_set_stream(nullptr);
+            if (rc) {
+                if (graph) (void)hipGraphDestroy(graph);
+                return rc;
             }
-            if (rc) return rc;
             if (e != hipSuccess) return fail(GH_EHIP, "decode graph capture: %s", hipGetErrorString(e));
             g->graph = graph;
             GH_HIP(hipGraphInstantiate(&g->graph_exec, graph, nullptr, nullptr, 0));
-            if (own) {
-                GH_HIP(hipStreamSynchronize(s));
-                GH_HIP(hipStreamDestroy(s));
-            }
         }
         for (; done < n_new; ++done) GH_HIP(hipGraphLaunch(g->graph_exec, stream()));
     } else {
