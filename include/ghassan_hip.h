@@ -259,8 +259,10 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
 /* One decode step (inference/generator.cpp:221-443) for `token`. */
 int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host);
 /* Greedy generation of n_new ids from the current logits
- * (inference/generator.cpp:985-1098, greedy branch). use_graph: capture the
- * decode step (embedding .. argmax) in a hipGraph and replay it. */
+ * (inference/generator.cpp:985-1098, greedy branch). use_graph: 0 launches the decode
+ * step's kernels one by one; 1 captures the step (embedding .. argmax) in a hipGraph
+ * and replays it; 2 runs the whole loop as one persistent cooperative launch (falls back
+ * to 1 when the model's shapes or the context do not fit that kernel). */
 int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int use_graph);
 
 #ifdef __cplusplus

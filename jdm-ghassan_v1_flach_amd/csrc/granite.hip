@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "gemv_fuse.h"
+#include "decode_persistent.h"
 
 namespace gh {
 
@@ -273,6 +274,10 @@ struct gh_granite {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     hipStream_t cap_stream = nullptr;  // the stream the graph was captured on; lives as long as the graph
+    // persistent decode loop: its model description (device copy) and hand-over buffers
+    PdModel* pd_dev = nullptr;
+    uint8_t* pd_buf = nullptr;
+    size_t pd_zero_bytes = 0;  // bytes of pd_buf zeroed before each launch (all of it)
 
     const void* W(const std::string& n) const {
         auto it = by_name.find(n);
@@ -300,6 +305,8 @@ static void free_all(gh_granite* g) {
         (void)hipStreamSynchronize(g->cap_stream);
         (void)hipStreamDestroy(g->cap_stream);
     }
+    if (g->pd_dev) (void)hipFree(g->pd_dev);
+    if (g->pd_buf) (void)hipFree(g->pd_buf);
     void* ptrs[] = {g->wbuf, g->state_buf, g->x, g->ids, g->ctl, g->gen_ids};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -771,6 +778,103 @@ int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host) {
     return GH_OK;
 }
 
+// The persistent decode loop's description of this model (host copy); buffers not set.
+static PdModel pd_describe(gh_granite* g) {
+    PdModel m;
+    memset(&m, 0, sizeof m);
+    m.L = g->L; m.d = g->d; m.V = g->V; m.H = g->H; m.KV = g->KV; m.hd = g->hd; m.E = g->E; m.ne = g->ne;
+    m.K = g->K; m.SH = g->SH; m.di = g->di; m.mh = g->mh; m.mdh = g->mdh; m.mds = g->mds; m.ck = g->ck;
+    m.kind = g->qkind; m.max_ctx = g->max_ctx; m.eps = g->eps; m.scale = g->scale;
+    m.emb = pd_g((const uint16_t*)g->W("tok_embeddings"));
+    m.final_norm = pd_g(g->F("final_norm"));
+    for (int l = 0; l < g->L && l < PD_MAX_LAYERS; ++l) {
+        const std::string pre = "layers." + std::to_string(l) + ".";
+        PdLayer& y = m.layers[l];
+        y.type = g->lt[l];
+        y.attn_norm = pd_g(g->F(pre + "attn_norm"));
+        y.ffn_norm = pd_g(g->F(pre + "ffn_norm"));
+        if (y.type == 0) {
+            const std::string mp = pre + "mamba.";
+            y.in_proj = pd_g((const uint8_t*)g->W(mp + "in_proj"));
+            y.conv_w = pd_g(g->F(mp + "conv1d.weight"));
+            y.conv_b = pd_g(g->F(mp + "conv1d.bias"));
+            y.dt_bias = pd_g(g->F(mp + "dt_bias"));
+            y.a_log = pd_g(g->F(mp + "A_log"));
+            y.Dp = pd_g(g->F(mp + "D"));
+            y.gnorm_w = pd_g(g->F(mp + "norm.weight"));
+            y.out_proj = pd_g((const uint8_t*)g->W(mp + "out_proj"));
+            y.conv_state = pd_g(g->conv[l]);
+            y.ssm_state = pd_g(g->ssm[l]);
+        } else {
+            y.wq = pd_g((const uint8_t*)g->W(pre + "wq"));
+            y.wk = pd_g((const uint8_t*)g->W(pre + "wk"));
+            y.wv = pd_g((const uint8_t*)g->W(pre + "wv"));
+            y.wo = pd_g((const uint8_t*)g->W(pre + "wo"));
+            y.kc = pd_g(g->kc[l]);
+            y.vc = pd_g(g->vc[l]);
+        }
+        y.router = pd_g(g->F(pre + "moe_router"));
+        y.gate = pd_g((const uint8_t*)g->W(pre + "moe_gate"));
+        y.up = pd_g((const uint8_t*)g->W(pre + "moe_up"));
+        y.down = pd_g((const uint8_t*)g->W(pre + "moe_down"));
+        y.sh_gate = pd_g((const uint8_t*)g->W(pre + "moe_sh_gate"));
+        y.sh_up = pd_g((const uint8_t*)g->W(pre + "moe_sh_up"));
+        y.sh_down = pd_g((const uint8_t*)g->W(pre + "moe_sh_down"));
+    }
+    return m;
+}
+
+// n_steps decode steps (each: the token in ctl[CTL_TOKEN] -> greedy id recorded at
+// gen_ids[step0 + i]) in one launch of the persistent loop. GH_EUNSUPPORTED (nothing
+// launched) if the model or context does not fit it.
+static int pd_generate(gh_granite* g, int step0, int n_steps) {
+    PdModel m = pd_describe(g);
+    const char* why = nullptr;
+    if (!pd_supported(m, g->host_len, n_steps, &why)) return GH_EUNSUPPORTED;
+    // hand-over buffers: tagged words, then keys, neg0 flags, counters
+    const int conv_dim = g->di + 2 * g->mds;
+    const size_t w_x = (size_t)g->d, w_proj = (size_t)g->di + conv_dim + g->mh, w_y = (size_t)g->di,
+                 w_q = (size_t)g->H * g->hd, w_kv = (size_t)2 * g->KV * g->hd,
+                 w_part = (size_t)g->H * PD_MAX_SPLITS * (g->hd + 2), w_act = (size_t)g->ne * g->E + g->SH,
+                 w_route = (size_t)2 * g->K;
+    // each vector in PD_REP replicas; the extra 64 words put consecutive replicas on
+    // different memory channels
+    auto stride = [](size_t words) { return (words + 31) / 32 * 32 + 64; };
+    const size_t sizes[8] = {w_x, w_proj, w_y, w_q, w_kv, w_part, w_act, w_route};
+    size_t tag_words = 0;
+    for (size_t w : sizes) tag_words += stride(w) * PD_REP;
+    const size_t bytes = tag_words * 8 + (size_t)g->max_ctx * 8 + (size_t)g->max_ctx * 4 + 256;
+    if (!g->pd_buf) {
+        GH_HIP(hipMalloc(&g->pd_buf, bytes));
+        GH_HIP(hipMalloc(&g->pd_dev, sizeof(PdModel)));
+        g->pd_zero_bytes = bytes;
+    }
+    uint64_t* t = (uint64_t*)g->pd_buf;
+    PdBuf* bufs[8] = {&m.tx, &m.tproj, &m.ty, &m.tq, &m.tkv, &m.tpart, &m.tact, &m.troute};
+    for (int i = 0; i < 8; ++i) {
+        bufs[i]->p = pd_g(t);
+        bufs[i]->stride = (int)stride(sizes[i]);
+        t += stride(sizes[i]) * PD_REP;
+    }
+    m.tag_words = tag_words;
+    m.keys = pd_g((unsigned long long*)t);
+    m.neg0 = pd_g((int32_t*)((unsigned long long*)t + g->max_ctx));
+    m.done = pd_g((uint32_t*)((int32_t*)((unsigned long long*)t + g->max_ctx) + g->max_ctx));
+    int32_t* abort_flag = (int32_t*)((uint32_t*)((int32_t*)((unsigned long long*)t + g->max_ctx) + g->max_ctx) + 1);
+    m.abort = pd_g(abort_flag);
+    m.ctl = pd_g(g->ctl);
+    m.gen_ids = pd_g(g->gen_ids);
+    m.logits = pd_g(g->logits);
+    GH_HIP(hipMemcpyAsync(g->pd_dev, &m, sizeof m, hipMemcpyHostToDevice, stream()));
+    GH_HIP(hipMemsetAsync(g->pd_buf, 0, g->pd_zero_bytes, stream()));
+    GHC(pd_launch(m, g->pd_dev, g->host_len, step0, n_steps));
+    int32_t aborted = 0;
+    GH_HIP(hipMemcpyAsync(&aborted, abort_flag, 4, hipMemcpyDeviceToHost, stream()));
+    GH_HIP(hipStreamSynchronize(stream()));
+    if (aborted) return fail(GH_EHIP, "persistent decode: a hand-over wait ran out (launch aborted)");
+    return GH_OK;
+}
+
 int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int use_graph) {
     GH_REQUIRE(g && ids_host && n_new >= 0, "granite_generate: bad arguments");
     GH_REQUIRE(g->host_len + n_new <= g->max_ctx, "granite_generate: %d + %d tokens exceed the context %d",
@@ -782,12 +886,23 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
     GHC(launch_argmax(g->logits, g->V, g->ctl + CTL_TOKEN));
     hipLaunchKernelGGL(k_record_token, dim3(1), dim3(1), 0, stream(), g->ctl, g->gen_ids, g->max_ctx);
     int done = 1;
+    if (use_graph == 2 && n_new > 1) {
+        // the whole loop in one persistent launch when the model fits it
+        const int rc = pd_generate(g, 1, n_new - 1);
+        if (rc == GH_OK) {
+            GH_HIP(hipMemcpyAsync(ids_host, g->gen_ids, (size_t)n_new * 4, hipMemcpyDeviceToHost, stream()));
+            GH_HIP(hipStreamSynchronize(stream()));
+            g->host_len += n_new - 1;
+            return GH_OK;
+        }
+        if (rc != GH_EUNSUPPORTED) return rc;
+    }
     if (n_new > 1) {
         // one plain step (also sizes every workspace before a capture)
         GHC(decode_step(g, true));
         ++done;
     }
-    if (use_graph && done < n_new) {
+    if (use_graph >= 1 && done < n_new) {
         if (!g->graph_exec) {
             // Capture needs a non-null stream. When the backend stream is the null stream, the
             // capture runs on a stream the model owns and keeps until the graph is destroyed

@@ -79,7 +79,7 @@ def test_weights_match_fixture(model):
     assert model.weights_sha() == str(g["weights_sha256"])
 
 
-@pytest.mark.parametrize("mamba_mode,use_graph", [(0, False), (1, False), (1, True)])
+@pytest.mark.parametrize("mamba_mode,use_graph", [(0, 0), (1, 0), (1, 1), (1, 2)])
 def test_greedy_ids_match_reference(model, mamba_mode, use_graph):
     g = golden("granite_c1_q8")
     ids, _ = model.generate(g["prompt"], int(g["n_new"]), mamba_mode, use_graph)
@@ -94,6 +94,16 @@ def test_graph_replay_equals_eager(model):
     c, lc = model.generate(g["prompt"], 24, 1, True)  # replays the already captured graph
     assert np.array_equal(a, b) and np.array_equal(a, c)
     assert np.array_equal(la, lb)
+
+
+def test_persistent_decode_equals_graph(model):
+    """use_graph=2: the whole decode loop in one cooperative launch gives the ids
+    of graph replay, twice in a row (the hand-over buffers are re-zeroed per call)."""
+    g = golden("granite_c1_q8")
+    a, _ = model.generate(g["prompt"], 40, 1, 1)
+    b, _ = model.generate(g["prompt"], 40, 1, 2)
+    c, _ = model.generate(g["prompt"], 40, 1, 2)
+    assert np.array_equal(a, b) and np.array_equal(a, c)
 
 
 def test_q4k_model_runs_and_matches_oracle(gh):
@@ -118,10 +128,10 @@ def expected_matches(margins):
     return int(small[0]) + 1 if small.size else len(margins)
 
 
-@pytest.mark.parametrize("use_graph", [False, True])
+@pytest.mark.parametrize("use_graph", [0, 1, 2])
 def test_q4k_benched_workload_vs_oracle(gh, use_graph):
     """The bench's headline workload: c1 in Q4_K, 128-token prompt (seed 1) and
-    64 greedy tokens, SSD prefill, decode eager and graph-replayed. Ids against
+    64 greedy tokens, SSD prefill, decode eager, graph-replayed and persistent. Ids against
     the oracle generator's run of the same workload
     (tests/golden/granite_c1_q4k_oracle.npz) up to its first near-tie."""
     import cases
