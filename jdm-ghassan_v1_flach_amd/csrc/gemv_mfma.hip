@@ -688,8 +688,10 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
 // receives D[4g + e][n] = part-e dot of its own 16 codes for e = 0, 1, 2 at
 // once. A and the per-sub-block scales are the same for every tile a wave
 // processes, so they live in registers.
-// Streaming: one persistent block per CU slot walks tiles b, b+G, ... (16
-// rows each); wave w owns super-blocks SBW*w .. SBW*w+SBW-1 of every tile and
+// Streaming: one block per CU slot takes a contiguous range of rows, equal for
+// every block up to 8 rows, in tiles of 16 rows (the last one may be short; its
+// missing rows are not fetched and not stored), so every CU streams the same bytes;
+// wave w owns super-blocks SBW*w .. SBW*w+SBW-1 of every tile and
 // keeps NB tiles in flight in its ring of LDS slices, filled by
 // global_load_lds_dwordx4 (SGPR base + per-lane offset) from inline assembly
 // with explicit in-order vmcnt waits: the compiler's own tracking of LDS DMA
@@ -700,7 +702,9 @@ __global__ void __launch_bounds__(TP == 1 ? 1024 : 512) k_gemv_mfma(const float*
 // stores its rows of y; groups alternate between two LDS areas, so the next
 // group's partials never overwrite ones still being added.
 // K a multiple of 256 SBW, K <= 4096.
-constexpr int GD_S = 4;  // tiles per reduction group
+constexpr int GD_S = 4;      // tiles per reduction group
+constexpr int GD_NB = 2;     // ring depth: tiles in flight per wave
+constexpr int GD_EARLY = 1;  // tiles requested before x is converted (more delay x itself)
 typedef int gd_i4 __attribute__((ext_vector_type(4)));
 
 template <int SBW>
@@ -721,11 +725,14 @@ __device__ __forceinline__ uint32_t gd_pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
 }
 
-// dynamic LDS of k_gemv_q4k_i8: ring, x, parts, part sums, scales, x sums, partial sums
+// dynamic LDS of k_gemv_q4k_i8: ring, x, partial sums, parts, part sums, scales, x sums
+__host__ __device__ constexpr size_t gd_xred_bytes(int K, int WB) {
+    return (size_t)K * 4 + (size_t)2 * GD_S * (WB + 1) * 64 * 4;
+}
 static size_t gd_lds_bytes(int K, int SBW, int NB) {
-    const size_t WB = K / (256 * SBW);
-    return (size_t)NB * WB * 144 * SBW * 16 + (size_t)K * 4 + 3 * (size_t)K + (size_t)K / 32 * 12 + (size_t)K / 32 * 8 +
-           2 * GD_S * WB * 64 * 4;
+    const int WB = K / (256 * SBW);
+    return (size_t)NB * WB * 144 * SBW * 16 + gd_xred_bytes(K, WB) + 3 * (size_t)K + (size_t)K / 32 * 12 +
+           (size_t)K / 32 * 8;
 }
 
 constexpr int GD_ATT_MAX = 1024;  // heads x splits of the attention-merge prologue
@@ -738,7 +745,7 @@ constexpr int GD_ATT_PT = 8;      // (max, sum) pairs per thread: GD_ATT_MAX / 1
 template <int SBW, int NB, bool FUSED = false>
 __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                            float* __restrict__ y, int K, int N, size_t rowb,
-                                                           GmFuse f) {
+                                                           int rpb, GmFuse f) {
     using C = GdCfg<SBW>;
     constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL;
     extern __shared__ __attribute__((aligned(16))) uint4 gd_lds[];
@@ -746,14 +753,16 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
     const int n16 = lane & 15, g = lane >> 4;
     const int WB = blockDim.x >> 6;  // = K / (256 SBW); K / 4 = SBW * blockDim.x float4 pieces of x
     const int K4 = K >> 2;
-    const int ntiles = (N + 15) >> 4, G = gridDim.x, t0 = blockIdx.x;
+    // rows [r_begin, r_end) of y, in tiles of 16 rows (the last one may hold fewer)
+    const int r_begin = blockIdx.x * rpb, r_end = min(N, r_begin + rpb);
+    const int nt = (r_end - r_begin + 15) >> 4;
     uint4* ring = gd_lds;                                   // [NB][WB][NP]
-    float4* sx = (float4*)(ring + (size_t)NB * WB * NP);    // [K / 4]
-    uint32_t* apart = (uint32_t*)(sx + K4);                 // [3][K / 4] four int8 parts each
+    float4* sx = (float4*)(ring + (size_t)NB * WB * NP);    // [K / 4], until x is converted
+    float4* sred = sx + K4;  // [2][GD_S][16 rows][WB + 1] (4 lane groups each; padded against bank conflicts)
+    uint32_t* apart = (uint32_t*)((char*)sx + gd_xred_bytes(K, WB));  // [3][K / 4] four int8 parts each
     int* shs = (int*)(apart + 3 * K4);                      // [K / 32][3] sums of the three parts
     float* ssc = (float*)(shs + 3 * (K >> 5));              // [K / 32] part scales s_j
     float* sxs = ssc + (K >> 5);                            // [K / 32] sums of x
-    float4* sred = (float4*)(sxs + (K >> 5));               // [2][GD_S][WB][16] (4 lane groups each)
     // x: piece tid + j * blockDim.x (contiguous per wave instruction)
     const bool pro = FUSED && f.pro != GM_PRO_NONE;
     const bool att = FUSED && f.pro == GM_PRO_ATTN;
@@ -821,33 +830,41 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         const int q = lane + 64 * i, r = q / PR, j = q - r * PR;
         voff[i] = (uint32_t)(r * rowb) + wave * (144 * SBW) + 16 * j;
     }
-    auto dma = [&](int tile, int b) {
+    // tile it of the block -> ring slice b
+    auto dma = [&](int it, int b) {
         uint4* dst = ring + ((size_t)b * WB + wave) * NP;
-        const uint8_t* base = W + (size_t)tile * 16 * rowb;
+        const int r0 = r_begin + 16 * it;
+        const uint8_t* base = W + (size_t)r0 * rowb;
         if (FUSED && f.w1) {  // weight segments (16-row aligned): rows [n0, n0+n1) from w1, then w2
-            const int r0 = tile * 16;
             if (r0 >= f.n0 + f.n1) base = (const uint8_t*)f.w2 + (size_t)(r0 - f.n0 - f.n1) * rowb;
             else if (r0 >= f.n0) base = (const uint8_t*)f.w1 + (size_t)(r0 - f.n0) * rowb;
         }
-        if (tile * 16 + 16 <= N) {
+        const int nv = r_end - r0;
+        if (nv >= 16) {
 #pragma unroll
             for (int i = 0; i < PPL; ++i)
                 if (NP % 64 == 0 || i + 1 < PPL || lane + 64 * i < NP) lds_dma16s(base, voff[i], lds_addr(dst + 64 * i));
-        } else {  // ragged last tile: rows past N re-read row N-1
+        } else {
+            // short tile: the pieces of rows past the range all read the wave's first piece of row
+            // r0 (one request per instruction; their outputs are not stored), so every lane still
+            // issues every transfer and the wave's transfer count stays the same
 #pragma unroll
             for (int i = 0; i < PPL; ++i) {
                 const int q = lane + 64 * i;
-                if (q < NP) {
-                    const int r = q / PR, j = q - r * PR, rc = tile * 16 + r < N ? r : N - 1 - tile * 16;
-                    lds_dma16s(base, (uint32_t)(rc * rowb) + wave * (144 * SBW) + 16 * j, lds_addr(dst + 64 * i));
+                if (NP % 64 == 0 || i + 1 < PPL || q < NP) {
+                    const int r = q / PR;
+                    lds_dma16s(base, r < nv ? voff[i] : (uint32_t)(wave * (144 * SBW)), lds_addr(dst + 64 * i));
                 }
             }
         }
     };
-    // the first NB tiles are always issued (a missing tile re-reads the last one), so every wait is exact
-    // only the first tile now: the memory system returns it sooner when the other tiles of the
-    // ring are requested after the conversion of x (the ring is always filled, so every wait is exact)
-    dma(t0 < ntiles ? t0 : ntiles - 1, 0);
+    // the first min(NB, nt) tiles are issued up front: GD_EARLY of them now, the rest after the
+    // conversion of x
+    const int early = min(GD_EARLY, nt);
+    dma(0, 0);
+#pragma unroll
+    for (int b = 1; b < GD_EARLY; ++b)
+        if (b < early) dma(b, b);
     if (att) {
         __shared__ float gd_att[2 * GD_ATT_MAX + 64];  // [H][S] max then split weight, [H][S] sums, [H] 1/L
         const int H = f.H, S = f.splits, HS = H * S;
@@ -930,8 +947,11 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         }
     }
     // ---- x -> three int8 parts per value; scale, x sum and part sums per 32 values (8 threads each)
-    lds_dma_wait<PPL>(1);  // x landed (the first tile in flight)
-    lds_barrier();
+    // With one super-block per wave, a wave converts exactly the 256 values its own A operands
+    // take (its lanes staged them), so no block barrier is needed before the tiles.
+    constexpr bool WAVE_LOCAL = SBW == 1;
+    lds_dma_wait<PPL>(early);  // x landed (the early tiles in flight)
+    if (WAVE_LOCAL) lds_wait_lgkm(); else lds_barrier();
 #pragma unroll
     for (int jj = 0; jj < SBW; ++jj) {
         const int idx = tid + jj * blockDim.x;
@@ -972,10 +992,11 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             shs[3 * sbk + 2] = ps[2];
         }
     }
-    // the rest of the ring (a missing tile re-reads the last one)
+    // the rest of the ring
 #pragma unroll
-    for (int b = 1; b < NB; ++b) dma(t0 + b * G < ntiles ? t0 + b * G : ntiles - 1, b);
-    lds_barrier();
+    for (int b = GD_EARLY; b < NB; ++b)
+        if (b < nt) dma(b, b);
+    if (WAVE_LOCAL) lds_wait_lgkm(); else lds_barrier();
     // A operands of this wave's super-blocks (rows m = 4g + e of group g), scales, high-nibble offsets
     gd_i4 A[SBW][2][2], hinit[SBW];
     float s_lo[SBW], s_hi[SBW], xs_lo[SBW], xs_hi[SBW];
@@ -1002,13 +1023,9 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         }
     }
     int b = 0;
-    for (int it = 0;; ++it) {
-        const int tile = t0 + it * G;
-        if (tile >= ntiles) break;
-        // tiles issued after this one: it+1 .. it+NB-1, each issued if among the first NB or real
-        int ahead = 0;
-#pragma unroll
-        for (int j = 1; j < NB; ++j) ahead += (it + j < NB || tile + j * G < ntiles) ? 1 : 0;
+    for (int it = 0; it < nt; ++it) {
+        // tiles issued after this one: it+1 .. min(it+NB-1, nt-1)
+        const int ahead = min(NB - 1, nt - 1 - it);
         lds_dma_wait<PPL>(ahead);
         const unsigned char* rowp = (const unsigned char*)(ring + ((size_t)b * WB + wave) * NP) + n16 * (144 * SBW);
         uint4 hd[SBW], qa[SBW], qb[SBW];
@@ -1018,9 +1035,9 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
             qa[sbl] = *(const uint4*)(rowp + 144 * sbl + 16 + 32 * g);
             qb[sbl] = *(const uint4*)(rowp + 144 * sbl + 32 + 32 * g);
         }
-        if (tile + NB * G < ntiles) {  // slice read: refill it
+        if (it + NB < nt) {  // slice read: refill it
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            dma(tile + NB * G, b);
+            dma(it + NB, b);
         }
         float acc = 0.f;
 #pragma unroll
@@ -1047,9 +1064,9 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         }
         // partial of (row n16, lane group g) -> slot; a group of GD_S tiles is added up at once
         const int slot = it & (GD_S - 1), grp = (it / GD_S) & 1;
-        float4* red = sred + (size_t)(grp * GD_S + slot) * WB * 16;
-        ((float*)&red[wave * 16 + n16])[g] = acc;
-        if (slot == GD_S - 1 || tile + G >= ntiles) {
+        float4* red = sred + (size_t)(grp * GD_S + slot) * 16 * (WB + 1);
+        ((float*)&red[n16 * (WB + 1) + wave])[g] = acc;
+        if (slot == GD_S - 1 || it + 1 >= nt) {
             lds_barrier();
             // thread (output o, wave w = tid % 16) adds w's four lane groups; 16 lanes add the waves
             const int w = tid & 15;
@@ -1057,15 +1074,15 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
                 const int tl = o >> 4, row = o & 15;
                 float v = 0.f;
                 if (w < WB) {
-                    const float4 p4 = sred[(size_t)(grp * GD_S + tl) * WB * 16 + w * 16 + row];
+                    const float4 p4 = sred[(size_t)(grp * GD_S + tl) * 16 * (WB + 1) + row * (WB + 1) + w];
                     v = (p4.x + p4.y) + (p4.z + p4.w);
                 }
                 v += __shfl_xor(v, 1, 64);
                 v += __shfl_xor(v, 2, 64);
                 v += __shfl_xor(v, 4, 64);
                 v += __shfl_xor(v, 8, 64);
-                const int n = (tile - (slot - tl) * G) * 16 + row;
-                if (w == 0 && n < N) {
+                const int n = r_begin + 16 * (it - (slot - tl)) + row;
+                if (w == 0 && n < r_end) {
                     if constexpr (FUSED) gm_epilogue(y, n, n, v, f, GmEpiPre{}, false);
                     else y[n] = v;
                 }
@@ -1175,19 +1192,22 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, c
         hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED>, 64 * wb, lds);
         per_cu[wb] = e == hipSuccess && nb > 0 ? nb : 1;
     }
-    const int ntiles = (N + 15) / 16;
+    // contiguous row ranges, equal up to 8 rows (16 with weight segments): every block
+    // streams the same number of bytes, so no CU runs a tile more than the others
     const int slots = per_cu[wb] * num_cus();
-    const int blocks = ntiles < slots ? ntiles : slots;
+    const int align = FUSED && f.w1 ? 16 : 8;
+    const int rpb = ((N + slots - 1) / slots + align - 1) / align * align;
+    const int blocks = (N + rpb - 1) / rpb;
     hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K, N,
-                       row_bytes(3, K), f);
+                       row_bytes(3, K), rpb, f);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
 }
 
 // variant 1: one super-block per wave; 2: two super-blocks per wave (needs K % 512 == 0)
 static int gemv_q4k_i8(const float* x, const uint8_t* w, float* y, int K, int N, int variant) {
-    if (variant == 2 && K % 512 == 0) return gd_launch<2, 2>(x, w, y, K, N);
-    return gd_launch<1, 2>(x, w, y, K, N);
+    if (variant == 2 && K % 512 == 0) return gd_launch<2, GD_NB>(x, w, y, K, N);
+    return gd_launch<1, GD_NB>(x, w, y, K, N);
 }
 
 // Returns 1 if handled (Q4_K / Q8_0, 1 <= M <= 8, K a multiple of 256).
@@ -1227,7 +1247,7 @@ int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, 
         (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
         // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
         // streaming GEMV
-        return gd_launch<1, 2, true>(x, (const uint8_t*)w, y, K, N, f);
+        return gd_launch<1, GD_NB, true>(x, (const uint8_t*)w, y, K, N, f);
     }
     if (f.emb) return GH_EUNSUPPORTED;  // the folded step start exists on the int8 path only (no launch made)
     if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
