@@ -51,12 +51,13 @@ __global__ void k_conv1d(const float* __restrict__ proj, int proj_ld, int col0, 
 }
 
 // dt = softplus(dt_raw + dt_bias), A = -exp(A_log), and the chunk-local
-// inclusive cumulative sums of A*dt. One wave per (chunk, head).
-__global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in, int dt_ld,
-                                                 const float* __restrict__ dt_bias, const float* __restrict__ A_in,
-                                                 const float* __restrict__ a_log, float* __restrict__ dt_out,
-                                                 float* __restrict__ cum, int T, int H, int L) {
-    const int c = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+// inclusive cumulative sums of A*dt of (chunk c, head h), by one wave; also into
+// the LDS arrays ldt / lcum ([L]) of the calling block.
+__device__ __forceinline__ void ssd_prep_wave(const float* __restrict__ dt_in, int dt_ld,
+                                              const float* __restrict__ dt_bias, const float* __restrict__ A_in,
+                                              const float* __restrict__ a_log, float* __restrict__ dt_out,
+                                              float* __restrict__ cum, int T, int H, int L, int c, int h, int lane,
+                                              float* ldt, float* lcum) {
     const int t0 = c * L, len = min(L, T - t0);
     const float A = A_in ? A_in[h] : -expf(a_log[h]);
     // the raw dt of all positions (up to 4 per lane) are requested before the first scan step
@@ -87,6 +88,8 @@ __global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in
         if (i < len) {
             dt_out[(size_t)(t0 + i) * H + h] = dt;
             cum[(size_t)(t0 + i) * H + h] = carry + inc;
+            ldt[i] = dt;
+            lcum[i] = carry + inc;
         }
         carry += __shfl(inc, 63, 64);
     }
@@ -96,11 +99,10 @@ __global__ void __launch_bounds__(64) k_ssd_prep(const float* __restrict__ dt_in
 // the matrix cores (fp16 operands, fp32 accumulation; G only enters the
 // scan as an fp16 operand). C and B rows are staged into LDS with 16-byte loads.
 template <int N>
-__global__ void __launch_bounds__(256) k_ssd_cb(const float* __restrict__ Bm, const float* __restrict__ Cm, int ld,
-                                                float* __restrict__ G, int T, int L) {
+__device__ __forceinline__ void ssd_cb_block(const float* __restrict__ Bm, const float* __restrict__ Cm, int ld,
+                                             float* __restrict__ G, int T, int L, int c, int ti, int si,
+                                             _Float16* sC, _Float16* sB) {
     constexpr int SN = N + 8;
-    __shared__ __attribute__((aligned(16))) _Float16 sC[64 * SN], sB[64 * SN];
-    const int c = blockIdx.z, ti = blockIdx.y * 64, si = blockIdx.x * 64;
     const int t0 = c * L, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int e = threadIdx.x; e < 64 * N / 4; e += 256) {
         const int r = (4 * e) / N, k = (4 * e) % N;
@@ -207,20 +209,38 @@ struct Stage64 {
     }
 };
 
+// The first launch of the scan. Blocks [0, nch H): the chunk state of (chunk, head)
+// with the dt / cum prep of that pair done by its first wave (written out for the
+// chunk-output launch, kept in LDS here); blocks after that: the G tiles of k_ssd
+// cb (they need nothing from the prep), side by side in the same launch.
+// dS[c][h][p][n] = sum_tau e^(cum_end - cum_tau) dt_tau x_tau[p] B_tau[n]
+// (P = 64 rows, N cols in 32-wide MFMA tiles), fp16 operands, fp32 acc.
 template <int N>
-__global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict__ xs, int ldx,
-                                                         const float* __restrict__ Bm, int ldb,
-                                                         const float* __restrict__ dt, const float* __restrict__ cum,
-                                                         float* __restrict__ dS, float* __restrict__ decay, int T,
-                                                         int H, int L) {
-    constexpr int P = 64, TK = 64, S = TK + 8;
-    __shared__ __attribute__((aligned(16))) _Float16 sX[P * S];  // [p][tau]
-    __shared__ __attribute__((aligned(16))) _Float16 sB[N * S];  // [n][tau]
-    __shared__ float sw[TK];
-    const int c = blockIdx.x, h = blockIdx.y;
+__global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ xs, int ldx,
+                                                      const float* __restrict__ Bm, const float* __restrict__ Cm,
+                                                      int ldb, const float* __restrict__ dt_in, int dt_ld,
+                                                      const float* __restrict__ dt_bias, const float* __restrict__ A_in,
+                                                      const float* __restrict__ a_log, float* __restrict__ dt,
+                                                      float* __restrict__ cum, float* __restrict__ G,
+                                                      float* __restrict__ dS, float* __restrict__ decay, int T,
+                                                      int H, int L) {
+    constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
+    constexpr int U_STATE = (P * S + N * S) * 2, U_CB = 2 * 64 * SN * 2;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[U_STATE > U_CB ? U_STATE : U_CB];
+    const int nch = (T + L - 1) / L;
+    if ((int)blockIdx.x >= nch * H) {
+        const int b = blockIdx.x - nch * H, nt = L / 64;
+        ssd_cb_block<N>(Bm, Cm, ldb, G, T, L, b / (nt * nt), (b / nt) % nt * 64, b % nt * 64, (_Float16*)smem,
+                        (_Float16*)smem + 64 * SN);
+        return;
+    }
+    _Float16* sX = (_Float16*)smem;  // [p][tau]
+    _Float16* sB = sX + P * S;       // [n][tau]
+    __shared__ float sw[TK], ldt[256], lcum[256];
+    const int c = blockIdx.x % nch, h = blockIdx.x / nch;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t0 = c * L, len = min(L, T - t0);
-    const float cend = cum[(size_t)(t0 + len - 1) * H + h];
+    if (wave == 0) ssd_prep_wave(dt_in, dt_ld, dt_bias, A_in, a_log, dt, cum, T, H, L, c, h, lane, ldt, lcum);
     constexpr int NT = (P / 32) * (N / 32);  // output tiles
     constexpr int TPW = NT / 4;              // tiles per wave
     f32x16 acc[TPW];
@@ -235,22 +255,21 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_state(const float* __restrict
     // tile is multiplied (no global round trip inside the loop)
     Stage64<P> rx;
     Stage64<N> rb;
-    float pc = 0.f, pd = 0.f;
     auto prefetch = [&](int kk) {
         const int k0 = ((kk + h) % ntk) * TK;
-        if (threadIdx.x < TK) {
-            const int tau = k0 + threadIdx.x;
-            pc = tau < len ? cum[(size_t)(t0 + tau) * H + h] : 0.f;
-            pd = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
-        }
         rx.load(xs + (size_t)(t0 + k0) * ldx + h * P, ldx, len - k0);
         rb.load(Bm + (size_t)(t0 + k0) * ldb, ldb, len - k0);
     };
     prefetch(0);
+    __syncthreads();  // the prep wave's ldt / lcum
+    const float cend = lcum[len - 1];
     for (int kk = 0; kk < ntk; ++kk) {
         const int k0 = ((kk + h) % ntk) * TK;
         __syncthreads();  // the previous tile's operands are consumed
-        if (threadIdx.x < TK) sw[threadIdx.x] = k0 + (int)threadIdx.x < len ? expf(cend - pc) * pd : 0.f;
+        if (threadIdx.x < TK) {
+            const int tau = k0 + (int)threadIdx.x;
+            sw[threadIdx.x] = tau < len ? expf(cend - lcum[tau]) * ldt[tau] : 0.f;
+        }
         __syncthreads();
         rx.template store<S>(sX, sw);
         rb.template store<S>(sB, nullptr);
@@ -333,8 +352,11 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
                                                        int T, int H, int L) {
     constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
     // phase 1 (inter-chunk term): sC [t][n] and sS [p][n]; phase 2: sA [t][tau] and sXt [p][tau]
-    constexpr int U1 = (64 * SN + P * SN) * 2, U2 = (64 * S + P * S) * 2;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[U1 > U2 ? U1 : U2];
+    // sDx [t][p] fp32: D x_t of the block's rows, kept from the diagonal tile's X rows for the
+    // epilogue (after sA / sXt; no second read of X)
+    constexpr int U1 = (64 * SN + P * SN) * 2, U2 = (64 * S + P * S) * 2, U3 = U2 + 64 * P * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[U1 > U3 ? U1 : U3];
+    float* sDx = (float*)(smem + U2);
     _Float16* sC = (_Float16*)smem;
     _Float16* sS = sC + 64 * SN;
     _Float16* sA = (_Float16*)smem;
@@ -362,26 +384,6 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
         const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
         cv[j] = tt + r < len ? *(const float4*)(Cm + (size_t)(t0 + tt + r) * ldc + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
         sv[j] = ((const float4*)Sc)[e];  // P * N / 4 == 64 * N / 4
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
-        const float sc = tt + r < len ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
-        const float4 v = cv[j], w = sv[j];
-        f16x4 hv, hw;
-        hv[0] = (_Float16)(v.x * sc); hv[1] = (_Float16)(v.y * sc); hv[2] = (_Float16)(v.z * sc); hv[3] = (_Float16)(v.w * sc);
-        *(f16x4*)(sC + r * SN + cc) = hv;
-        hw[0] = (_Float16)w.x; hw[1] = (_Float16)w.y; hw[2] = (_Float16)w.z; hw[3] = (_Float16)w.w;
-        *(f16x4*)(sS + r * SN + cc) = hw;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < N / 16; ++ks) {
-        const int ko = ks * 16 + 8 * (lane >> 5);
-        const f16x8 a = *(const f16x8*)(sC + ar * SN + ko);
-        const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
     }
     // ---- intra-chunk term over tau tiles up to the last row of this block. The next tile's
     // operands (cum / dt of its positions, the X rows, this block's G rows) are loaded into
@@ -412,6 +414,26 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
             pg[j] = t < len ? *(const float4*)(G + ((size_t)c * L + t) * L + k0 + q) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
+        const float sc = tt + r < len ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
+        const float4 v = cv[j], w = sv[j];
+        f16x4 hv, hw;
+        hv[0] = (_Float16)(v.x * sc); hv[1] = (_Float16)(v.y * sc); hv[2] = (_Float16)(v.z * sc); hv[3] = (_Float16)(v.w * sc);
+        *(f16x4*)(sC + r * SN + cc) = hv;
+        hw[0] = (_Float16)w.x; hw[1] = (_Float16)w.y; hw[2] = (_Float16)w.z; hw[3] = (_Float16)w.w;
+        *(f16x4*)(sS + r * SN + cc) = hw;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < N / 16; ++ks) {
+        const int ko = ks * 16 + 8 * (lane >> 5);
+        const f16x8 a = *(const f16x8*)(sC + ar * SN + ko);
+        const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+    }
     prefetch(0);
     for (int kk = 0; kk < ntk; ++kk) {
         const int k0 = ((kk + h) % ntk) * TK;
@@ -431,6 +453,13 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
                 h3[i] = (_Float16)px[i].w;
             }
             _Float16* d = sXt + (4 * xq) * S + xg * XR;
+            if (k0 == tt) {  // the diagonal tile: these X rows are the block's own rows
+                const float Dh = D[h];
+#pragma unroll
+                for (int i = 0; i < XR; ++i)
+                    *(float4*)(sDx + (xg * XR + i) * P + 4 * xq) =
+                        make_float4(Dh * px[i].x, Dh * px[i].y, Dh * px[i].z, Dh * px[i].w);
+            }
             *(hrun*)d = h0;
             *(hrun*)(d + S) = h1;
             *(hrun*)(d + 2 * S) = h2;
@@ -467,15 +496,12 @@ __global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__
         }
     }
     // ---- + D x, store. acc element e: t row wt + 8(e/4)+4(lane/32)+e%4, p col wp + lane%32
-    const float Dh = D[h];
+    __syncthreads();  // sDx complete
     const int p = wp + (lane & 31);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        const int t = tt + wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (t < len) {
-            const size_t row = (size_t)(t0 + t);
-            y[row * ldy + h * P + p] = acc[e] + Dh * xs[row * ldx + h * P + p];
-        }
+        const int tl = wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), t = tt + tl;
+        if (t < len) y[(size_t)(t0 + t) * ldy + h * P + p] = acc[e] + sDx[tl * P + p];
     }
 }
 
@@ -499,16 +525,13 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     float* dS = G + f_G;
     float* Sin = dS + f_S;
     float* decay = Sin + f_S;
-    hipLaunchKernelGGL(k_ssd_prep, dim3(nch, H), dim3(64), 0, stream(), dt_raw, dt_ld, dt_bias, A, a_log, dt, cum, T,
-                       H, L);
-    if (N == 128) hipLaunchKernelGGL(k_ssd_cb<128>, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, L);
-    else hipLaunchKernelGGL(k_ssd_cb<64>, dim3(L / 64, L / 64, nch), dim3(256), 0, stream(), Bm, Cm, ldbc, G, T, L);
+    const unsigned nb1 = (unsigned)(nch * H + nch * (L / 64) * (L / 64));  // chunk states, then G tiles
     if (N == 128) {
-        hipLaunchKernelGGL(k_ssd_chunk_state<128>, dim3(nch, H), dim3(256), 0, stream(), xs, ldx, Bm, ldbc, dt, cum, dS,
-                           decay, T, H, L);
+        hipLaunchKernelGGL(k_ssd_state_cb<128>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
+                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L);
     } else {
-        hipLaunchKernelGGL(k_ssd_chunk_state<64>, dim3(nch, H), dim3(256), 0, stream(), xs, ldx, Bm, ldbc, dt, cum, dS,
-                           decay, T, H, L);
+        hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
+                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L);
     }
     const int64_t nst = (int64_t)H * PN;
     hipLaunchKernelGGL(k_ssd_state_pass, dim3((unsigned)((nst + 255) / 256)), dim3(256), 0, stream(), state, dS, decay,
