@@ -206,9 +206,8 @@ __device__ __forceinline__ void gm_put_one(uint16_t* a16, float* xsum, int i, fl
 // Forms the activation vector of ONE token (K values) directly into the
 // MFMA layout + group sums; every block computes the same values. Every
 // operand is requested before the first one is used (one memory round trip
-// instead of one per dependent load): a thread keeps up to GM_PR elements
+// instead of one per dependent load): a thread keeps its first elements
 // of each input in registers; xf [K floats] is scratch for the rest.
-constexpr int GM_PR = 8;
 constexpr int GM_SPR = 4;  // attention splits whose partials are held in registers
 
 template <int KIND>

@@ -53,6 +53,9 @@ hipStream_t stream();
 // buffers that are live at the same time apart.
 void* workspace(int slot, size_t bytes);
 void  free_workspaces();
+// Changes whenever a workspace buffer is replaced or freed: work captured into a graph
+// holds the buffer addresses of its capture and is stale once this moves on.
+uint64_t workspace_generation();
 
 // Device count of compute units (for grid sizing).
 int num_cus();

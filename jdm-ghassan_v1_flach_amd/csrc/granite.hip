@@ -274,6 +274,7 @@ struct gh_granite {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     hipStream_t cap_stream = nullptr;  // the stream the graph was captured on; lives as long as the graph
+    uint64_t graph_ws_gen = 0;         // workspace generation the graph's buffer addresses belong to
     // persistent decode loop: its model description (device copy) and hand-over buffers
     PdModel* pd_dev = nullptr;
     uint8_t* pd_buf = nullptr;
@@ -903,6 +904,15 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
         ++done;
     }
     if (use_graph >= 1 && done < n_new) {
+        if (g->graph_exec && g->graph_ws_gen != workspace_generation()) {
+            // a workspace buffer the graph reads or writes was replaced since the capture (a
+            // larger prefill grew it): the captured addresses are stale, capture again
+            GH_HIP(hipStreamSynchronize(stream()));
+            (void)hipGraphExecDestroy(g->graph_exec);
+            (void)hipGraphDestroy(g->graph);
+            g->graph_exec = nullptr;
+            g->graph = nullptr;
+        }
         if (!g->graph_exec) {
             // Capture needs a non-null stream. When the backend stream is the null stream, the
             // capture runs on a stream the model owns and keeps until the graph is destroyed
@@ -927,6 +937,7 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
             if (e != hipSuccess) return fail(GH_EHIP, "decode graph capture: %s", hipGetErrorString(e));
             g->graph = graph;
             GH_HIP(hipGraphInstantiate(&g->graph_exec, graph, nullptr, nullptr, 0));
+            g->graph_ws_gen = workspace_generation();
         }
         for (; done < n_new; ++done) GH_HIP(hipGraphLaunch(g->graph_exec, stream()));
     } else {

@@ -48,10 +48,14 @@ struct Workspace {
 };
 static std::vector<Workspace> g_ws(64);
 
+static uint64_t g_ws_gen = 0;  // bumped whenever a slot gets a new buffer
+uint64_t workspace_generation() { return g_ws_gen; }
+
 void* workspace(int slot, size_t bytes) {
     if (slot < 0 || slot >= (int)g_ws.size()) return nullptr;
     Workspace& w = g_ws[(size_t)slot];
     if (w.bytes < bytes) {
+        ++g_ws_gen;
         // grow-only; the old buffer may still be read by queued work
         if (w.ptr) {
             (void)hipStreamSynchronize(g_stream);
@@ -71,6 +75,7 @@ void* workspace(int slot, size_t bytes) {
 
 void free_workspaces() {
     (void)hipStreamSynchronize(g_stream);
+    ++g_ws_gen;
     for (Workspace& w : g_ws) {
         if (w.ptr) (void)hipFree(w.ptr);
         w = Workspace{};

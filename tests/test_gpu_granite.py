@@ -96,6 +96,23 @@ def test_graph_replay_equals_eager(model):
     assert np.array_equal(la, lb)
 
 
+def test_graph_recaptured_after_workspace_growth(gh):
+    """A longer prefill after the decode graph was captured grows backend workspaces the
+    graph reads (the MoE routing slots among them); the next generate must capture again
+    rather than replay stale addresses: ids equal eager decode on the same prompt."""
+    gh.call("gh_free_workspace")  # every workspace starts small (other models' graphs recapture too)
+    m = Granite(gh, O.C1, 3, max_ctx=256)
+    try:
+        short = O.rng_below(5, 8, 4096)
+        long_ = O.rng_below(6, 160, 4096)
+        m.generate(short, 6, 1, 1)  # captures the graph with small workspaces
+        a, _ = m.generate(long_, 24, 1, 1)
+        b, _ = m.generate(long_, 24, 1, 0)
+        assert np.array_equal(a, b)
+    finally:
+        m.close()
+
+
 def test_persistent_decode_equals_graph(model):
     """use_graph=2: the whole decode loop in one cooperative launch gives the ids
     of graph replay, twice in a row (the hand-over buffers are re-zeroed per call)."""
