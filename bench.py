@@ -167,7 +167,7 @@ def kernel_suite(gh):
     ms = time_launches(gh, lambda: gh.call("gh_ssd_scan", *[b.p for b in bufs], st.p, yb.p, T, H, P, N, 256), 10)
     scan_bytes = 2 * (T * H * P + 2 * T * N + T * H + T * H * P) + 2 * H * P * N * 4  # fp16-equivalent I/O + state
     flops = 2.0 * (16 * 256 * 256 * N) + H * 16 * (2.0 * 256 * 256 * P + 4.0 * 256 * N * P)
-    res["c3_ssd_scan_T4096"] = entry("k_ssd_* (5 launches)", ms, bytes_=scan_bytes, flops=flops, bound="hbm")
+    res["c3_ssd_scan_T4096"] = entry("k_ssd_state_cb+k_ssd_state_pass+k_ssd_chunk_out (3 launches)", ms, bytes_=scan_bytes, flops=flops, bound="hbm")
     del bufs, st, yb
     d, di, nh, ds, kk = 1536, 3072, 48, 128, 4
     conv_dim = di + 2 * ds
