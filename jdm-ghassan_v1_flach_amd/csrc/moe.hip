@@ -974,6 +974,138 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny grouped GEMM (Q4_K, K = 256 or 512): tiles of 32 grouped rows x 64 weight
+// rows (DUAL: 32 gate + the matching 32 up rows, i.e. 32 outputs), the WHOLE K in
+// one pass: the block's 32 activation rows (fp16) go to LDS once, and each lane
+// requests every Q4_K byte its MFMA B operands need (8 values per k-step of 32,
+// plus the super-block headers) before the first multiply, so a block waits for
+// memory once instead of once per K step (the 128-row tiles of k_moe_group_gemm2
+// spent ~2 us per K step on a group of ~32 rows). Wave w owns weight rows
+// 16w..16w+15 of the tile: v_mfma_f32_16x16x32_f16 with the activations as A
+// (two 16-row halves) and the lane's dequantised weights as B (lane: weight row
+// l % 16, values 8 (l / 16) .. +7 of the k-step, one sub-block of one super-block).
+// Weights are rounded to fp16 after dequantisation (d sc q - dmin m in fp32),
+// as in the 128-row kernel.
+typedef _Float16 f16x8s __attribute__((ext_vector_type(8)));
+typedef float f32x4s __attribute__((ext_vector_type(4)));
+template <bool DUAL, int KK>
+__global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
+    constexpr int SA = KK + 8;  // LDS row stride (fp16)
+    constexpr int NSTEP = KK / 32, NSB = KK / 256;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
+    __shared__ float sU[DUAL ? 32 * 33 : 1];
+    const int tile = blockIdx.x;
+    if (tile >= P.tiles[0]) return;
+    const int g = P.tiles[1 + 2 * tile], m0 = P.tiles[2 + 2 * tile];
+    const int mend = P.offsets[g + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int K = KK;
+    // weight row of this lane: DUAL waves 0-1 gate, 2-3 up rows of outputs n0 .. n0+31
+    const int NT = DUAL ? 32 : 64;
+    const int n0 = blockIdx.y * NT;
+    const int col = lane & 15, kq = lane >> 4;
+    const int nrow = DUAL ? n0 + 16 * (wave & 1) + col : n0 + 16 * wave + col;
+    const bool nok = nrow < P.N;
+    const uint8_t* W = (DUAL && wave >= 2 ? P.W1 : P.W0) + (size_t)g * P.gstride;
+    const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * P.rowb;
+    // every weight byte of the lane, requested first
+    uint4 hdr[NSB];
+    uint2 qb[NSTEP];
+#pragma unroll
+    for (int b = 0; b < NSB; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)b * 144);
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+        const int sb = s >> 3, sub = s & 7;
+        qb[s] = *(const uint2*)(wrow + (size_t)sb * 144 + 16 + 32 * (sub >> 1) + 8 * kq);
+    }
+    // the 32 activation rows (grouped positions m0 .. m0+31) into LDS
+    const int rq = K / 8;  // 16-byte pieces per row
+    for (int e = tid; e < 32 * rq; e += 256) {
+        const int r = e / rq, c = e - r * rq, m = m0 + r;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (m < mend) {
+            const int arow = P.gather ? P.gather[m] / P.topk : m;
+            v = *(const uint4*)(P.A16 + (size_t)arow * P.lda + 8 * c);
+        }
+        *(uint4*)(sA + r * SA + 8 * c) = v;
+    }
+    __syncthreads();
+    f32x4s acc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) acc[h] = f32x4s{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+        const int sb = s >> 3, sub = s & 7;
+        // scale / min of sub-block `sub` (6-bit packed, as WLoad<3>)
+        const uint4 hd = hdr[sb];
+        const uint32_t sc4[3] = {hd.y, hd.z, hd.w};
+        auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+        int scv, mv;
+        if (sub < 4) {
+            scv = scb(sub) & 63;
+            mv = scb(sub + 4) & 63;
+        } else {
+            scv = (scb(sub + 4) & 0xF) | ((scb(sub - 4) >> 6) << 4);
+            mv = (scb(sub + 4) >> 4) | ((scb(sub) >> 6) << 4);
+        }
+        const float d1 = f16_to_f32((uint16_t)(hd.x & 0xFFFF)) * (float)scv;
+        const float m1 = f16_to_f32((uint16_t)(hd.x >> 16)) * (float)mv;
+        const int sh = 4 * (sub & 1);  // low nibbles: even sub-block, high: odd
+        const uint32_t q2[2] = {qb[s].x, qb[s].y};
+        f16x8s bv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float qq = (float)((q2[i >> 2] >> (8 * (i & 3) + sh)) & 0xF);
+            bv[i] = (_Float16)(nok ? d1 * qq - m1 : 0.f);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const f16x8s av = *(const f16x8s*)(sA + (16 * h + (lane & 15)) * SA + 32 * s + 8 * kq);
+            acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
+        }
+    }
+    // acc[h][j]: row 16 h + 4 (lane / 16) + j, weight row column lane % 16
+    if (DUAL) {
+        if (wave >= 2) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sU[(16 * h + 4 * kq + j) * 33 + 16 * (wave & 1) + col] = acc[h][j];
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const int oc = n0 + 16 * wave + col;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 16 * h + 4 * kq + j, m = m0 + r;
+                    if (m < mend && oc < P.N) {
+                        const float gv = acc[h][j], uv = sU[r * 33 + 16 * wave + col];
+                        P.out16[(size_t)m * P.N + oc] = f32_to_f16(gv / (1.0f + expf(-gv)) * uv);
+                    }
+                }
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = m0 + 16 * h + 4 * kq + j;
+                if (m < mend && nok) P.out[(size_t)m * P.N + nrow] = acc[h][j];
+            }
+    }
+}
+
+// the skinny kernel for K = 256 or 512 (the caller checks K); grid (tiles, outputs / 32 or 64)
+template <bool DUAL>
+static void launch_skinny(const GroupGemm& P, int ntiles) {
+    const dim3 grid(ntiles, DUAL ? P.N / 32 : cdiv(P.N, 64));
+    if (P.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(256), 0, stream(), P);
+    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(256), 0, stream(), P);
+}
+
 // tile table of one group covering rows [0, N)
 __global__ void k_single_group_tiles(int32_t* tiles, int32_t* offs, int N, int bm) {
     const int nt = (N + bm - 1) / bm;
@@ -1055,15 +1187,19 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         GH_LAUNCHED("k_moe_down_combine");
         return GH_OK;
     }
-    // prefill: permutation, grouped gate/up GEMM, grouped down GEMM, combine
-    int32_t* perm = (int32_t*)workspace(WS_MOE_XG, ((size_t)2 * S + ne + 1 + 1 + 2 * ((size_t)S / BM + ne + 1)) * 4);
+    // prefill: permutation, grouped gate/up GEMM, grouped down GEMM, combine. Small groups
+    // (a few dozen rows per expert) take the skinny 32-row tiles with the whole K in one pass.
+    auto kfits = [](int k) { return k == 256 || k == 512; };
+    const bool skinny = KIND == 3 && (size_t)S <= (size_t)64 * ne && kfits(d) && kfits(E) && (!has_sh || kfits(SH));
+    const int bm = skinny ? 32 : BM;
+    int32_t* perm = (int32_t*)workspace(WS_MOE_XG, ((size_t)2 * S + ne + 1 + 1 + 2 * ((size_t)S / bm + ne + 1)) * 4);
     if (!perm) return fail(GH_ENOMEM, "moe: workspace");
     int32_t* grouped = perm;
     int32_t* pos = perm + S;
     int32_t* offsets = pos + S;
     int32_t* tiles = offsets + ne + 1;
-    const int max_tiles = S / BM + ne + 1;
-    int rc = permute(idx, S, ne, grouped, offsets, pos, tiles, BM);
+    const int max_tiles = S / bm + ne + 1;
+    int rc = permute(idx, S, ne, grouped, offsets, pos, tiles, bm);
     if (rc) return rc;
     if constexpr (KIND == 2 || KIND == 3 || KIND == 4) {
         // v2: fp16 activations converted once; gate/up write fp16 SwiGLU rows
@@ -1077,29 +1213,33 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         P.A16 = x16; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
         P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
         P.K = d; P.N = E; P.out16 = act16;
-        hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
+        if (skinny) launch_skinny<true>(P, max_tiles);
+        else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
         GH_LAUNCHED("k_moe_group_gemm2(gate/up)");
         GroupGemm Q{};
         Q.A16 = act16; Q.lda = E; Q.gather = nullptr; Q.topk = 1; Q.tiles = tiles; Q.offsets = offsets;
         Q.W0 = (const uint8_t*)downs; Q.gstride = (size_t)d * rowb_E; Q.rowb = rowb_E; Q.K = E; Q.N = d; Q.out = yr;
-        hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
+        if (skinny) launch_skinny<false>(Q, max_tiles);
+        else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
         GH_LAUNCHED("k_moe_group_gemm2(down)");
         if (has_sh) {
-            int32_t* sh_tiles = (int32_t*)workspace(WS_MOE_H, ((size_t)2 * (N / BM + 2) + 1 + 2) * 4);
+            int32_t* sh_tiles = (int32_t*)workspace(WS_MOE_H, ((size_t)2 * (N / bm + 2) + 1 + 2) * 4);
             if (!sh_tiles) return fail(GH_ENOMEM, "moe: workspace");
-            int32_t* sh_off = sh_tiles + 2 * (N / BM + 2) + 1;
-            const int nt = cdiv(N, BM);
-            hipLaunchKernelGGL(k_single_group_tiles, dim3(1), dim3(64), 0, stream(), sh_tiles, sh_off, N, BM);
+            int32_t* sh_off = sh_tiles + 2 * (N / bm + 2) + 1;
+            const int nt = cdiv(N, bm);
+            hipLaunchKernelGGL(k_single_group_tiles, dim3(1), dim3(64), 0, stream(), sh_tiles, sh_off, N, bm);
             GH_LAUNCHED("k_single_group_tiles");
             GroupGemm R{};
             R.A16 = x16; R.lda = d; R.gather = nullptr; R.topk = 1; R.tiles = sh_tiles; R.offsets = sh_off;
             R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.gstride = 0; R.rowb = rowb_d;
             R.K = d; R.N = SH; R.out16 = sh_act16;
-            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
+            if (skinny) launch_skinny<true>(R, nt);
+            else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
             GroupGemm U{};
             U.A16 = sh_act16; U.lda = SH; U.gather = nullptr; U.topk = 1; U.tiles = sh_tiles; U.offsets = sh_off;
             U.W0 = (const uint8_t*)sh_d; U.gstride = 0; U.rowb = rowb_SH; U.K = SH; U.N = d; U.out = sh_y;
-            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
+            if (skinny) launch_skinny<false>(U, nt);
+            else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
             GH_LAUNCHED("k_moe_group_gemm2(shared)");
         }
         {
