@@ -549,6 +549,85 @@ __global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int
         y[i] += t[i];
 }
 
+// ---------------------------------------------------------------- skinny
+// Small M (prefill of a short prompt), Q4_K, K = 256, 512 or 1024: a block takes 32
+// rows of x (fp32, converted to fp16 while staged into LDS) and 64 weight rows over
+// the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the
+// first multiply (one memory wait per block instead of one per K step, and no split-K
+// partials to add), wave w owns weight rows 16w..16w+15 (v_mfma_f32_16x16x32_f16,
+// activations as A in two 16-row halves). Each output is written (or added, with
+// `accumulate`) by exactly one lane.
+template <int KK>
+__global__ void __launch_bounds__(256) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
+                                                     float* __restrict__ Y, int M, int N, size_t rowb,
+                                                     int accumulate) {
+    constexpr int SA = KK + 8, NSTEP = KK / 32, NSB = KK / 256;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
+    const int m0 = blockIdx.x * 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, kq = lane >> 4;
+    const int nrow = blockIdx.y * 64 + 16 * wave + col;
+    const bool nok = nrow < N;
+    const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * rowb;
+    uint4 hdr[NSB];
+    uint2 qb[NSTEP];
+#pragma unroll
+    for (int b = 0; b < NSB; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)b * 144);
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s, kq));
+    // 32 rows x KK fp32 -> fp16 LDS (8 values per piece)
+    constexpr int RQ = KK / 8;
+    for (int e = tid; e < 32 * RQ; e += 256) {
+        const int r = e / RQ, c = e - r * RQ;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (m0 + r < M) {
+            const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK + 8 * c);
+            a = src[0];
+            b = src[1];
+        }
+        sk_f16x8 h;
+        h[0] = (_Float16)a.x; h[1] = (_Float16)a.y; h[2] = (_Float16)a.z; h[3] = (_Float16)a.w;
+        h[4] = (_Float16)b.x; h[5] = (_Float16)b.y; h[6] = (_Float16)b.z; h[7] = (_Float16)b.w;
+        *(sk_f16x8*)(sA + r * SA + 8 * c) = h;
+    }
+    __syncthreads();
+    typedef float f32x4k __attribute__((ext_vector_type(4)));
+    f32x4k acc[2] = {f32x4k{0.f, 0.f, 0.f, 0.f}, f32x4k{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+        const sk_f16x8 bv = sk_q4k_bfrag(hdr[s >> 3], qb[s], s & 7, nok);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const sk_f16x8 av = *(const sk_f16x8*)(sA + (16 * h + col) * SA + 32 * s + 8 * kq);
+            acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
+        }
+    }
+    if (!nok) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + 16 * h + 4 * kq + j;
+            if (m < M) {
+                float* yp = Y + (size_t)m * N + nrow;
+                *yp = accumulate ? *yp + acc[h][j] : acc[h][j];
+            }
+        }
+}
+
+// Returns 1 if the skinny path took the product (Q4_K, K 256 / 512 / 1024, M <= 256).
+static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate,
+                       int* rc) {
+    if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
+    const dim3 grid(cdiv(M, 32), cdiv(N, 64));
+    const uint8_t* wb = (const uint8_t*)w;
+    if (K == 256) hipLaunchKernelGGL(k_gemm_skinny<256>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    else if (K == 512) hipLaunchKernelGGL(k_gemm_skinny<512>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    else hipLaunchKernelGGL(k_gemm_skinny<1024>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    GH_LAUNCHED("k_gemm_skinny");
+    *rc = GH_OK;
+    return 1;
+}
+
 // y = x W^T, or y += x W^T with `accumulate` (the split-K sum adds in place; the other paths
 // write a temporary that one more launch adds)
 template <int KIND>
@@ -630,7 +709,11 @@ int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, 
     if ((kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
         switch (kind) {
             case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb, accumulate);
-            case 3: return gemm2_launch<3>(x, w, y, M, K, N, rowb, accumulate);
+            case 3: {
+                int rc = GH_OK;
+                if (gemm_skinny(x, w, y, M, K, N, rowb, accumulate, &rc)) return rc;
+                return gemm2_launch<3>(x, w, y, M, K, N, rowb, accumulate);
+            }
             default: return gemm2_launch<4>(x, w, y, M, K, N, rowb, accumulate);
         }
     }

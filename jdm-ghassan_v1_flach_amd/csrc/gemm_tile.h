@@ -234,6 +234,39 @@ __device__ __forceinline__ void decode16(const WLoad<KIND>& wl, uint16_t* dst, u
 }
 
 
+// Skinny-GEMM B operand: 8 weights (values 8 kq .. 8 kq + 7 of sub-block `sub`) of a Q4_K
+// row as fp16, from the super-block header hd and the 8 nibble bytes q (low nibbles for an
+// even sub-block, high for an odd one): d sc q - dmin m in fp32, rounded to fp16 (zero when
+// !ok). Lane layout of v_mfma_f32_16x16x32_f16's B operand.
+typedef _Float16 sk_f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ sk_f16x8 sk_q4k_bfrag(uint4 hd, uint2 q, int sub, bool ok) {
+    const uint32_t sc4[3] = {hd.y, hd.z, hd.w};
+    auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
+    int scv, mv;
+    if (sub < 4) {
+        scv = scb(sub) & 63;
+        mv = scb(sub + 4) & 63;
+    } else {
+        scv = (scb(sub + 4) & 0xF) | ((scb(sub - 4) >> 6) << 4);
+        mv = (scb(sub + 4) >> 4) | ((scb(sub) >> 6) << 4);
+    }
+    const float d1 = f16_to_f32((uint16_t)(hd.x & 0xFFFF)) * (float)scv;
+    const float m1 = f16_to_f32((uint16_t)(hd.x >> 16)) * (float)mv;
+    const int sh = 4 * (sub & 1);
+    const uint32_t q2[2] = {q.x, q.y};
+    sk_f16x8 bv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float qq = (float)((q2[i >> 2] >> (8 * (i & 3) + sh)) & 0xF);
+        bv[i] = (_Float16)(ok ? d1 * qq - m1 : 0.f);
+    }
+    return bv;
+}
+// byte offset, within a Q4_K row, of the 8 nibble bytes of k-step s (32 values) for lane group kq
+__device__ __forceinline__ size_t sk_q4k_qofs(int s, int kq) {
+    return (size_t)(s >> 3) * 144 + 16 + 32 * ((s & 7) >> 1) + 8 * kq;
+}
+
 // fp32 -> fp16 copy of n values (n a multiple of 4), on the backend stream
 int launch_to_f16(const float* x, uint16_t* y, int64_t n);
 

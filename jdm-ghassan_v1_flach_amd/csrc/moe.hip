@@ -987,7 +987,7 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 // l % 16, values 8 (l / 16) .. +7 of the k-step, one sub-block of one super-block).
 // Weights are rounded to fp16 after dequantisation (d sc q - dmin m in fp32),
 // as in the 128-row kernel.
-typedef _Float16 f16x8s __attribute__((ext_vector_type(8)));
+typedef sk_f16x8 f16x8s;
 typedef float f32x4s __attribute__((ext_vector_type(4)));
 template <bool DUAL, int KK>
 __global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
@@ -1016,8 +1016,7 @@ __global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
     for (int b = 0; b < NSB; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)b * 144);
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
-        const int sb = s >> 3, sub = s & 7;
-        qb[s] = *(const uint2*)(wrow + (size_t)sb * 144 + 16 + 32 * (sub >> 1) + 8 * kq);
+        qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s, kq));
     }
     // the 32 activation rows (grouped positions m0 .. m0+31) into LDS
     const int rq = K / 8;  // 16-byte pieces per row
@@ -1036,29 +1035,7 @@ __global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
     for (int h = 0; h < 2; ++h) acc[h] = f32x4s{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
-        const int sb = s >> 3, sub = s & 7;
-        // scale / min of sub-block `sub` (6-bit packed, as WLoad<3>)
-        const uint4 hd = hdr[sb];
-        const uint32_t sc4[3] = {hd.y, hd.z, hd.w};
-        auto scb = [&](int i) { return (int)((sc4[i >> 2] >> (8 * (i & 3))) & 0xFF); };
-        int scv, mv;
-        if (sub < 4) {
-            scv = scb(sub) & 63;
-            mv = scb(sub + 4) & 63;
-        } else {
-            scv = (scb(sub + 4) & 0xF) | ((scb(sub - 4) >> 6) << 4);
-            mv = (scb(sub + 4) >> 4) | ((scb(sub) >> 6) << 4);
-        }
-        const float d1 = f16_to_f32((uint16_t)(hd.x & 0xFFFF)) * (float)scv;
-        const float m1 = f16_to_f32((uint16_t)(hd.x >> 16)) * (float)mv;
-        const int sh = 4 * (sub & 1);  // low nibbles: even sub-block, high: odd
-        const uint32_t q2[2] = {qb[s].x, qb[s].y};
-        f16x8s bv;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float qq = (float)((q2[i >> 2] >> (8 * (i & 3) + sh)) & 0xF);
-            bv[i] = (_Float16)(nok ? d1 * qq - m1 : 0.f);
-        }
+        const f16x8s bv = sk_q4k_bfrag(hdr[s >> 3], qb[s], s & 7, nok);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const f16x8s av = *(const f16x8s*)(sA + (16 * h + (lane & 15)) * SA + 32 * s + 8 * kq);
