@@ -554,29 +554,36 @@ __global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int
 // rows of x (fp32, converted to fp16 while staged into LDS) and 64 weight rows over
 // the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the
 // first multiply (one memory wait per block instead of one per K step, and no split-K
-// partials to add), wave w owns weight rows 16w..16w+15 (v_mfma_f32_16x16x32_f16,
-// activations as A in two 16-row halves). Each output is written (or added, with
-// `accumulate`) by exactly one lane.
-template <int KK>
-__global__ void __launch_bounds__(256) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
-                                                     float* __restrict__ Y, int M, int N, size_t rowb,
-                                                     int accumulate) {
-    constexpr int SA = KK + 8, NSTEP = KK / 32, NSB = KK / 256;
+// partials to add), wave w owns weight rows 16(w%4)..+15 over K range w/4 of NWK
+// (v_mfma_f32_16x16x32_f16, activations as A in two 16-row halves). Each output is
+// written (or added, with `accumulate`) by exactly one lane.
+template <int KK, int NWK>
+__global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
+                                                           float* __restrict__ Y, int M, int N, size_t rowb,
+                                                           int accumulate) {
+    // NWK wave groups split K: group kg takes k-steps kg*NS .. kg*NS + NS - 1; the groups'
+    // sums meet in LDS and group 0 adds them in group order
+    constexpr int SA = KK + 8, NS = KK / 32 / NWK;
     __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
+    __shared__ float sR[NWK > 1 ? (NWK - 1) * 4 * 64 * 8 : 1];
     const int m0 = blockIdx.x * 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, kg = wave >> 2;
     const int col = lane & 15, kq = lane >> 4;
-    const int nrow = blockIdx.y * 64 + 16 * wave + col;
+    const int nrow = blockIdx.y * 64 + 16 * wr + col;
     const bool nok = nrow < N;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * rowb;
-    uint4 hdr[NSB];
-    uint2 qb[NSTEP];
+    const int s0 = kg * NS;
+    // every weight byte of the lane, requested first (headers of the super-blocks it touches)
+    constexpr int NH = NS >= 8 ? NS / 8 : 1;
+    uint4 hdr[NH];
+    uint2 qb[NS];
 #pragma unroll
-    for (int b = 0; b < NSB; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)b * 144);
+    for (int b = 0; b < NH; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)((s0 >> 3) + b) * 144);
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s, kq));
+    for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
     // 32 rows x KK fp32 -> fp16 LDS (8 values per piece)
     constexpr int RQ = KK / 8;
-    for (int e = tid; e < 32 * RQ; e += 256) {
+    for (int e = tid; e < 32 * RQ; e += 256 * NWK) {
         const int r = e / RQ, c = e - r * RQ;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
         if (m0 + r < M) {
@@ -593,12 +600,32 @@ __global__ void __launch_bounds__(256) k_gemm_skinny(const float* __restrict__ X
     typedef float f32x4k __attribute__((ext_vector_type(4)));
     f32x4k acc[2] = {f32x4k{0.f, 0.f, 0.f, 0.f}, f32x4k{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-        const sk_f16x8 bv = sk_q4k_bfrag(hdr[s >> 3], qb[s], s & 7, nok);
+    for (int s = 0; s < NS; ++s) {
+        const int sg = s0 + s;
+        const sk_f16x8 bv = sk_q4k_bfrag(hdr[NS >= 8 ? s >> 3 : 0], qb[s], sg & 7, nok);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const sk_f16x8 av = *(const sk_f16x8*)(sA + (16 * h + col) * SA + 32 * s + 8 * kq);
+            const sk_f16x8 av = *(const sk_f16x8*)(sA + (16 * h + col) * SA + 32 * sg + 8 * kq);
             acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
+        }
+    }
+    if constexpr (NWK > 1) {
+        if (kg > 0) {
+            float* r = sR + (((kg - 1) * 4 + wr) * 64 + lane) * 8;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) r[4 * h + j] = acc[h][j];
+        }
+        __syncthreads();
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < NWK; ++g) {
+            const float* r = sR + (((g - 1) * 4 + wr) * 64 + lane) * 8;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[h][j] += r[4 * h + j];
         }
     }
     if (!nok) return;
@@ -620,9 +647,12 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
     if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
     const dim3 grid(cdiv(M, 32), cdiv(N, 64));
     const uint8_t* wb = (const uint8_t*)w;
-    if (K == 256) hipLaunchKernelGGL(k_gemm_skinny<256>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
-    else if (K == 512) hipLaunchKernelGGL(k_gemm_skinny<512>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
-    else hipLaunchKernelGGL(k_gemm_skinny<1024>, grid, dim3(256), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    if (K == 256)
+        hipLaunchKernelGGL((k_gemm_skinny<256, 2>), grid, dim3(512), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    else if (K == 512)
+        hipLaunchKernelGGL((k_gemm_skinny<512, 2>), grid, dim3(512), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    else
+        hipLaunchKernelGGL((k_gemm_skinny<1024, 4>), grid, dim3(1024), 0, stream(), x, wb, y, M, N, rowb, accumulate);
     GH_LAUNCHED("k_gemm_skinny");
     *rc = GH_OK;
     return 1;
