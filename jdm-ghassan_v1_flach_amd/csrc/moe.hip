@@ -990,37 +990,37 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 typedef sk_f16x8 f16x8s;
 typedef float f32x4s __attribute__((ext_vector_type(4)));
 template <bool DUAL, int KK>
-__global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
+__global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P) {
+    // two wave groups split K (steps kg*NS ..); group 1's sums meet group 0's in LDS
     constexpr int SA = KK + 8;  // LDS row stride (fp16)
-    constexpr int NSTEP = KK / 32, NSB = KK / 256;
+    constexpr int NS = KK / 32 / 2;
     __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
     __shared__ float sU[DUAL ? 32 * 33 : 1];
+    __shared__ float sR[4 * 64 * 8];
     const int tile = blockIdx.x;
     if (tile >= P.tiles[0]) return;
     const int g = P.tiles[1 + 2 * tile], m0 = P.tiles[2 + 2 * tile];
     const int mend = P.offsets[g + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 3, kg = wave >> 2;
     constexpr int K = KK;
     // weight row of this lane: DUAL waves 0-1 gate, 2-3 up rows of outputs n0 .. n0+31
     const int NT = DUAL ? 32 : 64;
     const int n0 = blockIdx.y * NT;
     const int col = lane & 15, kq = lane >> 4;
-    const int nrow = DUAL ? n0 + 16 * (wave & 1) + col : n0 + 16 * wave + col;
+    const int nrow = DUAL ? n0 + 16 * (wr & 1) + col : n0 + 16 * wr + col;
     const bool nok = nrow < P.N;
-    const uint8_t* W = (DUAL && wave >= 2 ? P.W1 : P.W0) + (size_t)g * P.gstride;
+    const uint8_t* W = (DUAL && wr >= 2 ? P.W1 : P.W0) + (size_t)g * P.gstride;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * P.rowb;
+    const int s0 = kg * NS;
     // every weight byte of the lane, requested first
-    uint4 hdr[NSB];
-    uint2 qb[NSTEP];
+    uint4 hdr = *(const uint4*)(wrow + (size_t)(s0 >> 3) * 144);
+    uint2 qb[NS];
 #pragma unroll
-    for (int b = 0; b < NSB; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)b * 144);
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-        qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s, kq));
-    }
+    for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
     // the 32 activation rows (grouped positions m0 .. m0+31) into LDS
     const int rq = K / 8;  // 16-byte pieces per row
-    for (int e = tid; e < 32 * rq; e += 256) {
+    for (int e = tid; e < 32 * rq; e += 512) {
         const int r = e / rq, c = e - r * rq, m = m0 + r;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
         if (m < mend) {
@@ -1034,37 +1034,52 @@ __global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) acc[h] = f32x4s{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-        const f16x8s bv = sk_q4k_bfrag(hdr[s >> 3], qb[s], s & 7, nok);
+    for (int s = 0; s < NS; ++s) {
+        const f16x8s bv = sk_q4k_bfrag(hdr, qb[s], (s0 + s) & 7, nok);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const f16x8s av = *(const f16x8s*)(sA + (16 * h + (lane & 15)) * SA + 32 * s + 8 * kq);
+            const f16x8s av = *(const f16x8s*)(sA + (16 * h + (lane & 15)) * SA + 32 * (s0 + s) + 8 * kq);
             acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
         }
     }
-    // acc[h][j]: row 16 h + 4 (lane / 16) + j, weight row column lane % 16
+    if (kg == 1) {
+        float* r = sR + (wr * 64 + lane) * 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[4 * h + j] = acc[h][j];
+    }
+    __syncthreads();
+    if (kg == 0) {
+        const float* r = sR + (wr * 64 + lane) * 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[h][j] += r[4 * h + j];
+    }
+    // acc[h][j] of waves 0-3: row 16 h + 4 (lane / 16) + j, weight row column lane % 16
     if (DUAL) {
-        if (wave >= 2) {
+        if (kg == 0 && wr >= 2) {
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) sU[(16 * h + 4 * kq + j) * 33 + 16 * (wave & 1) + col] = acc[h][j];
+                for (int j = 0; j < 4; ++j) sU[(16 * h + 4 * kq + j) * 33 + 16 * (wr & 1) + col] = acc[h][j];
         }
         __syncthreads();
-        if (wave < 2) {
-            const int oc = n0 + 16 * wave + col;
+        if (kg == 0 && wr < 2) {
+            const int oc = n0 + 16 * wr + col;
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int r = 16 * h + 4 * kq + j, m = m0 + r;
                     if (m < mend && oc < P.N) {
-                        const float gv = acc[h][j], uv = sU[r * 33 + 16 * wave + col];
+                        const float gv = acc[h][j], uv = sU[r * 33 + 16 * wr + col];
                         P.out16[(size_t)m * P.N + oc] = f32_to_f16(gv / (1.0f + expf(-gv)) * uv);
                     }
                 }
         }
-    } else {
+    } else if (kg == 0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -1079,8 +1094,8 @@ __global__ void __launch_bounds__(256) k_moe_skinny_q4k(GroupGemm P) {
 template <bool DUAL>
 static void launch_skinny(const GroupGemm& P, int ntiles) {
     const dim3 grid(ntiles, DUAL ? P.N / 32 : cdiv(P.N, 64));
-    if (P.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(256), 0, stream(), P);
-    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(256), 0, stream(), P);
+    if (P.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(512), 0, stream(), P);
+    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(512), 0, stream(), P);
 }
 
 // tile table of one group covering rows [0, N)
