@@ -357,8 +357,57 @@ __global__ void __launch_bounds__(256) k_perm_scatter(const int32_t* __restrict_
     }
 }
 
+// The three passes in one block when every slot fits one chunk (S <= 256).
+__global__ void __launch_bounds__(256) k_perm_small(const int32_t* __restrict__ idx, int S, int ne,
+                                                    int32_t* __restrict__ grouped, int32_t* __restrict__ offsets,
+                                                    int32_t* __restrict__ pos_of_slot, int32_t* __restrict__ tiles,
+                                                    int bm) {
+    __shared__ int wc[4 * 64];
+    __shared__ int offs[65];
+    int e_l, rank;
+    chunk_ranks(idx, S, ne, 0, wc, e_l, rank);
+    if (threadIdx.x < 64) {
+        const int e = threadIdx.x;
+        const int tot = e < ne ? wc[e] + wc[64 + e] + wc[128 + e] + wc[192 + e] : 0;
+        int incl = tot;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (e >= o) incl += v;
+        }
+        if (e < ne) offs[e] = incl - tot;
+        if (e == 0) offs[ne] = S;
+    }
+    __syncthreads();
+    const int s = threadIdx.x;
+    if (s < S) {
+        const int wave = threadIdx.x >> 6;
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += wc[w * 64 + e_l];
+        const int pos = offs[e_l] + before + rank;
+        grouped[pos] = s;
+        if (pos_of_slot) pos_of_slot[s] = pos;
+    }
+    for (int i = threadIdx.x; i <= ne; i += 256) offsets[i] = offs[i];
+    if (threadIdx.x == 0 && tiles) {
+        int nt = 0;
+        for (int g = 0; g < ne; ++g)
+            for (int m0 = offs[g]; m0 < offs[g + 1]; m0 += bm) {
+                tiles[1 + 2 * nt] = g;
+                tiles[2 + 2 * nt] = m0;
+                ++nt;
+            }
+        tiles[0] = nt;
+    }
+}
+
 static int permute(const int32_t* idx, int S, int ne, int32_t* grouped, int32_t* offsets, int32_t* pos_of_slot,
                    int32_t* tiles, int bm) {
+    if (S <= PERM_CHUNK) {
+        hipLaunchKernelGGL(k_perm_small, dim3(1), dim3(256), 0, stream(), idx, S, ne, grouped, offsets, pos_of_slot,
+                           tiles, bm);
+        GH_LAUNCHED("k_perm_small");
+        return GH_OK;
+    }
     const int nch = cdiv(S > 0 ? S : 1, PERM_CHUNK);
     if (nch > PERM_MAX_CHUNKS) return fail(GH_EUNSUPPORTED, "moe permute: %d slots (max %d)", S, PERM_CHUNK * PERM_MAX_CHUNKS);
     int32_t* counts = (int32_t*)workspace(WS_MOE_PERM, (size_t)nch * ne * 4);
@@ -738,6 +787,15 @@ struct GroupGemm {
     float* out;                // [rows][N], row = grouped position
     const uint16_t* A16;       // v2: fp16 activations (instead of A)
     uint16_t* out16;           // v2 DUAL: fp16 SwiGLU output (instead of out)
+    int rows;                  // skinny kernel without a tile table: one group of `rows` rows
+    // skinny non-DUAL epilogue = the ordered combine (k_moe_combine's arithmetic): this product
+    // is the shared expert's down projection; out row t = [cout +] (shared + sum_k cw[t K + k]
+    // cy[cpos[t K + k]]), k in order
+    const float* cy;
+    const int32_t* cpos;
+    const float* cw;
+    int cK, caccum;
+    float* cout;
 };
 
 template <int KIND, bool DUAL>
@@ -990,23 +1048,29 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 typedef sk_f16x8 f16x8s;
 typedef float f32x4s __attribute__((ext_vector_type(4)));
 template <bool DUAL, int KK>
-__global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P) {
+__global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm P1, int ntiles0) {
+    // blocks [0, ntiles0) take problem P0, the rest problem P1 (the shared expert beside the
+    // routed ones in one launch)
+    const bool second = (int)blockIdx.x >= ntiles0;
+    const GroupGemm& P = second ? P1 : P0;
     // two wave groups split K (steps kg*NS ..); group 1's sums meet group 0's in LDS
     constexpr int SA = KK + 8;  // LDS row stride (fp16)
     constexpr int NS = KK / 32 / 2;
     __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
     __shared__ float sU[DUAL ? 32 * 33 : 1];
     __shared__ float sR[4 * 64 * 8];
-    const int tile = blockIdx.x;
-    if (tile >= P.tiles[0]) return;
-    const int g = P.tiles[1 + 2 * tile], m0 = P.tiles[2 + 2 * tile];
-    const int mend = P.offsets[g + 1];
+    const int tile = second ? (int)blockIdx.x - ntiles0 : (int)blockIdx.x;
+    const bool table = P.tiles != nullptr;
+    if (table && tile >= P.tiles[0]) return;
+    const int g = table ? P.tiles[1 + 2 * tile] : 0, m0 = table ? P.tiles[2 + 2 * tile] : 32 * tile;
+    const int mend = table ? P.offsets[g + 1] : P.rows;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave & 3, kg = wave >> 2;
     constexpr int K = KK;
     // weight row of this lane: DUAL waves 0-1 gate, 2-3 up rows of outputs n0 .. n0+31
     const int NT = DUAL ? 32 : 64;
     const int n0 = blockIdx.y * NT;
+    if (n0 >= P.N) return;  // the other problem's output range is wider
     const int col = lane & 15, kq = lane >> 4;
     const int nrow = DUAL ? n0 + 16 * (wr & 1) + col : n0 + 16 * wr + col;
     const bool nok = nrow < P.N;
@@ -1085,17 +1149,32 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int m = m0 + 16 * h + 4 * kq + j;
-                if (m < mend && nok) P.out[(size_t)m * P.N + nrow] = acc[h][j];
+                if (m < mend && nok) {
+                    if (P.cout) {  // the ordered combine of token m, output nrow
+                        float v = acc[h][j];
+                        for (int k = 0; k < P.cK; ++k) {
+                            const int sl = m * P.cK + k;
+                            v += P.cw[sl] * P.cy[(size_t)P.cpos[sl] * P.N + nrow];
+                        }
+                        float* o = P.cout + (size_t)m * P.N + nrow;
+                        *o = P.caccum ? *o + v : v;
+                    } else {
+                        P.out[(size_t)m * P.N + nrow] = acc[h][j];
+                    }
+                }
             }
     }
 }
 
 // the skinny kernel for K = 256 or 512 (the caller checks K); grid (tiles, outputs / 32 or 64)
+// P1 (optional, ntiles1 blocks) runs in the same launch after P0's ntiles0; both take the same K
 template <bool DUAL>
-static void launch_skinny(const GroupGemm& P, int ntiles) {
-    const dim3 grid(ntiles, DUAL ? P.N / 32 : cdiv(P.N, 64));
-    if (P.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(512), 0, stream(), P);
-    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(512), 0, stream(), P);
+static void launch_skinny(const GroupGemm& P0, int ntiles0, const GroupGemm* P1 = nullptr, int ntiles1 = 0) {
+    const int nw = std::max(P0.N, P1 ? P1->N : 0);
+    const dim3 grid(ntiles0 + ntiles1, DUAL ? cdiv(nw, 32) : cdiv(nw, 64));
+    const GroupGemm Q1 = P1 ? *P1 : GroupGemm{};
+    if (P0.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
+    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
 }
 
 // tile table of one group covering rows [0, N)
@@ -1205,15 +1284,39 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         P.A16 = x16; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
         P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
         P.K = d; P.N = E; P.out16 = act16;
-        if (skinny) launch_skinny<true>(P, max_tiles);
-        else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
-        GH_LAUNCHED("k_moe_group_gemm2(gate/up)");
         GroupGemm Q{};
         Q.A16 = act16; Q.lda = E; Q.gather = nullptr; Q.topk = 1; Q.tiles = tiles; Q.offsets = offsets;
         Q.W0 = (const uint8_t*)downs; Q.gstride = (size_t)d * rowb_E; Q.rowb = rowb_E; Q.K = E; Q.N = d; Q.out = yr;
-        if (skinny) launch_skinny<false>(Q, max_tiles);
-        else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
-        GH_LAUNCHED("k_moe_group_gemm2(down)");
+        if (skinny) {
+            // gate/up of the routed experts and of the shared expert (one group of N rows, no tile
+            // table) in one launch; the routed downs; the shared down with the ordered combine
+            // (and the residual add) in its epilogue
+            GroupGemm R{};
+            R.A16 = x16; R.lda = d; R.topk = 1; R.rows = N;
+            R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.rowb = rowb_d; R.K = d; R.N = SH;
+            R.out16 = sh_act16;
+            launch_skinny<true>(P, max_tiles, has_sh ? &R : nullptr, has_sh ? cdiv(N, 32) : 0);
+            GH_LAUNCHED("k_moe_skinny_q4k(gate/up)");
+            launch_skinny<false>(Q, max_tiles);
+            GH_LAUNCHED("k_moe_skinny_q4k(down)");
+            if (has_sh) {
+                float* cdst = out;
+                int cacc = 0;
+                combine_target(acc_dst, added, cdst, cacc);
+                GroupGemm U{};
+                U.A16 = sh_act16; U.lda = SH; U.topk = 1; U.rows = N;
+                U.W0 = (const uint8_t*)sh_d; U.rowb = rowb_SH; U.K = SH; U.N = d;
+                U.cy = yr; U.cpos = pos; U.cw = w_route; U.cK = K; U.caccum = cacc; U.cout = cdst;
+                launch_skinny<false>(U, cdiv(N, 32));
+                GH_LAUNCHED("k_moe_skinny_q4k(shared down + combine)");
+                return GH_OK;
+            }
+        } else {
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(max_tiles, cdiv(E, 64)), dim3(256), 0, stream(), P);
+            GH_LAUNCHED("k_moe_group_gemm2(gate/up)");
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(max_tiles, cdiv(d, BN)), dim3(256), 0, stream(), Q);
+            GH_LAUNCHED("k_moe_group_gemm2(down)");
+        }
         if (has_sh) {
             int32_t* sh_tiles = (int32_t*)workspace(WS_MOE_H, ((size_t)2 * (N / bm + 2) + 1 + 2) * 4);
             if (!sh_tiles) return fail(GH_ENOMEM, "moe: workspace");
@@ -1225,13 +1328,11 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             R.A16 = x16; R.lda = d; R.gather = nullptr; R.topk = 1; R.tiles = sh_tiles; R.offsets = sh_off;
             R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.gstride = 0; R.rowb = rowb_d;
             R.K = d; R.N = SH; R.out16 = sh_act16;
-            if (skinny) launch_skinny<true>(R, nt);
-            else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, true>), dim3(nt, cdiv(SH, 64)), dim3(256), 0, stream(), R);
             GroupGemm U{};
             U.A16 = sh_act16; U.lda = SH; U.gather = nullptr; U.topk = 1; U.tiles = sh_tiles; U.offsets = sh_off;
             U.W0 = (const uint8_t*)sh_d; U.gstride = 0; U.rowb = rowb_SH; U.K = SH; U.N = d; U.out = sh_y;
-            if (skinny) launch_skinny<false>(U, nt);
-            else hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
+            hipLaunchKernelGGL((k_moe_group_gemm2<KIND, false>), dim3(nt, cdiv(d, BN)), dim3(256), 0, stream(), U);
             GH_LAUNCHED("k_moe_group_gemm2(shared)");
         }
         {
