@@ -1089,7 +1089,16 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
         if (m < mend) {
             const int arow = P.gather ? P.gather[m] / P.topk : m;
-            v = *(const uint4*)(P.A16 + (size_t)arow * P.lda + 8 * c);
+            if (P.A16) {
+                v = *(const uint4*)(P.A16 + (size_t)arow * P.lda + 8 * c);
+            } else {  // fp32 rows, converted here
+                const float4* src = (const float4*)(P.A + (size_t)arow * P.lda + 8 * c);
+                const float4 a = src[0], b = src[1];
+                f16x8s hv;
+                hv[0] = (_Float16)a.x; hv[1] = (_Float16)a.y; hv[2] = (_Float16)a.z; hv[3] = (_Float16)a.w;
+                hv[4] = (_Float16)b.x; hv[5] = (_Float16)b.y; hv[6] = (_Float16)b.z; hv[7] = (_Float16)b.w;
+                v = __builtin_bit_cast(uint4, hv);
+            }
         }
         *(uint4*)(sA + r * SA + 8 * c) = v;
     }
@@ -1278,10 +1287,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
         if (!x16) return fail(GH_ENOMEM, "moe: workspace");
         uint16_t* act16 = (uint16_t*)act;         // [S][E] fp16 in the fp32 buffer
         uint16_t* sh_act16 = (uint16_t*)sh_act;   // [N][SH] fp16
-        rc = launch_to_f16(x, x16, (int64_t)N * d);
-        if (rc) return rc;
+        if (!skinny) {  // the skinny gate/up converts its fp32 rows itself
+            rc = launch_to_f16(x, x16, (int64_t)N * d);
+            if (rc) return rc;
+        }
         GroupGemm P{};
-        P.A16 = x16; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles; P.offsets = offsets;
+        P.A16 = skinny ? nullptr : x16; P.A = x; P.lda = d; P.gather = grouped; P.topk = K; P.tiles = tiles;
+        P.offsets = offsets;
         P.W0 = (const uint8_t*)gates; P.W1 = (const uint8_t*)ups; P.gstride = (size_t)E * rowb_d; P.rowb = rowb_d;
         P.K = d; P.N = E; P.out16 = act16;
         GroupGemm Q{};
@@ -1292,7 +1304,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             // table) in one launch; the routed downs; the shared down with the ordered combine
             // (and the residual add) in its epilogue
             GroupGemm R{};
-            R.A16 = x16; R.lda = d; R.topk = 1; R.rows = N;
+            R.A = x; R.lda = d; R.topk = 1; R.rows = N;
             R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.rowb = rowb_d; R.K = d; R.N = SH;
             R.out16 = sh_act16;
             launch_skinny<true>(P, max_tiles, has_sh ? &R : nullptr, has_sh ? cdiv(N, 32) : 0);
