@@ -33,9 +33,11 @@ __device__ __forceinline__ float softplus_ref(float v) {
 // ================================================================ conv1d
 // out[t][c] = silu(b_c + sum_j w[c][j] * raw[t-(k-1)+j][c]), raw = the bc
 // part of the projection; the window starts at zero for every sequence
-// (core/mamba_cpu.cpp:70-118). Every (t, c) is independent.
+// (core/mamba_cpu.cpp:70-118). Every (t, c) is independent. With `win` (one sequence) the
+// threads of the last row also leave the conv window for decode: the last k-1 raw rows.
 __global__ void k_conv1d(const float* __restrict__ proj, int proj_ld, int col0, const float* __restrict__ w,
-                         const float* __restrict__ b, float* __restrict__ out, int B, int T, int C, int k) {
+                         const float* __restrict__ b, float* __restrict__ out, int B, int T, int C, int k,
+                         float* __restrict__ win) {
 #pragma clang fp contract(off)
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int row = blockIdx.y;  // b*T + t
@@ -48,6 +50,13 @@ __global__ void k_conv1d(const float* __restrict__ proj, int proj_ld, int col0, 
         acc += w[(size_t)c * k + j] * v;
     }
     out[(size_t)row * C + c] = acc / (1.0f + expf(-acc));
+    if (win && row == T - 1) {
+        const int wl = k > 1 ? k - 1 : 1;
+        for (int j = 0; j < wl; ++j) {
+            const int tw = T - wl + j;
+            win[(size_t)c * wl + j] = tw >= 0 ? proj[(size_t)tw * proj_ld + col0 + c] : 0.f;
+        }
+    }
 }
 
 // dt = softplus(dt_raw + dt_bias), A = -exp(A_log), and the chunk-local
@@ -223,7 +232,8 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
                                                       const float* __restrict__ a_log, float* __restrict__ dt,
                                                       float* __restrict__ cum, float* __restrict__ G,
                                                       float* __restrict__ dS, float* __restrict__ decay, int T,
-                                                      int H, int L) {
+                                                      int H, int L, float* __restrict__ state,
+                                                      float* __restrict__ Sin) {
     constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
     constexpr int U_STATE = (P * S + N * S) * 2, U_CB = 2 * 64 * SN * 2;
     __shared__ __attribute__((aligned(16))) unsigned char smem[U_STATE > U_CB ? U_STATE : U_CB];
@@ -289,6 +299,9 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
         }
     }
     float* out = dS + ((size_t)c * H + h) * P * N;
+    // one chunk (state != null): the inter-chunk pass of this head right here, k_ssd_state_pass's
+    // arithmetic: S_in = state, state = state * decay + dS
+    const float dec = expf(cend);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
         const int tile = wave * TPW + i;
@@ -297,10 +310,17 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
         for (int e = 0; e < 16; ++e) {
             const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
             const int n = nt * 32 + (lane & 31);
-            out[(size_t)p * N + n] = acc[i][e];
+            if (state) {
+                const size_t si = ((size_t)h * P + p) * N + n;
+                const float s0 = state[si];
+                Sin[si] = s0;
+                state[si] = s0 * dec + acc[i][e];
+            } else {
+                out[(size_t)p * N + n] = acc[i][e];
+            }
         }
     }
-    if (threadIdx.x == 0) decay[(size_t)c * H + h] = expf(cend);
+    if (threadIdx.x == 0) decay[(size_t)c * H + h] = dec;
 }
 
 // Inter-chunk pass: S_in[c] = state before chunk c; state <- S_in*decay + dS.
@@ -526,16 +546,18 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     float* Sin = dS + f_S;
     float* decay = Sin + f_S;
     const unsigned nb1 = (unsigned)(nch * H + nch * (L / 64) * (L / 64));  // chunk states, then G tiles
+    const bool one = nch == 1;  // a single chunk: the state pass runs in the chunk-state blocks
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_state_cb<128>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L);
+                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L, one ? state : nullptr, Sin);
     } else {
         hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L);
+                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L, one ? state : nullptr, Sin);
     }
     const int64_t nst = (int64_t)H * PN;
-    hipLaunchKernelGGL(k_ssd_state_pass, dim3((unsigned)((nst + 255) / 256)), dim3(256), 0, stream(), state, dS, decay,
-                       Sin, nch, H, (int)PN);
+    if (!one)
+        hipLaunchKernelGGL(k_ssd_state_pass, dim3((unsigned)((nst + 255) / 256)), dim3(256), 0, stream(), state, dS,
+                           decay, Sin, nch, H, (int)PN);
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_chunk_out<128>, dim3(nch, H, L / 64), dim3(256), 0, stream(), xs, ldx, Cm, ldbc, G,
                            dt, cum, Sin, D, y, ldy, T, H, L);
@@ -630,18 +652,6 @@ __global__ void __launch_bounds__(256) k_step_scan(const float* __restrict__ xbc
     if (tc == 0) y[i] = acc + D[h] * xv;
 }
 
-// conv window after a batched prefill: the last k-1 raw xBC rows
-__global__ void k_save_window(const float* __restrict__ proj, int proj_ld, int col0, float* __restrict__ win, int T,
-                              int C, int k) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
-    const int wl = k > 1 ? k - 1 : 1;
-    for (int j = 0; j < wl; ++j) {
-        const int t = T - wl + j;
-        win[(size_t)c * wl + j] = t >= 0 ? proj[(size_t)t * proj_ld + col0 + c] : 0.f;
-    }
-}
-
 // One sequence of T tokens: in_proj, conv1d (+ optionally the conv window
 // left for decode), chunked scan, gated norm, out_proj. kind 0-3 packed,
 // 4 fp16 weights.
@@ -660,13 +670,8 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
     int rc = linear_any(x, w_in, pr, T, d, proj, kind);
     if (rc) return rc;
     hipLaunchKernelGGL(k_conv1d, dim3(cdiv(conv_dim, 256), T), dim3(256), 0, stream(), pr, proj, d_inner, conv_w,
-                       conv_b, xbc, 1, T, conv_dim, k);
+                       conv_b, xbc, 1, T, conv_dim, k, conv_state);
     GH_LAUNCHED("k_conv1d");
-    if (conv_state) {
-        hipLaunchKernelGGL(k_save_window, dim3(cdiv(conv_dim, 256)), dim3(256), 0, stream(), pr, proj, d_inner,
-                           conv_state, T, conv_dim, k);
-        GH_LAUNCHED("k_save_window");
-    }
     rc = ssd_run(xbc, conv_dim, xbc + d_inner, xbc + d_inner + d_state, conv_dim, pr + d_inner + conv_dim, proj,
                  dt_bias, nullptr, a_log, D, state, yb, d_inner, T, n_heads, d_head, d_state, 256);
     if (rc) return rc;
