@@ -1082,6 +1082,24 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
     uint2 qb[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
+    // combine epilogue: the rows' slot positions and weights (up to top-2 here), requested now
+    constexpr int CKM = 2;
+    int cp[2][4][CKM];
+    float cwv[2][4][CKM];
+    const bool comb = !DUAL && P.cout && P.cK <= CKM && kg == 0;
+    if (comb) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int k = 0; k < CKM; ++k) {
+                    const int m = m0 + 16 * h + 4 * kq + j;
+                    const bool ok = m < mend && k < P.cK;
+                    cp[h][j][k] = ok ? P.cpos[m * P.cK + k] : 0;
+                    cwv[h][j][k] = ok ? P.cw[m * P.cK + k] : 0.f;
+                }
+    }
     // the 32 activation rows (grouped positions m0 .. m0+31) into LDS
     const int rq = K / 8;  // 16-byte pieces per row
     for (int e = tid; e < 32 * rq; e += 512) {
@@ -1159,7 +1177,14 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
             for (int j = 0; j < 4; ++j) {
                 const int m = m0 + 16 * h + 4 * kq + j;
                 if (m < mend && nok) {
-                    if (P.cout) {  // the ordered combine of token m, output nrow
+                    if (comb) {  // the ordered combine of token m, output nrow
+                        float v = acc[h][j];
+#pragma unroll
+                        for (int k = 0; k < CKM; ++k)
+                            if (k < P.cK) v += cwv[h][j][k] * P.cy[(size_t)cp[h][j][k] * P.N + nrow];
+                        float* o = P.cout + (size_t)m * P.N + nrow;
+                        *o = P.caccum ? *o + v : v;
+                    } else if (P.cout) {  // more than CKM experts per token
                         float v = acc[h][j];
                         for (int k = 0; k < P.cK; ++k) {
                             const int sl = m * P.cK + k;
