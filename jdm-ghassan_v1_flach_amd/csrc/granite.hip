@@ -399,7 +399,8 @@ int attn_chunk_min();
 int moe_forward_acc(const float* x, const float* router_w, const float* router_bias, const void* gates,
                     const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d,
                     float* out, float* acc_dst, int* added, float* probs_cache, int32_t* idx_cache, float* w_cache,
-                    int64_t N, int d, int E, int ne, int K, int SH, int qkind);
+                    int64_t N, int d, int E, int ne, int K, int SH, int qkind, const float* nw, float eps,
+                    float* xn);
 }
 static bool fused_supported(const gh_granite* g) {
     const int k = g->qkind;
@@ -745,13 +746,13 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
             GHC(linear_acc(g->att, g->W(pre + "wo"), g->x, P, g->qd, d, g->qkind));  // x += attn W_o^T
         }
         if (g->lt[l] == 0 && mamba_mode == 0) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
-        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, P, d, g->eps));
-        // x += moe(x): added by the combine launch when the path has one, else here
+        // x += moe(ffn_norm(x)): the norm rides on the router launch (normalised rows into xb); the
+        // residual add on the combine launch when the path has one, else here
         int added = 0;
-        GHC(moe_forward_acc(g->xb, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
+        GHC(moe_forward_acc(g->x, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
                             g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"),
                             g->W(pre + "moe_sh_down"), g->pr, g->x, &added, nullptr, nullptr, nullptr, P, d, g->E,
-                            g->ne, g->K, g->SH, g->qkind));
+                            g->ne, g->K, g->SH, g->qkind, g->F(pre + "ffn_norm"), g->eps, g->xb));
         if (!added) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
     }
     // cache length P, ring start 0 (KVCache::set_length)

@@ -1532,7 +1532,8 @@ namespace gh {
 int moe_forward_acc(const float* x, const float* router_w, const float* router_bias, const void* gates,
                     const void* ups, const void* downs, const void* sh_g, const void* sh_u, const void* sh_d,
                     float* out, float* acc_dst, int* added, float* probs_cache, int32_t* idx_cache, float* w_cache,
-                    int64_t N, int d, int E, int ne, int K, int SH, int qkind) {
+                    int64_t N, int d, int E, int ne, int K, int SH, int qkind, const float* nw, float eps,
+                    float* xn) {
     if (added) *added = 0;
     if (N <= 0) return GH_OK;
     // core/moe_cpu.cpp:207-209
@@ -1555,7 +1556,22 @@ int moe_forward_acc(const float* x, const float* router_w, const float* router_b
         if (!idx) idx = (int32_t*)r;
         if (!w) w = (float*)(r + (size_t)S * 4);
     }
-    int rc = moe_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
+    int rc;
+    if (nw) {
+        // x is the raw residual row: the norm (ffn_norm) runs inside the router launch where that
+        // path has it (k_route writes the normalised rows to xn), else as its own launch first
+        GH_REQUIRE(xn, "moe_forward: a normalised-row buffer is needed with the norm");
+        const bool fused = !(N > 8 && ne >= 16);  // the many-token logits path has no norm
+        if (fused) {
+            rc = launch_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K, nw, eps, xn);
+        } else {
+            rc = gh_rmsnorm_forward(x, nw, xn, nullptr, N, d, eps);
+            if (!rc) rc = moe_route(xn, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
+        }
+        x = xn;
+    } else {
+        rc = moe_route(x, router_w, router_bias, probs_cache, idx, w, (int)N, d, ne, K);
+    }
     if (rc) return rc;
     const int n = (int)N;
     switch (qkind) {
@@ -1595,7 +1611,7 @@ int gh_moe_forward_bias_half(const float* x, const float* router_w, const float*
     (void)s_up;
     (void)s_act;
     return moe_forward_acc(x, router_w, router_bias, gates, ups, downs, sh_g, sh_u, sh_d, out, nullptr, nullptr,
-                           probs_cache, idx_cache, w_cache, N, d, E, ne, K, SH, qkind);
+                           probs_cache, idx_cache, w_cache, N, d, E, ne, K, SH, qkind, nullptr, 0.f, nullptr);
 }
 
 }  // extern "C"
