@@ -95,6 +95,10 @@ int gh_add_inplace(float* a, const float* b, int64_t n);               /* core/o
 int gh_scale_inplace(float* a, float s, int64_t n);                    /* core/ops.h:125 */
 int gh_zero(float* a, int64_t n);                                      /* core/ops.h:126 */
 int gh_copy(float* dst, const float* src, int64_t n);                  /* core/ops.h:127 */
+/* Measurement helper, no counterpart in the reference: reads `bytes` (a multiple of 16) once with
+ * 16-byte loads from `blocks` blocks of 256 lanes and writes one XOR word per block to sink[blocks].
+ * Its time is the HBM read ceiling the weight-streaming kernels are compared with. */
+int gh_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks);
 /* core/ops.h:134 rmsnorm_forward (rrms may be NULL) */
 int gh_rmsnorm_forward(const float* x, const float* w, float* out, float* rrms, int64_t rows, int dim,
                        float eps);
@@ -239,6 +243,13 @@ int gh_rng_below_host(uint64_t seed, uint64_t bound, int32_t* out_host, int64_t 
  * fcfg: eps, attention scale. */
 typedef struct gh_granite gh_granite;
 int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_granite** out);
+/* The same with the optional Granite fields: cfg[16 + L] tie_embeddings (default 1; 0 adds an fp16
+ * "lm_head" [V, d], model/model.cpp:1160), cfg[17 + L] moe_aux_free (default 0; 1 adds fp32
+ * "layers.N.moe_bias" [ne] router biases, model/model.cpp:179-199); fcfg[2] embedding_multiplier,
+ * fcfg[3] residual_multiplier, fcfg[4] logits_scaling (default 1; inference/generator.cpp:248,
+ * 266, 440, model/model.cpp:2431, 2531). Entries past ncfg / nfcfg take their defaults. */
+int gh_granite_create_ex(const int32_t* cfg, int ncfg, const float* fcfg, int nfcfg, int max_ctx,
+                         gh_granite** out);
 int gh_granite_destroy(gh_granite* g);
 /* Parameter storage bytes by reference name (host buffer, nbytes must match). */
 int gh_granite_set_param(gh_granite* g, const char* name, const void* host, size_t nbytes);
@@ -264,6 +275,12 @@ int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host);
  * and replays it; 2 runs the whole loop as one persistent cooperative launch (falls back
  * to 1 when the model's shapes or the context do not fit that kernel). */
 int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int use_graph);
+/* When a persistent launch (use_graph 2) aborts (a bounded hand-over wait ran out), the
+ * recurrent state, KV cache and ids are partly advanced: generate returns GH_EHIP and the
+ * model refuses prefill / decode / generate until gh_granite_reset. Test hook, no reference
+ * counterpart: makes the next persistent launch start with its abort flag raised (every
+ * kernel still runs to its end), to exercise that contract. */
+int gh_granite_test_force_abort(gh_granite* g);
 
 #ifdef __cplusplus
 }

@@ -231,6 +231,10 @@ int gh_synth_param_f32(const char* name, uint64_t seed, float* out, int64_t n) {
         for (int64_t i = 0; i < n; ++i) out[i] = 1.0f;
         return GH_OK;
     }
+    if (ends("moe_bias")) {  // model/model.cpp:179-191: the aux-free router bias starts at zero
+        for (int64_t i = 0; i < n; ++i) out[i] = 0.0f;
+        return GH_OK;
+    }
     if (ends("A_log")) {  // model/model.cpp:1597-1600
         for (int64_t i = 0; i < n; ++i) out[i] = logf((float)(i + 1));
         return GH_OK;

@@ -86,11 +86,14 @@ constexpr int PD_STAGE = 4096;  // words
 // their dst (LDS). A poll moves every chunk still missing straight into the LDS staging area
 // (global_load_lds_dwordx4 with sc1: from the coherent memory side, no registers), all in
 // flight at once, then each lane checks the chunks it moved; chunks that arrived complete are
-// not requested again. Ranges start at even words (16-byte aligned); at most PD_STAGE / 2
-// chunks in all. false if the launch is aborting.
+// not requested again. Ranges start at even words (16-byte aligned). The chunks are taken in
+// windows of at most PD_STAGE / 2 (the staging area's capacity), one window after the other,
+// so any total fits. false if the launch is aborting.
 #ifdef GH_PD_TRACE
 __device__ uint32_t pd_last_spins;
 #endif
+constexpr int PD_WIN = PD_STAGE / 2;  // chunks per window
+static_assert(PD_WIN / PD_T <= 32, "the per-lane done mask holds one bit per chunk slot");
 template <int NR>
 __device__ bool pd_wait_n(const PdRange (&r)[NR], PD_G int32_t* abort, PD_L uint64_t* stage) {
     __shared__ int s_abort;
@@ -98,72 +101,77 @@ __device__ bool pd_wait_n(const PdRange (&r)[NR], PD_G int32_t* abort, PD_L uint
     int total = 0;
 #pragma unroll
     for (int q = 0; q < NR; ++q) total += (r[q].n + 1) / 2;
-    const int nj = (total + PD_T - 1) / PD_T;  // <= 8
-    uint32_t done = 0;
-    for (uint32_t spin = 0;; ++spin) {
-        // request the missing chunks: chunk c = 256 j + tid lands at stage[2 c]
-        for (int j = 0; j < nj; ++j) {
-            const int c = PD_T * j + threadIdx.x;
-            if (c < total && !((done >> j) & 1u)) {
-                int cc = c;
-                const PD_G uint64_t* g = nullptr;
+    for (int base = 0; base < total; base += PD_WIN) {
+        const int cnt = min(total - base, PD_WIN);
+        const int nj = (cnt + PD_T - 1) / PD_T;  // <= PD_WIN / PD_T
+        uint32_t done = 0;
+        for (uint32_t spin = 0;; ++spin) {
+            // request the missing chunks: chunk base + c, c = PD_T j + tid, lands at stage[2 c]
+            for (int j = 0; j < nj; ++j) {
+                const int c = PD_T * j + threadIdx.x;
+                if (c < cnt && !((done >> j) & 1u)) {
+                    int cc = base + c;
+                    const PD_G uint64_t* g = nullptr;
+#pragma unroll
+                    for (int q = 0; q < NR; ++q) {
+                        const int nq = (r[q].n + 1) / 2;
+                        if (!g && cc < nq) g = r[q].src + 2 * cc;
+                        else if (!g) cc -= nq;
+                    }
+                    const uint32_t lds = (uint32_t)(uintptr_t)(stage + 2 * (PD_T * j + wave_base));
+                    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g),
+                                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                                 : "memory", "m0");
+                }
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            int miss = 0;
+            for (int j = 0; j < nj; ++j) {
+                const int c = PD_T * j + threadIdx.x;
+                if (c >= cnt || ((done >> j) & 1u)) continue;
+                int cc = base + c;
+                bool found = false, ok = true;
 #pragma unroll
                 for (int q = 0; q < NR; ++q) {
                     const int nq = (r[q].n + 1) / 2;
-                    if (!g && cc < nq) g = r[q].src + 2 * cc;
-                    else if (!g) cc -= nq;
-                }
-                const uint32_t lds = (uint32_t)(uintptr_t)(stage + 2 * (PD_T * j + wave_base));
-                asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g),
-                             "s"(__builtin_amdgcn_readfirstlane(lds))
-                             : "memory");
-            }
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        int miss = 0;
-        for (int j = 0; j < nj; ++j) {
-            const int c = PD_T * j + threadIdx.x;
-            if (c >= total || ((done >> j) & 1u)) continue;
-            int cc = c;
-            bool found = false, ok = true;
-#pragma unroll
-            for (int q = 0; q < NR; ++q) {
-                const int nq = (r[q].n + 1) / 2;
-                if (!found && cc < nq) {
-                    found = true;
-                    const int k = 2 * cc;
-                    const uint64_t v0 = stage[2 * c], v1 = stage[2 * c + 1];
-                    const bool two = k + 1 < r[q].n;
-                    ok = (uint32_t)(v0 >> 32) == r[q].tag && (!two || (uint32_t)(v1 >> 32) == r[q].tag);
-                    if (ok) {
-                        r[q].dst[k] = __builtin_bit_cast(float, (uint32_t)v0);
-                        if (two) r[q].dst[k + 1] = __builtin_bit_cast(float, (uint32_t)v1);
+                    if (!found && cc < nq) {
+                        found = true;
+                        const int k = 2 * cc;
+                        const uint64_t v0 = stage[2 * c], v1 = stage[2 * c + 1];
+                        const bool two = k + 1 < r[q].n;
+                        ok = (uint32_t)(v0 >> 32) == r[q].tag && (!two || (uint32_t)(v1 >> 32) == r[q].tag);
+                        if (ok) {
+                            r[q].dst[k] = __builtin_bit_cast(float, (uint32_t)v0);
+                            if (two) r[q].dst[k + 1] = __builtin_bit_cast(float, (uint32_t)v1);
+                        }
+                    } else if (!found) {
+                        cc -= nq;
                     }
-                } else if (!found) {
-                    cc -= nq;
                 }
+                if (ok) done |= 1u << j;
+                else miss = 1;
             }
-            if (ok) done |= 1u << j;
-            else miss = 1;
-        }
-        if (!__syncthreads_or(miss)) {
+            // the barrier also keeps the next window's transfers behind every lane's reads
+            if (!__syncthreads_or(miss)) {
 #ifdef GH_PD_TRACE
-            if (threadIdx.x == 0) __hip_atomic_store(&pd_last_spins, spin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (threadIdx.x == 0) __hip_atomic_store(&pd_last_spins, spin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #endif
-            return true;
-        }
-        if (threadIdx.x == 0) {
-            int a = __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (!a && spin >= PD_SPIN) {
-                __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                a = 1;
+                break;
             }
-            s_abort = a;
+            if (threadIdx.x == 0) {
+                int a = __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (!a && spin >= PD_SPIN) {
+                    __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    a = 1;
+                }
+                s_abort = a;
+            }
+            __syncthreads();
+            if (s_abort) return false;
+            __builtin_amdgcn_s_sleep(PD_SLEEP);
         }
-        __syncthreads();
-        if (s_abort) return false;
-        __builtin_amdgcn_s_sleep(PD_SLEEP);
     }
+    return true;
 }
 __device__ bool pd_wait(const PD_G uint64_t* src, int n, uint32_t tag, PD_L float* dst, PD_G int32_t* abort,
                         PD_L uint64_t* stage) {

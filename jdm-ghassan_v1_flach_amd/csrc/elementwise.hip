@@ -26,6 +26,34 @@ __global__ void k_scale(float* a, float s, int64_t n) { GRID_STRIDE(i, n) a[i] *
 __global__ void k_fill0(float* a, int64_t n) { GRID_STRIDE(i, n) a[i] = 0.f; }
 __global__ void k_copy(float* d, const float* s, int64_t n) { GRID_STRIDE(i, n) d[i] = s[i]; }
 
+// Read-only streaming probe: every lane reads 16-byte pieces, four requests in
+// flight per lane, grid-strided so that consecutive lanes read consecutive
+// pieces; the XOR of everything read leaves one word per block (so nothing is
+// elided). The measured time of one pass is the HBM read ceiling that the
+// weight-streaming GEMVs are compared with.
+__global__ void __launch_bounds__(256) k_stream_read(const uint4* __restrict__ src, int64_t n16,
+                                                     uint32_t* __restrict__ sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = src[i];
+        const uint4 b = src[i + stride];
+        const uint4 c = src[i + 2 * stride];
+        const uint4 d = src[i + 3 * stride];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = src[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    __shared__ uint32_t red[4];
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 // core/math_cpu.cpp:522-529 (silu(g) * u)
 __global__ void k_swiglu(const float* g, const float* u, float* o, int64_t n) {
     GRID_STRIDE(i, n) {
@@ -191,6 +219,14 @@ int gh_copy(float* d, const float* s, int64_t n) {
     GH_REQUIRE(d && s, "ops::copy on null pointer");
     hipLaunchKernelGGL(k_copy, grid1d(n), dim3(256), 0, stream(), d, s, n);
     GH_LAUNCHED("k_copy");
+    return GH_OK;
+}
+int gh_stream_read(const void* src, int64_t bytes, uint32_t* sink, int blocks) {
+    GH_REQUIRE(src && sink && bytes > 0 && bytes % 16 == 0 && blocks > 0 && blocks <= 65536,
+               "stream_read: bad arguments (bytes must be a positive multiple of 16, 1 <= blocks <= 65536)");
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)blocks), dim3(256), 0, stream(), (const uint4*)src, bytes / 16,
+                       sink);
+    GH_LAUNCHED("k_stream_read");
     return GH_OK;
 }
 int gh_rmsnorm_forward(const float* x, const float* w, float* out, float* rrms, int64_t rows, int dim, float eps) {

@@ -138,9 +138,48 @@ __global__ void k_to_f16(const float* __restrict__ x, uint16_t* __restrict__ y, 
     }
 }
 
+// Range-safe fp16 activations for the MFMA GEMMs: row r is stored as x * 2^s_r with s_r chosen
+// so that the row's largest magnitude lands in [2^14, 2^15) (fp16's largest finite value is
+// 65504), and rinv[r] = 2^-s_r rescales that row of the product exactly. The relative rounding
+// of every element is then fp16's 2^-11 whatever the row's range (a plain cast turns
+// |x| > 65504 into inf and flushes |x| < 6e-8 to zero). Rows without a finite non-zero
+// maximum keep s_r = 0. One block per row.
+__device__ __forceinline__ int f16_row_shift(float amax) {
+    if (!(amax > 0.0f) || !isfinite(amax)) return 0;
+    int e = 0;
+    (void)frexpf(amax, &e);  // amax = m 2^e, m in [0.5, 1)
+    return min(max(15 - e, -120), 120);
+}
+__global__ void __launch_bounds__(256) k_to_f16_rows(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                     float* __restrict__ rinv, int K) {
+    const int r = blockIdx.x;
+    const float4* xr = (const float4*)(x + (size_t)r * K);
+    const int k4 = K / 4;
+    float amax = 0.0f;
+    for (int i = threadIdx.x; i < k4; i += 256) {
+        const float4 v = xr[i];
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    __shared__ float red[4];
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    const int sh = f16_row_shift(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+    if (threadIdx.x == 0) rinv[r] = ldexpf(1.0f, -sh);
+    f16x4v* yr = (f16x4v*)(y + (size_t)r * K);
+    for (int i = threadIdx.x; i < k4; i += 256) {
+        const float4 v = xr[i];
+        f16x4v h;
+        h[0] = (_Float16)ldexpf(v.x, sh); h[1] = (_Float16)ldexpf(v.y, sh);
+        h[2] = (_Float16)ldexpf(v.z, sh); h[3] = (_Float16)ldexpf(v.w, sh);
+        yr[i] = h;
+    }
+}
+
 template <int KIND>
-__global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb, int Ts) {
+__global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__ X16, const float* __restrict__ rinv,
+                                                   const uint8_t* __restrict__ W, float* __restrict__ Y, int M, int K,
+                                                   int N, size_t rowb, int Ts) {
     __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDS_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -234,7 +273,7 @@ __global__ void __launch_bounds__(256, 2) k_gemm_q2(const uint16_t* __restrict__
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) Y[(size_t)row * N + col] = acc[i][j][e];
+                if (row < M) Y[(size_t)row * N + col] = acc[i][j][e] * rinv[row];
             }
         }
 }
@@ -273,7 +312,7 @@ constexpr size_t G4_LDS = 4 * 256 * 128;  // A[2], B[2]: 256 rows x 128 bytes
 __device__ __forceinline__ void g4_dma(const void* base, uint32_t voff, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base))
-                 : "memory");
+                 : "memory", "m0");
 }
 
 struct G4Scale {
@@ -387,8 +426,9 @@ __device__ __forceinline__ void g4_quarter_rt(const G4Raw<KIND>& r, const G4Scal
 
 // K steps [t_beg, t_beg + T) of block (tile, blockIdx.y); T even, >= 2
 template <int KIND>
-__global__ void __launch_bounds__(256, 1) k_gemm_q4(const uint16_t* __restrict__ X16, const uint8_t* __restrict__ W,
-                                                   float* __restrict__ Y, int M, int K, int N, size_t rowb, int T) {
+__global__ void __launch_bounds__(256, 1) k_gemm_q4(const uint16_t* __restrict__ X16, const float* __restrict__ rinv,
+                                                   const uint8_t* __restrict__ W, float* __restrict__ Y, int M, int K,
+                                                   int N, size_t rowb, int T) {
     extern __shared__ __attribute__((aligned(16))) uint8_t g4_smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tilesN = cdiv(N, G4N), tilesM = cdiv(M, G4M);
@@ -525,8 +565,9 @@ __global__ void __launch_bounds__(256, 1) k_gemm_q4(const uint16_t* __restrict__
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if (row >= M) continue;
-                if (split) atomicAdd(&Y[(size_t)row * N + col], acc[i][j][e]);
-                else Y[(size_t)row * N + col] = acc[i][j][e];
+                const float v = acc[i][j][e] * rinv[row];
+                if (split) atomicAdd(&Y[(size_t)row * N + col], v);
+                else Y[(size_t)row * N + col] = v;
             }
         }
 }
@@ -581,8 +622,27 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
     for (int b = 0; b < NH; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)((s0 >> 3) + b) * 144);
 #pragma unroll
     for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
-    // 32 rows x KK fp32 -> fp16 LDS (8 values per piece)
+    // 32 rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as
+    // k_to_f16_rows does (the row maxima first, one wave per group of rows)
     constexpr int RQ = KK / 8;
+    __shared__ int sShift[32];
+    {
+        constexpr int NW = 4 * NWK, RPW = 32 / NW;  // rows per wave
+        for (int rr = 0; rr < RPW; ++rr) {
+            const int r = wave * RPW + rr;
+            float amax = 0.0f;
+            if (m0 + r < M) {
+                const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK);
+                for (int i = lane; i < KK / 4; i += 64) {
+                    const float4 v = src[i];
+                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+            }
+            for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            if (lane == 0) sShift[r] = f16_row_shift(amax);
+        }
+    }
+    __syncthreads();
     for (int e = tid; e < 32 * RQ; e += 256 * NWK) {
         const int r = e / RQ, c = e - r * RQ;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
@@ -591,9 +651,12 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
             a = src[0];
             b = src[1];
         }
+        const int sh = sShift[r];
         sk_f16x8 h;
-        h[0] = (_Float16)a.x; h[1] = (_Float16)a.y; h[2] = (_Float16)a.z; h[3] = (_Float16)a.w;
-        h[4] = (_Float16)b.x; h[5] = (_Float16)b.y; h[6] = (_Float16)b.z; h[7] = (_Float16)b.w;
+        h[0] = (_Float16)ldexpf(a.x, sh); h[1] = (_Float16)ldexpf(a.y, sh);
+        h[2] = (_Float16)ldexpf(a.z, sh); h[3] = (_Float16)ldexpf(a.w, sh);
+        h[4] = (_Float16)ldexpf(b.x, sh); h[5] = (_Float16)ldexpf(b.y, sh);
+        h[6] = (_Float16)ldexpf(b.z, sh); h[7] = (_Float16)ldexpf(b.w, sh);
         *(sk_f16x8*)(sA + r * SA + 8 * c) = h;
     }
     __syncthreads();
@@ -636,7 +699,8 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
             const int m = m0 + 16 * h + 4 * kq + j;
             if (m < M) {
                 float* yp = Y + (size_t)m * N + nrow;
-                *yp = accumulate ? *yp + acc[h][j] : acc[h][j];
+                const float v = ldexpf(acc[h][j], -sShift[m - m0]);
+                *yp = accumulate ? *yp + v : v;
             }
         }
 }
@@ -662,11 +726,12 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
 // write a temporary that one more launch adds)
 template <int KIND>
 static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate) {
-    uint16_t* x16 = (uint16_t*)workspace(WS_GEMM_X, (size_t)M * K * 2);
+    const size_t xbytes = ((size_t)M * K * 2 + 255) & ~(size_t)255;
+    uint16_t* x16 = (uint16_t*)workspace(WS_GEMM_X, xbytes + (size_t)M * 4);
     if (!x16) return fail(GH_ENOMEM, "gemm: workspace");
-    const int64_t n4 = (int64_t)M * K / 4;
-    hipLaunchKernelGGL(k_to_f16, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 8192)), dim3(256), 0, stream(), x,
-                       x16, n4);
+    float* rinv = (float*)((uint8_t*)x16 + xbytes);
+    hipLaunchKernelGGL(k_to_f16_rows, dim3((unsigned)M), dim3(256), 0, stream(), x, x16, rinv, K);
+    GH_LAUNCHED("k_to_f16_rows");
     float* yout = y;  // where the product goes; with accumulate outside the split-K path: a temporary
     auto finish_acc = [&]() -> int {
         if (yout == y) return GH_OK;
@@ -701,7 +766,7 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
                 hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)std::min<int64_t>(cdiv64(n4, 256), 4096)), dim3(256), 0,
                                    stream(), yout, n4);
             }
-            hipLaunchKernelGGL(k_gemm_q4<KIND>, dim3(tiles, split), dim3(256), G4_LDS, stream(), x16,
+            hipLaunchKernelGGL(k_gemm_q4<KIND>, dim3(tiles, split), dim3(256), G4_LDS, stream(), x16, rinv,
                                (const uint8_t*)w, yout, M, K, N, rowb, T / split);
             GH_LAUNCHED("k_gemm_q4");
             return finish_acc();
@@ -718,16 +783,16 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
         const int Ts = cdiv(T, S);
         float* part = (float*)workspace(WS_GEMM_PART, (size_t)S * M * N * 4);
         if (!part) return fail(GH_ENOMEM, "gemm: split-K workspace");
-        hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks, S), dim3(256), 0, stream(), x16, (const uint8_t*)w, part, M,
-                           K, N, rowb, Ts);
+        hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks, S), dim3(256), 0, stream(), x16, rinv, (const uint8_t*)w,
+                           part, M, K, N, rowb, Ts);
         const int64_t n = (int64_t)M * N;
         hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)std::min<int64_t>(cdiv64(n, 256), 2048)), dim3(256), 0,
                            stream(), part, y, n, S, accumulate);
         GH_LAUNCHED("k_gemm_q2 (split K)");
         return GH_OK;
     }
-    hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, (const uint8_t*)w, yout, M, K, N,
-                       rowb, T);
+    hipLaunchKernelGGL(k_gemm_q2<KIND>, dim3(blocks), dim3(256), 0, stream(), x16, rinv, (const uint8_t*)w, yout, M, K,
+                       N, rowb, T);
     GH_LAUNCHED("k_gemm_q2");
     return finish_acc();
 }

@@ -252,10 +252,22 @@ struct Param {
     size_t nbytes, off;
 };
 
+static const char* const STATE_INVALID_MSG =
+    "the model state is invalid after an aborted persistent decode (call gh_granite_reset, then prefill again)";
+
 struct gh_granite {
     int V, d, L, H, KV, hd, E, ne, K, SH, di, mh, mdh, mds, ck, qkind;
     std::vector<int> lt;
     float eps, scale;
+    // Granite multipliers (model/model.cpp:2431-2432, 2531; inference/generator.cpp:248, 266, 440):
+    // embeddings x emb_mult, every branch output x res_mult before its residual add, logits x
+    // (1 / logits_scaling). tied: the lm head is tok_embeddings, else its own fp16 "lm_head"
+    // [V, d] (model/model.cpp:1160). aux_free: per-layer router bias "layers.N.moe_bias" [ne]
+    // added to the probabilities for the selection (model/model.cpp:179-194).
+    float emb_mult = 1.0f, res_mult = 1.0f, logits_scaling = 1.0f;
+    bool tied = true, aux_free = false;
+    bool plain_multipliers() const { return emb_mult == 1.0f && res_mult == 1.0f; }
+    const char* head_name() const { return tied ? "tok_embeddings" : "lm_head"; }
     int max_ctx, conv_dim, proj, qd, kvd, pinned_cfg;
     std::vector<Param> params;
     std::map<std::string, size_t> by_name;
@@ -279,6 +291,10 @@ struct gh_granite {
     PdModel* pd_dev = nullptr;
     uint8_t* pd_buf = nullptr;
     size_t pd_zero_bytes = 0;  // bytes of pd_buf zeroed before each launch (all of it)
+    // An aborted persistent launch leaves the recurrent state, the KV cache and the generated
+    // ids partly advanced: the model refuses every call that reads that state until a reset.
+    bool state_invalid = false;
+    bool pd_force_abort = false;  // test hook: the next persistent launch starts aborted
 
     const void* W(const std::string& n) const {
         auto it = by_name.find(n);
@@ -337,9 +353,28 @@ static int ensure_acts(gh_granite* g, int rows) {
         if (rc_) return rc_;           \
     } while (0)
 
+// Model::moe_bias_ptr (model/model.cpp:192-199): the layer's router bias, or null
+static const float* moe_bias(const gh_granite* g, int l) {
+    return g->aux_free ? g->F("layers." + std::to_string(l) + ".moe_bias") : nullptr;
+}
+
+// x += res_mult * branch (inference/generator.cpp:266-268: scale_inplace, then add_inplace;
+// two roundings, as the reference does them)
+static int add_branch(gh_granite* g, float* branch, int64_t n) {
+    if (g->res_mult != 1.0f) GHC(gh_scale_inplace(branch, g->res_mult, n));
+    return gh_add_inplace(g->x, branch, n);
+}
+
+// final norm output -> logits (inference/generator.cpp:438-441)
+static int lm_head(gh_granite* g, const float* xb) {
+    GHC(linear_any(xb, g->W(g->head_name()), g->logits, 1, g->d, g->V, 4));
+    if (g->logits_scaling != 1.0f) GHC(gh_scale_inplace(g->logits, 1.0f / g->logits_scaling, g->V));
+    return GH_OK;
+}
+
 static int moe_layer(gh_granite* g, int l, const float* xb, float* out, int n) {
     const std::string pre = "layers." + std::to_string(l) + ".";
-    return gh_moe_forward_bias_half(xb, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
+    return gh_moe_forward_bias_half(xb, g->F(pre + "moe_router"), moe_bias(g, l), g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
                                     g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"),
                                     g->W(pre + "moe_sh_down"), out, nullptr, nullptr, nullptr, nullptr, nullptr,
                                     nullptr, n, g->d, g->E, g->ne, g->K, g->SH, g->qkind);
@@ -359,6 +394,7 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
     const int d = g->d;
     hipLaunchKernelGGL(k_alloc_slot, dim3(1), dim3(1), 0, stream(), g->ctl);
     GHC(gh_embedding_forward_half(g->ctl + CTL_TOKEN, (const uint16_t*)g->W("tok_embeddings"), g->x, 1, d, g->V));
+    if (g->emb_mult != 1.0f) GHC(gh_scale_inplace(g->x, g->emb_mult, d));
     for (int l = 0; l < g->L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, 1, d, g->eps));
@@ -373,13 +409,13 @@ static int decode_step_dev(gh_granite* g, bool argmax) {
             GHC(attn_decode_devctl(g->q, g->kc[l], g->vc[l], g->att, g->H, g->KV, g->hd, g->max_ctx, g->ctl, g->scale));
             GHC(linear_any(g->att, g->W(pre + "wo"), g->pr, 1, g->qd, d, g->qkind));
         }
-        GHC(gh_add_inplace(g->x, g->pr, d));
+        GHC(add_branch(g, g->pr, d));
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "ffn_norm"), g->xb, nullptr, 1, d, g->eps));
         GHC(moe_layer(g, l, g->xb, g->pr, 1));
-        GHC(gh_add_inplace(g->x, g->pr, d));
+        GHC(add_branch(g, g->pr, d));
     }
     GHC(gh_rmsnorm_forward(g->x, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
-    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    GHC(lm_head(g, g->xb));
     if (argmax) {
         GHC(launch_argmax(g->logits, g->V, g->ctl + CTL_TOKEN));
         hipLaunchKernelGGL(k_record_token, dim3(1), dim3(1), 0, stream(), g->ctl, g->gen_ids, g->max_ctx);
@@ -405,6 +441,9 @@ int moe_forward_acc(const float* x, const float* router_w, const float* router_b
 static bool fused_supported(const gh_granite* g) {
     const int k = g->qkind;
     if (k != 2 && k != 3) return false;
+    // the fused launches add branch outputs into the residual stream unscaled and take the
+    // embedding row as is: other multipliers run the step launch by launch
+    if (!g->plain_multipliers()) return false;
     if (g->d % 256 || g->di % 256 || g->qd % 256 || g->qd % 16 || g->kvd % 16) return false;
     if (g->mds != 64 && g->mds != 128) return false;
     const int chunk_min = attn_chunk_min();
@@ -478,18 +517,21 @@ static int decode_step_fused(gh_granite* g, bool argmax) {
             f3.epi = GM_EPI_ADD;
             GHC(gemv_fused(g->q, g->W(pre + "wo"), g->x, g->qd, d, g->qkind, f3));
         }
-        GHC(moe_decode_fused(g->x, g->F(pre + "ffn_norm"), g->eps, g->F(pre + "moe_router"), nullptr,
+        GHC(moe_decode_fused(g->x, g->F(pre + "ffn_norm"), g->eps, g->F(pre + "moe_router"), moe_bias(g, l),
                              g->W(pre + "moe_gate"), g->W(pre + "moe_up"), g->W(pre + "moe_down"),
                              g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"), g->W(pre + "moe_sh_down"), 1, d, g->E,
                              g->ne, g->K, g->SH, g->qkind));
     }
-    if (launch_head_argmax(g->x, g->F("final_norm"), g->eps, (const uint16_t*)g->W("tok_embeddings"), g->logits, d,
+    // the one-launch tail picks the id from unscaled logits: with a logits_scaling it runs as
+    // norm, head, scale and argmax launches (the scaled values decide ties, as in the reference)
+    if (g->logits_scaling == 1.0f &&
+        launch_head_argmax(g->x, g->F("final_norm"), g->eps, (const uint16_t*)g->W(g->head_name()), g->logits, d,
                            g->V, g->ctl, g->gen_ids, g->max_ctx, argmax)) {
         GH_LAUNCHED("decode_step");
         return GH_OK;
     }
     GHC(gh_rmsnorm_forward(g->x, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
-    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    GHC(lm_head(g, g->xb));
     if (argmax)
         GHC(launch_argmax_record(g->logits, g->V, g->ctl + CTL_TOKEN, g->ctl + CTL_STEP, g->gen_ids, g->max_ctx));
     GH_LAUNCHED("decode_step");
@@ -519,7 +561,26 @@ int gh_lm_head_greedy_dev(const float* x, const float* norm_w, float eps, const 
 
 int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_granite** out) {
     GH_REQUIRE(cfg && fcfg && out, "granite_create: null argument");
+    GH_REQUIRE(cfg[2] > 0 && cfg[2] <= 1024, "granite_create: bad layer count %d", cfg[2]);
+    return gh_granite_create_ex(cfg, 16 + cfg[2], fcfg, 2, max_ctx, out);
+}
+
+int gh_granite_create_ex(const int32_t* cfg, int ncfg, const float* fcfg, int nfcfg, int max_ctx, gh_granite** out) {
+    GH_REQUIRE(cfg && fcfg && out && ncfg >= 17 && nfcfg >= 2, "granite_create: null argument or short arrays");
+    GH_REQUIRE(cfg[2] > 0 && cfg[2] <= 1024 && ncfg >= 16 + cfg[2], "granite_create: bad layer count %d", cfg[2]);
+    const int L0 = cfg[2];
+    const float emb_mult = nfcfg > 2 ? fcfg[2] : 1.0f, res_mult = nfcfg > 3 ? fcfg[3] : 1.0f,
+                logits_scaling = nfcfg > 4 ? fcfg[4] : 1.0f;
+    // model/model.cpp:360-366: logits_scaling is a divisor, the multipliers must be finite
+    GH_REQUIRE(std::isfinite(logits_scaling) && logits_scaling > 0.0f,
+               "granite_create: logits_scaling must be finite and > 0");
+    GH_REQUIRE(std::isfinite(emb_mult) && std::isfinite(res_mult), "granite_create: multipliers must be finite");
     gh_granite* g = new gh_granite();
+    g->emb_mult = emb_mult;
+    g->res_mult = res_mult;
+    g->logits_scaling = logits_scaling;
+    g->tied = ncfg > 16 + L0 ? cfg[16 + L0] != 0 : true;
+    g->aux_free = ncfg > 17 + L0 ? cfg[17 + L0] != 0 : false;
     g->V = cfg[0]; g->d = cfg[1]; g->L = cfg[2]; g->H = cfg[3]; g->KV = cfg[4]; g->hd = cfg[5]; g->E = cfg[6];
     g->ne = cfg[7]; g->K = cfg[8]; g->SH = cfg[9]; g->di = cfg[10]; g->mh = cfg[11]; g->mdh = cfg[12];
     g->mds = cfg[13]; g->ck = cfg[14]; g->qkind = cfg[15];
@@ -536,7 +597,7 @@ int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_gra
         delete g;
         return fail(GH_EINVAL, "granite_create: bad configuration");
     }
-    // parameter table, model/model.cpp:1087-1160 (tied lm_head)
+    // parameter table, model/model.cpp:1087-1160
     const int64_t d = g->d;
     add_param(g, "tok_embeddings", (int64_t)g->V * d, 1);
     for (int i = 0; i < g->L; ++i) {
@@ -566,8 +627,10 @@ int gh_granite_create(const int32_t* cfg, const float* fcfg, int max_ctx, gh_gra
         add_param(g, pre + "moe_sh_gate", (int64_t)g->SH * d, 0);
         add_param(g, pre + "moe_sh_up", (int64_t)g->SH * d, 0);
         add_param(g, pre + "moe_sh_down", d * g->SH, 0);
+        if (g->aux_free) add_param(g, pre + "moe_bias", g->ne, 2);
     }
     add_param(g, "final_norm", d, 2);
+    if (!g->tied) add_param(g, "lm_head", (int64_t)g->V * d, 1);  // fp16, like tok_embeddings
     size_t off = 0;
     for (Param& p : g->params) {
         p.off = off;
@@ -649,7 +712,20 @@ int gh_granite_set_param(gh_granite* g, const char* name, const void* host, size
 int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f) {
     GH_REQUIRE(g && f, "granite_load_gguf: null argument");
     for (const Param& p : g->params) {
-        const int64_t ti = gh_gguf_find_tensor(f, p.name.c_str());
+        const bool is_bias = p.name.size() > 9 && p.name.compare(p.name.size() - 9, 9, ".moe_bias") == 0;
+        std::string src = p.name;
+        int64_t ti = gh_gguf_find_tensor(f, src.c_str());
+        if (ti < 0 && p.name == "lm_head") {
+            // no output projection in the file: the token embedding serves as the lm head
+            // (format/gguf_codec.cpp:1517-1523)
+            src = "tok_embeddings";
+            ti = gh_gguf_find_tensor(f, src.c_str());
+        }
+        if (ti < 0 && is_bias) {
+            // a router bias absent from the file stays zero (format/gguf_codec.cpp:1549-1556)
+            GH_HIP(hipMemset(g->wbuf + p.off, 0, p.nbytes));
+            continue;
+        }
         GH_REQUIRE(ti >= 0, "granite_load_gguf: tensor not found: %s", p.name.c_str());
         int nd = 0;
         uint64_t dims[8], nb = 0;
@@ -659,9 +735,9 @@ int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f) {
         GH_REQUIRE(numel == (uint64_t)p.numel, "granite_load_gguf: %s has %llu values, the model needs %lld",
                    p.name.c_str(), (unsigned long long)numel, (long long)p.numel);
         void* dst = g->wbuf + p.off;
-        if (p.storage == 0) GHC(gh_gguf_read_packed(f, p.name.c_str(), g->qkind, dst, GH_DEV_GPU, p.nbytes));
-        else if (p.storage == 1) GHC(gh_gguf_read_f16(f, p.name.c_str(), (uint16_t*)dst, GH_DEV_GPU, (size_t)p.numel));
-        else GHC(gh_gguf_read_f32(f, p.name.c_str(), (float*)dst, GH_DEV_GPU, (size_t)p.numel));
+        if (p.storage == 0) GHC(gh_gguf_read_packed(f, src.c_str(), g->qkind, dst, GH_DEV_GPU, p.nbytes));
+        else if (p.storage == 1) GHC(gh_gguf_read_f16(f, src.c_str(), (uint16_t*)dst, GH_DEV_GPU, (size_t)p.numel));
+        else GHC(gh_gguf_read_f32(f, src.c_str(), (float*)dst, GH_DEV_GPU, (size_t)p.numel));
     }
     return GH_OK;
 }
@@ -697,6 +773,12 @@ int gh_granite_init_synthetic(gh_granite* g, uint64_t seed) {
     return GH_OK;
 }
 
+int gh_granite_test_force_abort(gh_granite* g) {
+    GH_REQUIRE(g != nullptr, "granite_test_force_abort: null model");
+    g->pd_force_abort = true;
+    return GH_OK;
+}
+
 int gh_granite_reset(gh_granite* g) {
     GH_REQUIRE(g != nullptr, "granite_reset: null model");
     size_t sbytes = 0;
@@ -709,17 +791,22 @@ int gh_granite_reset(gh_granite* g) {
     GH_HIP(hipMemcpyAsync(g->ctl, ctl, sizeof ctl, hipMemcpyHostToDevice, stream()));
     GH_HIP(hipStreamSynchronize(stream()));
     g->host_len = 0;
+    g->state_invalid = false;
     return GH_OK;
 }
 
 int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* logits_host, int mamba_mode) {
     GH_REQUIRE(g && ids_host && P > 0, "granite_prefill: bad arguments");
+    GH_REQUIRE(!g->state_invalid, "granite_prefill: %s", STATE_INVALID_MSG);
     GH_REQUIRE(g->host_len == 0, "granite_prefill: the cache is not empty (reset first)");
     GH_REQUIRE(P <= 1024 && P < g->max_ctx, "granite_prefill: %d tokens (batched prefill takes <= 1024 and < ctx)", P);
     const int d = g->d;
     GHC(ensure_acts(g, P));
     GH_HIP(hipMemcpyAsync(g->ids, ids_host, (size_t)P * 4, hipMemcpyHostToDevice, stream()));
     GHC(gh_embedding_forward_half(g->ids, (const uint16_t*)g->W("tok_embeddings"), g->x, P, d, g->V));
+    if (g->emb_mult != 1.0f) GHC(gh_scale_inplace(g->x, g->emb_mult, (int64_t)P * d));
+    // with a residual multiplier every branch lands in pr first and is scaled there
+    const bool acc = g->res_mult == 1.0f;
     for (int l = 0; l < g->L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
         GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, P, d, g->eps));
@@ -733,8 +820,9 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
                 GHC(mamba_forward_impl(g->xb, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
                                        g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"),
                                        g->F(mp + "D"), g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->ssm[l],
-                                       g->conv[l], g->x, P, d, g->di, g->conv_dim, g->mh, g->mdh, g->mds, g->ck,
-                                       g->eps, g->qkind, true));
+                                       g->conv[l], acc ? g->x : g->pr, P, d, g->di, g->conv_dim, g->mh, g->mdh,
+                                       g->mds, g->ck, g->eps, g->qkind, acc));
+                if (!acc) GHC(add_branch(g, g->pr, (int64_t)P * d));
             }
         } else {
             GHC(linear_any(g->xb, g->W(pre + "wq"), g->q, P, d, g->qd, g->qkind));
@@ -743,17 +831,22 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
             GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
             GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
             GHC(attention_prefill(g->q, g->k, g->v, g->att, 1, P, g->H, g->KV, g->hd, g->scale, 0));
-            GHC(linear_acc(g->att, g->W(pre + "wo"), g->x, P, g->qd, d, g->qkind));  // x += attn W_o^T
+            if (acc) {
+                GHC(linear_acc(g->att, g->W(pre + "wo"), g->x, P, g->qd, d, g->qkind));  // x += attn W_o^T
+            } else {
+                GHC(linear_any(g->att, g->W(pre + "wo"), g->pr, P, g->qd, d, g->qkind));
+                GHC(add_branch(g, g->pr, (int64_t)P * d));
+            }
         }
-        if (g->lt[l] == 0 && mamba_mode == 0) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        if (g->lt[l] == 0 && mamba_mode == 0) GHC(add_branch(g, g->pr, (int64_t)P * d));
         // x += moe(ffn_norm(x)): the norm rides on the router launch (normalised rows into xb); the
         // residual add on the combine launch when the path has one, else here
         int added = 0;
-        GHC(moe_forward_acc(g->x, g->F(pre + "moe_router"), nullptr, g->W(pre + "moe_gate"), g->W(pre + "moe_up"),
-                            g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"), g->W(pre + "moe_sh_up"),
-                            g->W(pre + "moe_sh_down"), g->pr, g->x, &added, nullptr, nullptr, nullptr, P, d, g->E,
+        GHC(moe_forward_acc(g->x, g->F(pre + "moe_router"), moe_bias(g, l), g->W(pre + "moe_gate"),
+                            g->W(pre + "moe_up"), g->W(pre + "moe_down"), g->W(pre + "moe_sh_gate"),
+                            g->W(pre + "moe_sh_up"), g->W(pre + "moe_sh_down"), g->pr, acc ? g->x : nullptr, &added, nullptr, nullptr, nullptr, P, d, g->E,
                             g->ne, g->K, g->SH, g->qkind, g->F(pre + "ffn_norm"), g->eps, g->xb));
-        if (!added) GHC(gh_add_inplace(g->x, g->pr, (int64_t)P * d));
+        if (!added) GHC(add_branch(g, g->pr, (int64_t)P * d));
     }
     // cache length P, ring start 0 (KVCache::set_length)
     const int32_t lenstart[2] = {P, 0};
@@ -762,7 +855,7 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
     GH_HIP(hipMemcpyAsync(g->ctl + CTL_STEP, &zero, 4, hipMemcpyHostToDevice, stream()));
     g->host_len = P;
     GHC(gh_rmsnorm_forward(g->x + (size_t)(P - 1) * d, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
-    GHC(linear_any(g->xb, g->W("tok_embeddings"), g->logits, 1, d, g->V, 4));
+    GHC(lm_head(g, g->xb));
     if (logits_host) {
         GH_HIP(hipMemcpyAsync(logits_host, g->logits, (size_t)g->V * 4, hipMemcpyDeviceToHost, stream()));
     }
@@ -772,6 +865,7 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
 
 int gh_granite_decode(gh_granite* g, int32_t token, float* logits_host) {
     GH_REQUIRE(g != nullptr, "granite_decode: null model");
+    GH_REQUIRE(!g->state_invalid, "granite_decode: %s", STATE_INVALID_MSG);
     GH_HIP(hipMemcpyAsync(g->ctl + CTL_TOKEN, &token, 4, hipMemcpyHostToDevice, stream()));
     GHC(decode_step(g, false));
     g->host_len = g->host_len < g->max_ctx ? g->host_len + 1 : g->host_len;
@@ -869,16 +963,26 @@ static int pd_generate(gh_granite* g, int step0, int n_steps) {
     m.logits = pd_g(g->logits);
     GH_HIP(hipMemcpyAsync(g->pd_dev, &m, sizeof m, hipMemcpyHostToDevice, stream()));
     GH_HIP(hipMemsetAsync(g->pd_buf, 0, g->pd_zero_bytes, stream()));
+    if (g->pd_force_abort) {
+        // every wait that misses sees the flag and returns; the launch still runs to its end
+        const int32_t one = 1;
+        GH_HIP(hipMemcpyAsync(abort_flag, &one, 4, hipMemcpyHostToDevice, stream()));
+        g->pd_force_abort = false;
+    }
     GHC(pd_launch(m, g->pd_dev, g->host_len, step0, n_steps));
     int32_t aborted = 0;
     GH_HIP(hipMemcpyAsync(&aborted, abort_flag, 4, hipMemcpyDeviceToHost, stream()));
     GH_HIP(hipStreamSynchronize(stream()));
-    if (aborted) return fail(GH_EHIP, "persistent decode: a hand-over wait ran out (launch aborted)");
+    if (aborted) {
+        g->state_invalid = true;
+        return fail(GH_EHIP, "persistent decode: a hand-over wait ran out (launch aborted); %s", STATE_INVALID_MSG);
+    }
     return GH_OK;
 }
 
 int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int use_graph) {
     GH_REQUIRE(g && ids_host && n_new >= 0, "granite_generate: bad arguments");
+    GH_REQUIRE(!g->state_invalid, "granite_generate: %s", STATE_INVALID_MSG);
     GH_REQUIRE(g->host_len + n_new <= g->max_ctx, "granite_generate: %d + %d tokens exceed the context %d",
                g->host_len, n_new, g->max_ctx);
     if (n_new == 0) return GH_OK;
@@ -888,7 +992,10 @@ int gh_granite_generate_greedy(gh_granite* g, int n_new, int32_t* ids_host, int 
     GHC(launch_argmax(g->logits, g->V, g->ctl + CTL_TOKEN));
     hipLaunchKernelGGL(k_record_token, dim3(1), dim3(1), 0, stream(), g->ctl, g->gen_ids, g->max_ctx);
     int done = 1;
-    if (use_graph == 2 && n_new > 1) {
+    // the persistent kernel implements the plain c1-style sequence (tied head, no router bias,
+    // unit multipliers); other models decode through the graph
+    const bool pd_model = g->tied && !g->aux_free && g->plain_multipliers() && g->logits_scaling == 1.0f;
+    if (use_graph == 2 && n_new > 1 && pd_model) {
         // the whole loop in one persistent launch when the model fits it
         const int rc = pd_generate(g, 1, n_new - 1);
         if (rc == GH_OK) {

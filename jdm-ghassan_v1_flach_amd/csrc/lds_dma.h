@@ -13,11 +13,11 @@ namespace gh {
 
 // 64-bit address per lane
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
 }
 // 64-bit base in SGPRs + 32-bit per-lane offset (no per-lane address arithmetic)
 __device__ __forceinline__ void lds_dma16s(const void* base, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
 // wave-uniform LDS byte address of p
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {

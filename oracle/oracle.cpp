@@ -1005,8 +1005,9 @@ int orc_moe_forward_q(const float* x, const float* rw, const float* bias, const 
 // Synthetic Granite weights (our own recipe, shared with the product's
 // host-side initialiser): every parameter has its own Rng stream seeded
 // with seed ^ fnv1a64(name). Norm weights, conv bias, D and dt_bias are 1,
-// A_log[h] = log(h+1) (the reference's init, model/model.cpp:1586-1603);
-// everything else is N(0, 0.02).
+// A_log[h] = log(h+1) (the reference's init, model/model.cpp:1586-1603),
+// the aux-free router bias 0 (model/model.cpp:179-191); everything else is
+// N(0, 0.02).
 void orc_synth_param_f32(const char* name, uint64_t seed, float* out, int64_t n) {
     const std::string s(name);
     auto ends = [&](const char* suf) {
@@ -1019,6 +1020,10 @@ void orc_synth_param_f32(const char* name, uint64_t seed, float* out, int64_t n)
     }
     if (ends("A_log")) {
         for (i64 i = 0; i < n; ++i) out[i] = std::log((float)(i + 1));
+        return;
+    }
+    if (ends("moe_bias")) {
+        for (i64 i = 0; i < n; ++i) out[i] = 0.0f;
         return;
     }
     orc_rng_normal(seed ^ orc_fnv1a64(name, (i64)s.size()), 0.0f, 0.02f, out, n);
@@ -1042,6 +1047,23 @@ int orc_granite_generate(const int32_t* cfg, const float* fcfg, const char** nam
 int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char** names, const void** ptrs,
                                int nparams, const int32_t* prompt, int P, int n_new, int max_ctx, int32_t* out_ids,
                                float* out_margins, double* seconds) {
+    return orc_granite_generate_ex(cfg, 16 + cfg[2], fcfg, 2, names, ptrs, nparams, prompt, P, n_new, max_ctx,
+                                   nullptr, out_ids, out_margins, nullptr, seconds);
+}
+
+// The general form. Optional Granite fields (defaults when past ncfg / nfcfg):
+// cfg[16+L] tie_embeddings (1; 0 = the "lm_head" fp16 parameter is the output
+// projection, model/model.h:465), cfg[17+L] moe_aux_free (0; 1 = per-layer
+// "layers.N.moe_bias" fp32 router bias, Model::moe_bias_ptr), fcfg[2]
+// embedding_multiplier, fcfg[3] residual_multiplier, fcfg[4] logits_scaling
+// (1; inference/generator.cpp:248-249, 266-267, 440-441 and :705, 762, 907).
+// forced (optional, n_new ids): step s feeds forced[s] instead of the greedy
+// id (teacher forcing; out_ids still records the greedy id of each step).
+// out_logits (optional, n_new x V): the logits each id was picked from.
+int orc_granite_generate_ex(const int32_t* cfg, int ncfg, const float* fcfg, int nfcfg, const char** names,
+                            const void** ptrs, int nparams, const int32_t* prompt, int P, int n_new, int max_ctx,
+                            const int32_t* forced, int32_t* out_ids, float* out_margins, float* out_logits,
+                            double* seconds) {
     using clk = std::chrono::steady_clock;
     const auto t_start = clk::now();
     const int V = cfg[0], d = cfg[1], L = cfg[2], H = cfg[3], KV = cfg[4], hd = cfg[5], E = cfg[6], ne = cfg[7],
@@ -1049,6 +1071,11 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
               qk = cfg[15];
     const int* lt = cfg + 16;
     const float eps = fcfg[0], scale = fcfg[1];
+    if (ncfg < 16 + L) return -1;
+    const bool tied = ncfg > 16 + L ? cfg[16 + L] != 0 : true;
+    const bool aux_free = ncfg > 17 + L ? cfg[17 + L] != 0 : false;
+    const float emb_mult = nfcfg > 2 ? fcfg[2] : 1.0f, res_mult = nfcfg > 3 ? fcfg[3] : 1.0f,
+                logits_scaling = nfcfg > 4 ? fcfg[4] : 1.0f;
     const int conv_dim = di + 2 * mds, qd = H * hd, kvd = KV * hd, win = ck > 1 ? ck - 1 : 1;
     if (P < 1 || P > 1024 || P + n_new > max_ctx) return -1;
     std::map<std::string, const void*> pm;
@@ -1065,7 +1092,17 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
         if (lt[l] != 0 && !W(pre + "wq")) return -2;
     }
     const u16* emb = (const u16*)W("tok_embeddings");
-    if (!emb || !W("final_norm")) return -2;
+    const u16* head = tied ? emb : (const u16*)W("lm_head");
+    if (!emb || !head || !W("final_norm")) return -2;
+    auto scale_emb = [&](float* x, size_t n) {  // ops::scale_inplace: a[i] *= s
+        if (emb_mult != 1.0f)
+            for (size_t i = 0; i < n; ++i) x[i] *= emb_mult;
+    };
+    auto add_branch = [&](float* x, float* br, size_t n) {
+        if (res_mult != 1.0f)
+            for (size_t i = 0; i < n; ++i) br[i] *= res_mult;
+        for (size_t i = 0; i < n; ++i) x[i] += br[i];
+    };
 
     // state: per-mamba-layer conv + ssm, per-attention-layer fp16 K/V cache
     std::map<int, std::vector<float>> conv, ssm;
@@ -1084,7 +1121,8 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
 
     auto moe = [&](int l, const float* xb, float* outp, int n) {
         const std::string pre = "layers." + std::to_string(l) + ".";
-        orc_moe_forward_q(xb, F(pre + "moe_router"), nullptr, W(pre + "moe_gate"), W(pre + "moe_up"),
+        orc_moe_forward_q(xb, F(pre + "moe_router"), aux_free ? F(pre + "moe_bias") : nullptr, W(pre + "moe_gate"),
+                          W(pre + "moe_up"),
                           W(pre + "moe_down"), W(pre + "moe_sh_gate"), W(pre + "moe_sh_up"), W(pre + "moe_sh_down"),
                           outp, nullptr, nullptr, n, d, E, ne, K, SH, qk);
     };
@@ -1101,7 +1139,11 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
     auto finish = [&](const float* xrow) {
         std::vector<float> h((size_t)d);
         rmsnorm(xrow, F("final_norm"), h.data(), nullptr, 1, d, eps);
-        linear_fp16(h.data(), emb, logits.data(), 1, d, V);  // tied lm_head, fp16
+        linear_fp16(h.data(), head, logits.data(), 1, d, V);  // lm_head, fp16
+        if (logits_scaling != 1.0f) {
+            const float inv = 1.0f / logits_scaling;
+            for (int i = 0; i < V; ++i) logits[(size_t)i] *= inv;
+        }
     };
 
     // ---- prefill (generator.cpp:627-915)
@@ -1109,6 +1151,7 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
         std::vector<float> x((size_t)P * d), xb((size_t)P * d), pr((size_t)P * d), q((size_t)P * qd),
             k((size_t)P * kvd), v((size_t)P * kvd), att((size_t)P * qd);
         orc_embedding_forward_half(prompt, emb, x.data(), P, d, V);
+        scale_emb(x.data(), x.size());
         for (int l = 0; l < L; ++l) {
             const std::string pre = "layers." + std::to_string(l) + ".";
             rmsnorm(x.data(), F(pre + "attn_norm"), xb.data(), nullptr, P, d, eps);
@@ -1125,10 +1168,10 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
                 attn_prefill(q.data(), k.data(), v.data(), att.data(), 1, P, H, KV, hd, scale, 0);
                 lin(pre + "wo", att.data(), pr.data(), P, qd, d);
             }
-            for (size_t i = 0; i < x.size(); ++i) x[i] += pr[i];
+            add_branch(x.data(), pr.data(), x.size());
             rmsnorm(x.data(), F(pre + "ffn_norm"), xb.data(), nullptr, P, d, eps);
             moe(l, xb.data(), pr.data(), P);
-            for (size_t i = 0; i < x.size(); ++i) x[i] += pr[i];
+            add_branch(x.data(), pr.data(), x.size());
         }
         len = P;
         finish(x.data() + (size_t)(P - 1) * d);
@@ -1147,8 +1190,11 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
         }
         out_ids[step] = next;
         out_margins[step] = best - second;
+        if (out_logits) std::memcpy(out_logits + (size_t)step * V, logits.data(), sizeof(float) * (size_t)V);
         if (step == n_new - 1) break;
-        orc_embedding_forward_half(&next, emb, x.data(), 1, d, V);
+        const i32 fed = forced ? forced[step] : next;
+        orc_embedding_forward_half(&fed, emb, x.data(), 1, d, V);
+        scale_emb(x.data(), x.size());
         const int slot = len;  // ring never wraps: P + n_new <= max_ctx
         ++len;
         for (int l = 0; l < L; ++l) {
@@ -1169,10 +1215,10 @@ int orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const char
                             scale, 0, [](u16 h) { return f16_to_f32(h); });
                 lin(pre + "wo", att.data(), pr.data(), 1, qd, d);
             }
-            for (int i = 0; i < d; ++i) x[(size_t)i] += pr[(size_t)i];
+            add_branch(x.data(), pr.data(), (size_t)d);
             rmsnorm(x.data(), F(pre + "ffn_norm"), xb.data(), nullptr, 1, d, eps);
             moe(l, xb.data(), pr.data(), 1);
-            for (int i = 0; i < d; ++i) x[(size_t)i] += pr[(size_t)i];
+            add_branch(x.data(), pr.data(), (size_t)d);
         }
         finish(x.data());
     }

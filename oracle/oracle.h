@@ -100,6 +100,13 @@ int  orc_granite_generate_timed(const int32_t* cfg, const float* fcfg, const cha
                                 const void** ptrs, int nparams, const int32_t* prompt, int P,
                                 int n_new, int max_ctx, int32_t* out_ids, float* out_margins,
                                 double* seconds);
+/* General form: optional Granite fields past cfg[16+L] / fcfg[2] (tie_embeddings, moe_aux_free;
+ * embedding_multiplier, residual_multiplier, logits_scaling), teacher forcing (forced: the id fed
+ * at each step, NULL = greedy) and the per-step logits (out_logits [n_new x V], may be NULL). */
+int  orc_granite_generate_ex(const int32_t* cfg, int ncfg, const float* fcfg, int nfcfg, const char** names,
+                             const void** ptrs, int nparams, const int32_t* prompt, int P, int n_new,
+                             int max_ctx, const int32_t* forced, int32_t* out_ids, float* out_margins,
+                             float* out_logits, double* seconds);
 
 #ifdef __cplusplus
 }

@@ -153,11 +153,38 @@ int ref_granite_generate(const i32* cfg, const float* fcfg, const char** names, 
                                       out_margins, nullptr);
 }
 
+int ref_granite_generate_ex(const i32* cfg, int ncfg, const float* fcfg, int nfcfg, const char** names,
+                            const void** ptrs, int nparams, const i32* prompt, int P, int n_new, int max_ctx,
+                            const i32* forced, i32* out_ids, float* out_margins, float* out_logits, double* seconds);
+
 // seconds (optional): [0] prefill wall time, [1] wall time of the n_new-1
 // decode steps (Generator::decode_step on the host path).
 int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** names, const void** ptrs, int nparams,
                                const i32* prompt, int P, int n_new, int max_ctx, i32* out_ids, float* out_margins,
                                double* seconds) {
+    return ref_granite_generate_ex(cfg, 16 + cfg[2], fcfg, 2, names, ptrs, nparams, prompt, P, n_new, max_ctx,
+                                   nullptr, out_ids, out_margins, nullptr, seconds);
+}
+
+// The optional Granite fields of orc_granite_generate_ex (oracle/oracle.h) set on the
+// reference ModelConfig: tie_embeddings, moe_aux_free (router biases from parameters named
+// "layers.N.moe_bias" through Model::set_moe_bias, as load_model_from_gguf does), and the
+// embedding / residual multipliers and logits scaling.
+static void granite_options(ModelConfig& c, const i32* cfg, int ncfg, const float* fcfg, int nfcfg) {
+    const int L = cfg[2];
+    c.tie_embeddings = ncfg > 16 + L ? cfg[16 + L] != 0 : true;
+    c.moe_aux_free = ncfg > 17 + L ? cfg[17 + L] != 0 : false;
+    if (c.moe_aux_free) c.moe_aux_scale = 0.0f;  // model/model.cpp:388 (no aux-loss term with the bias)
+    if (nfcfg > 2) c.embedding_multiplier = fcfg[2];
+    if (nfcfg > 3) c.residual_multiplier = fcfg[3];
+    if (nfcfg > 4) c.logits_scaling = fcfg[4];
+}
+
+// forced (optional): the id fed at each step instead of the greedy one (out_ids
+// keeps the greedy id); out_logits (optional, n_new x V): the host logits of each step.
+int ref_granite_generate_ex(const i32* cfg, int ncfg, const float* fcfg, int nfcfg, const char** names,
+                            const void** ptrs, int nparams, const i32* prompt, int P, int n_new, int max_ctx,
+                            const i32* forced, i32* out_ids, float* out_margins, float* out_logits, double* seconds) {
     try {
         ModelConfig c;
         c.arch = ModelConfig::ArchGranite;
@@ -186,6 +213,7 @@ int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** n
         c.intermediate_size = cfg[6];
         c.max_seq_len = max_ctx;
         c.tie_embeddings = true;
+        granite_options(c, cfg, ncfg, fcfg, nfcfg);
         const int qkind = cfg[15];
         Model m(c, Device::CPU, false, qkind);
         std::map<std::string, const void*> pm;
@@ -194,6 +222,12 @@ int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** n
             auto it = pm.find(p->name);
             if (it == pm.end()) return -3;
             std::memcpy(p->w.data_ptr(), it->second, p->w.nbytes());
+        }
+        if (c.moe_aux_free) {
+            for (int l = 0; l < c.num_layers; ++l) {
+                auto it = pm.find("layers." + std::to_string(l) + ".moe_bias");
+                if (it != pm.end()) m.set_moe_bias(l, (const float*)it->second, (size_t)c.num_experts);
+            }
         }
         ops::set_fused_q4(true);
         Tokenizer tok;
@@ -215,9 +249,11 @@ int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** n
             }
             out_ids[step] = next;
             out_margins[step] = best - second;
+            if (out_logits) std::memcpy(out_logits + (size_t)step * V, lg, sizeof(float) * (size_t)V);
             if (step == n_new - 1) break;
-            g.push_history(next);
-            g.decode_step(next, (int)g.absolute_pos_);
+            const i32 fed = forced ? forced[step] : next;
+            g.push_history(fed);
+            g.decode_step(fed, (int)g.absolute_pos_);
             ++g.absolute_pos_;
         }
         if (seconds) seconds[1] = td.seconds();
@@ -231,8 +267,15 @@ int ref_granite_generate_timed(const i32* cfg, const float* fcfg, const char** n
 // The parameter table the reference Model allocates for a config: names,
 // element counts and storage dtypes (core/dtype.h:9-21 numbering), so the
 // fixture writer fills exactly the tensors the reference expects.
+int ref_granite_param_table_ex(const i32* cfg, int ncfg, const float* fcfg, int nfcfg, int max_ctx,
+                               char* names_out, int names_cap, i64* numel_out, i32* dtype_out, int cap);
 int ref_granite_param_table(const i32* cfg, const float* fcfg, int max_ctx, char* names_out, int names_cap,
                             i64* numel_out, i32* dtype_out, int cap) {
+    return ref_granite_param_table_ex(cfg, 16 + cfg[2], fcfg, 2, max_ctx, names_out, names_cap, numel_out, dtype_out,
+                                      cap);
+}
+int ref_granite_param_table_ex(const i32* cfg, int ncfg, const float* fcfg, int nfcfg, int max_ctx,
+                               char* names_out, int names_cap, i64* numel_out, i32* dtype_out, int cap) {
     ModelConfig c;
     c.arch = ModelConfig::ArchGranite;
     c.vocab_size = cfg[0]; c.hidden_size = cfg[1]; c.num_layers = cfg[2]; c.num_heads = cfg[3];
@@ -243,6 +286,7 @@ int ref_granite_param_table(const i32* cfg, const float* fcfg, int max_ctx, char
     c.layer_types.assign(cfg + 16, cfg + 16 + cfg[2]); c.position_embedding = 1; c.rms_eps = fcfg[0];
     c.attention_multiplier = fcfg[1]; c.intermediate_size = cfg[6]; c.max_seq_len = max_ctx;
     c.tie_embeddings = true;
+    granite_options(c, cfg, ncfg, fcfg, nfcfg);
     Model m(c, Device::CPU, false, cfg[15]);
     int i = 0, off = 0;
     for (Parameter* p : m.parameters()) {

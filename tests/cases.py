@@ -4,6 +4,21 @@ import numpy as np
 
 import oracle_lib as O
 
+# c1 with the Granite-4.0 fields a real checkpoint sets: an untied fp16 lm_head, per-layer
+# aux-free router biases, embedding / residual multipliers and logits scaling
+# (tests/golden/granite_c1_q8_opts.npz is the compiled reference Generator on it, Q8_0).
+C1_OPTS = dict(O.C1, tied=0, aux_free=1, emb_mult=12.0, res_mult=0.22, logits_scaling=8.0)
+
+
+def granite_opts_weights(qkind=2):
+    """Synthetic weights of C1_OPTS (the shared recipe) with router biases N(0, 0.05)
+    (seeds 90 + layer) in place of the recipe's zeros."""
+    w = O.granite_weights(C1_OPTS, qkind, seed=0)
+    for layer in range(C1_OPTS["L"]):
+        w[f"layers.{layer}.moe_bias"] = O.rng_normal(90 + layer, C1_OPTS["ne"], 0, 0.05)
+    return w
+
+
 # BASELINE config 1 benched workload (bench.py): 128-token prompt + 64 greedy tokens.
 C1_PROMPT, C1_NEW, C1_MAX_CTX = 128, 64, 256
 

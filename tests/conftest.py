@@ -60,9 +60,11 @@ def close(a, b, tol):
     <= tol AND elementwise relative error <= elem_tol(tol) on the entries with
     |b| >= 10 % of max|b|. The elementwise bound is looser than tol because
     the reference's CPU path rounds every dequantised weight to fp16
-    (core/ops.cpp:304-338) while the GPU multiplies the exact codes, which
-    alone moves a single output by ~2^-12 of its row's scale; chained layers
-    add up such differences."""
+    (core/ops.cpp:304-338) while the GPU multiplies the exact codes:
+    tests/test_gpu_exact.py measures the GPU within 2e-4 elementwise of the
+    float64 product over the exact weights and the oracle further away than
+    that, and chained layers (a model step's logits) add such differences up to
+    about 5.6e-3 elementwise at the 1e-3 normwise level."""
     n = relerr(a, b)
     e = elemerr(a, b, 0.1)
     assert n <= tol, f"normwise rel-err {n:.3g} > {tol:g}"
@@ -71,7 +73,7 @@ def close(a, b, tol):
 
 
 def elem_tol(tol):
-    return 10 * tol if tol <= 1e-3 else 3 * tol
+    return 7.5 * tol if tol <= 1e-3 else 3 * tol
 
 
 def pytest_sessionfinish(session, exitstatus):

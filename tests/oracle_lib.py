@@ -18,10 +18,24 @@ C1 = dict(V=4096, d=512, L=6, H=8, KV=2, hd=64, E=256, ne=8, K=2, SH=512, d_inne
           eps=1e-5, scale=0.125)
 
 
+OPTION_KEYS = ("tied", "aux_free", "emb_mult", "res_mult", "logits_scaling")
+
+
+def has_options(c):
+    return any(k in c for k in OPTION_KEYS)
+
+
 def granite_cfg(c, qkind):
+    """(ints, floats) of a config. With any of the optional Granite fields in c
+    (tied, aux_free, emb_mult, res_mult, logits_scaling) both arrays carry the
+    extended layout: ints + [tied, aux_free], floats + [emb, res, logits]."""
     ints = [c["V"], c["d"], c["L"], c["H"], c["KV"], c["hd"], c["E"], c["ne"], c["K"], c["SH"],
             c["d_inner"], c["m_heads"], c["m_dhead"], c["m_dstate"], c["conv_k"], qkind] + list(c["layer_types"])
-    return np.array(ints, dtype=np.int32), np.array([c["eps"], c["scale"]], dtype=np.float32)
+    fl = [c["eps"], c["scale"]]
+    if has_options(c):
+        ints += [int(c.get("tied", 1)), int(c.get("aux_free", 0))]
+        fl += [c.get("emb_mult", 1.0), c.get("res_mult", 1.0), c.get("logits_scaling", 1.0)]
+    return np.array(ints, dtype=np.int32), np.array(fl, dtype=np.float32)
 
 
 def P(a):
@@ -185,7 +199,11 @@ def granite_param_specs(c):
                   (pre + "moe_up", ne * E * d, "q"), (pre + "moe_down", ne * d * E, "q"),
                   (pre + "moe_sh_gate", SH * d, "q"), (pre + "moe_sh_up", SH * d, "q"),
                   (pre + "moe_sh_down", d * SH, "q")]
+        if c.get("aux_free", 0):
+            specs.append((pre + "moe_bias", ne, "f32"))
     specs.append(("final_norm", d, "f32"))
+    if not c.get("tied", 1):
+        specs.append(("lm_head", c["V"] * d, "f16"))
     return specs
 
 
@@ -208,6 +226,22 @@ def _param_arrays(weights):
     arr_names = (C.c_char_p * len(names))(*[n.encode() for n in names])
     arr_ptrs = (C.c_void_p * len(names))(*[weights[n].ctypes.data for n in names])
     return arr_names, arr_ptrs, len(names)
+
+
+def granite_generate_ex(lib_fn, c, qkind, weights, prompt, n_new, max_ctx=256, forced=None, logits=False):
+    """orc_granite_generate_ex / ref_granite_generate_ex: (ids, margins, logits or None).
+    forced: ids fed at each step instead of the greedy ones (teacher forcing)."""
+    cfg, fcfg = granite_cfg(c, qkind)
+    names, ptrs, n = _param_arrays(weights)
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    ids = np.zeros(n_new, np.int32)
+    margins = np.zeros(n_new, np.float32)
+    lg = np.zeros((n_new, c["V"]), np.float32) if logits else None
+    fo = None if forced is None else np.ascontiguousarray(forced, np.int32)
+    rc = lib_fn(P(cfg), len(cfg), P(fcfg), len(fcfg), names, ptrs, n, P(prompt), len(prompt), n_new, max_ctx, P(fo),
+                P(ids), P(margins), P(lg), None)
+    assert rc == 0, rc
+    return ids, margins, lg
 
 
 def granite_generate(lib_fn, c, qkind, weights, prompt, n_new, max_ctx=256):

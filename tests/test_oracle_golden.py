@@ -317,6 +317,51 @@ def test_granite_greedy_golden():
     assert np.array_equal(bits(margins), bits(g["margins"][:8]))
 
 
+def test_granite_options_golden():
+    """The oracle generator with the Granite-4.0 fields (untied lm_head, aux-free router
+    biases, embedding / residual multipliers, logits scaling) reproduces the compiled
+    reference Generator bit for bit: ids, margins and every step's logits (first 10
+    steps here; the GPU tests take all 24)."""
+    import cases
+    g = golden("granite_c1_q8_opts")
+    w = cases.granite_opts_weights()
+    ids, margins, lg = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, cases.C1_OPTS, 2, w, g["prompt"],
+                                             10, max_ctx=int(g["max_ctx"]), logits=True)
+    assert np.array_equal(ids, g["ids"][:10])
+    assert np.array_equal(bits(margins), bits(g["margins"][:10]))
+    assert np.array_equal(bits(lg), bits(g["logits"][:10]))
+    assert np.array_equal(np.stack([w[f"layers.{i}.moe_bias"] for i in range(6)]), g["moe_bias"])
+
+
+def test_granite_options_change_the_result():
+    """Each option moves the logits (so the fixture above pins each of them): the same
+    weights with one option reset to its default give different first logits."""
+    import cases
+    g = golden("granite_c1_q8_opts")
+    w = cases.granite_opts_weights()
+    prompt = g["prompt"][:16]
+    base = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, cases.C1_OPTS, 2, w, prompt, 1, max_ctx=64,
+                                 logits=True)[2]
+    for key, default in (("emb_mult", 1.0), ("res_mult", 1.0), ("logits_scaling", 1.0)):
+        c = dict(cases.C1_OPTS, **{key: default})
+        other = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, c, 2, w, prompt, 1, max_ctx=64,
+                                      logits=True)[2]
+        assert not np.array_equal(other, base), key
+    wz = dict(w)
+    for i in range(6):
+        wz[f"layers.{i}.moe_bias"] = np.zeros(8, np.float32)
+    other = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, cases.C1_OPTS, 2, wz, prompt, 1, max_ctx=64,
+                                  logits=True)[2]
+    assert not np.array_equal(other, base), "moe_bias"
+    wt = dict(w)
+    wt["lm_head"] = w["tok_embeddings"]
+    other = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, cases.C1_OPTS, 2, wt, prompt, 1, max_ctx=64,
+                                  logits=True)[2]
+    tied = O.granite_generate_ex(O.oracle().orc_granite_generate_ex, dict(cases.C1_OPTS, tied=1), 2, w, prompt, 1,
+                                 max_ctx=64, logits=True)[2]
+    assert not np.array_equal(other, base) and np.array_equal(other, tied), "lm_head"
+
+
 def _orc_topk(lg, K):
     vals = np.zeros(K, np.float32)
     ids = np.zeros(K, np.int32)
@@ -362,3 +407,37 @@ def test_rep_penalties_closed_forms():
     o = x.copy()  # neutral settings leave the logits alone
     O.oracle().orc_apply_rep_penalties(P(o), V, P(hist), len(hist), O.f(1.0), O.f(0.0), O.f(0.0))
     assert np.array_equal(bits(o), bits(x))
+
+
+@pytest.mark.parametrize("kind", [2, 3])
+def test_exact_decoder_agrees_with_oracle(kind):
+    """The float64 block decoder of tests/exact.py (written from the block layouts) and
+    the oracle's fp32 decode agree to the fp32 rounding of the oracle's arithmetic
+    (Q8_0: q * d is exact in fp32, so bit-exact), hand-built blocks included."""
+    import exact
+    n = 256 * 64
+    x = O.rng_normal(61, n, 0, 0.5)
+    q = O.quantize(kind, x)
+    ex = exact.dequant(kind, q, n)
+    orc = O.dequantize(kind, q, n).astype(np.float64)
+    if kind == 2:
+        assert np.array_equal(ex, orc)
+    else:
+        assert np.max(np.abs(ex - orc) / np.maximum(np.abs(ex), 1e-30)) < 2.0 ** -22
+        # a hand-built block: d = 1, dmin = 0.5, scale j = j + 1, min j = 2 j, code = (i % 16)
+        blk = np.zeros(144, np.uint8)
+        blk[0:2] = np.array([1.0], np.float16).view(np.uint8)
+        blk[2:4] = np.array([0.5], np.float16).view(np.uint8)
+        sc, mn = np.arange(1, 9), 2 * np.arange(8)
+        s12 = np.zeros(12, np.int64)
+        for j in range(4):
+            s12[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+            s12[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+            s12[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+        blk[4:16] = s12.astype(np.uint8)
+        codes = np.arange(256) % 16
+        for i in range(4):
+            blk[16 + 32 * i: 48 + 32 * i] = codes[64 * i: 64 * i + 32] | (codes[64 * i + 32: 64 * i + 64] << 4)
+        want = np.array([(j + 1) * codes[32 * j + t] - 0.5 * 2 * j for j in range(8) for t in range(32)], np.float64)
+        assert np.array_equal(exact.dequant_q4_k(blk, 256), want)
+        assert np.array_equal(O.dequantize(3, blk, 256).astype(np.float64), want)
