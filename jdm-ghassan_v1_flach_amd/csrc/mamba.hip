@@ -9,11 +9,12 @@
 //   y_t = sum_{tau<=t} (C_t.B_tau) e^(cum_t-cum_tau) dt_tau x_tau
 //         + e^(cum_t) C_t S_in + D x_t
 //   S_out = e^(cum_end) S_in + sum_tau e^(cum_end-cum_tau) dt_tau x_tau B_tau^T
-// in four launches: G = C B^T per chunk (shared by all heads), the per-chunk
-// state contributions dS on the matrix cores, a wave-level pass carrying the
-// state across chunks, and the chunk outputs (intra-chunk M X and the
-// C S_in correction on the matrix cores). Decode is one fused conv+update
-// kernel between the two projections.
+// in three launches: (1) G = C B^T per chunk (shared by all heads, fp16) beside
+// the per-chunk state contributions dS on the matrix cores; (2) a pass carrying
+// the state across chunks (S_in of every chunk, fp16); (3) per (chunk, head,
+// half of the p columns) the chunk's outputs (intra-chunk M X and the C S_in
+// correction on the matrix cores), reading X once.
+// Decode is one fused conv+update kernel between the two projections.
 #include "gemv_fuse.h"
 
 namespace gh {
@@ -107,10 +108,18 @@ __device__ __forceinline__ void ssd_prep_wave(const float* __restrict__ dt_in, i
 // G[c][t][tau] = C_t . B_tau inside chunk c: 64x64 tiles, 4 waves x 32x32 on
 // the matrix cores (fp16 operands, fp32 accumulation; G only enters the
 // scan as an fp16 operand). C and B rows are staged into LDS with 16-byte loads.
+// G and the fp16 C rows are written in MFMA-fragment order, the layout in which the chunk
+// outputs take them as A operands: fragment (chunk c, 32-row block rb, 16-column step ks) is
+// 64 lanes x 8 halves, lane (r, kh) holding row 32 rb + r, columns 16 ks + 8 kh .. + 7; one
+// fragment is one contiguous 1 KB load for a wave (a row-major layout makes each lane of that
+// load touch a different row).
+__device__ __forceinline__ size_t ssd_frag(int c, int rb, int ks, int nrb, int nks) {
+    return (((size_t)c * nrb + rb) * nks + ks) * 512;
+}
 template <int N>
 __device__ __forceinline__ void ssd_cb_block(const float* __restrict__ Bm, const float* __restrict__ Cm, int ld,
-                                             float* __restrict__ G, int T, int L, int c, int ti, int si,
-                                             _Float16* sC, _Float16* sB) {
+                                             _Float16* __restrict__ G, _Float16* __restrict__ C16, int T, int L,
+                                             int c, int ti, int si, _Float16* sC, _Float16* sB) {
     constexpr int SN = N + 8;
     const int t0 = c * L, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int e = threadIdx.x; e < 64 * N / 4; e += 256) {
@@ -135,11 +144,26 @@ __device__ __forceinline__ void ssd_cb_block(const float* __restrict__ Bm, const
         const f16x8 a = *(const f16x8*)(sC + (wt + (lane & 31)) * SN + ko);
         const f16x8 b = *(const f16x8*)(sB + (ws + (lane & 31)) * SN + ko);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+        // the A operand is exactly a C fragment: the si = 0 tiles write the chunk's C rows once
+        // (rows past the sequence end are zeros), shared by every head's chunk outputs
+        if (si == 0 && ws == 0) *(f16x8*)(C16 + ssd_frag(c, (ti + wt) / 32, ks, L / 32, N / 16) + 8 * lane) = a;
     }
+    // G tile -> LDS [t][tau] fp16 (sC is free once every wave has its operands), then out in
+    // fragment order, 16 bytes per store
+    constexpr int ST = 64 + 8;
+    _Float16* sT = sC;
+    __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        const int t = ti + wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), sc = si + ws + (lane & 31);
-        if (t < L && sc < L) G[((size_t)c * L + t) * L + sc] = acc[e];
+        const int tl = wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), sl = ws + (lane & 31);
+        sT[tl * ST + sl] = (_Float16)acc[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int q = threadIdx.x + 256 * j, rbl = q >> 8, ksl = (q >> 6) & 3, ln = q & 63;
+        const f16x8 v = *(const f16x8*)(sT + (32 * rbl + (ln & 31)) * ST + 16 * ksl + 8 * (ln >> 5));
+        *(f16x8*)(G + ssd_frag(c, ti / 32 + rbl, si / 16 + ksl, L / 32, L / 16) + 8 * ln) = v;
     }
 }
 
@@ -189,8 +213,9 @@ template <int W>
 struct Stage64 {
     static constexpr int Q = W / 4, G = 256 / Q, R = 64 / G;
     float4 v[R];
-    __device__ __forceinline__ void load(const float* __restrict__ src, int ld, int nvalid) {
-        const int cq = threadIdx.x % Q, g = threadIdx.x / Q;
+    __device__ __forceinline__ void load(const float* __restrict__ src, int ld, int nvalid, int ltid = -1) {
+        const int tx = ltid < 0 ? (int)threadIdx.x : ltid;
+        const int cq = tx % Q, g = tx / Q;
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const int r = g * R + i;
@@ -198,8 +223,9 @@ struct Stage64 {
         }
     }
     template <int S>
-    __device__ __forceinline__ void store(_Float16* dst, const float* sw) const {
-        const int cq = threadIdx.x % Q, g = threadIdx.x / Q;
+    __device__ __forceinline__ void store(_Float16* dst, const float* sw, int ltid = -1) const {
+        const int tx = ltid < 0 ? (int)threadIdx.x : ltid;
+        const int cq = tx % Q, g = tx / Q;
         typedef _Float16 hrun __attribute__((ext_vector_type(R)));
         hrun h0, h1, h2, h3;
 #pragma unroll
@@ -230,18 +256,17 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
                                                       int ldb, const float* __restrict__ dt_in, int dt_ld,
                                                       const float* __restrict__ dt_bias, const float* __restrict__ A_in,
                                                       const float* __restrict__ a_log, float* __restrict__ dt,
-                                                      float* __restrict__ cum, float* __restrict__ G,
-                                                      float* __restrict__ dS, float* __restrict__ decay, int T,
-                                                      int H, int L, float* __restrict__ state,
-                                                      float* __restrict__ Sin) {
+                                                      float* __restrict__ cum, _Float16* __restrict__ G,
+                                                      _Float16* __restrict__ C16, float* __restrict__ dS,
+                                                      float* __restrict__ decay, int T, int H, int L) {
     constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
     constexpr int U_STATE = (P * S + N * S) * 2, U_CB = 2 * 64 * SN * 2;
     __shared__ __attribute__((aligned(16))) unsigned char smem[U_STATE > U_CB ? U_STATE : U_CB];
     const int nch = (T + L - 1) / L;
     if ((int)blockIdx.x >= nch * H) {
         const int b = blockIdx.x - nch * H, nt = L / 64;
-        ssd_cb_block<N>(Bm, Cm, ldb, G, T, L, b / (nt * nt), (b / nt) % nt * 64, b % nt * 64, (_Float16*)smem,
-                        (_Float16*)smem + 64 * SN);
+        ssd_cb_block<N>(Bm, Cm, ldb, G, C16, T, L, b / (nt * nt), (b / nt) % nt * 64, b % nt * 64,
+                        (_Float16*)smem, (_Float16*)smem + 64 * SN);
         return;
     }
     _Float16* sX = (_Float16*)smem;  // [p][tau]
@@ -299,8 +324,6 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
         }
     }
     float* out = dS + ((size_t)c * H + h) * P * N;
-    // one chunk (state != null): the inter-chunk pass of this head right here, k_ssd_state_pass's
-    // arithmetic: S_in = state, state = state * decay + dS
     const float dec = expf(cend);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -310,218 +333,226 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
         for (int e = 0; e < 16; ++e) {
             const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
             const int n = nt * 32 + (lane & 31);
-            if (state) {
-                const size_t si = ((size_t)h * P + p) * N + n;
-                const float s0 = state[si];
-                Sin[si] = s0;
-                state[si] = s0 * dec + acc[i][e];
-            } else {
-                out[(size_t)p * N + n] = acc[i][e];
-            }
+            out[(size_t)p * N + n] = acc[i][e];
         }
     }
     if (threadIdx.x == 0) decay[(size_t)c * H + h] = dec;
 }
 
-// Inter-chunk pass: S_in[c] = state before chunk c; state <- S_in*decay + dS.
-// One thread per (h, p, n): the recurrence over chunks is serial, the
-// elements are independent and their loads coalesce.
-__global__ void k_ssd_state_pass(float* __restrict__ state, const float* __restrict__ dS,
-                                 const float* __restrict__ decay, float* __restrict__ Sin, int nchunks, int H,
-                                 int PN) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (int64_t)H * PN) return;
-    const int h = (int)(i / PN);
-    float s = state[i];
-    // the loads of 8 chunks go out together; only the recurrence is serial
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
-        float dv[8], dc[8];
+// Inter-chunk pass: S_in[c] = the state entering chunk c (written as fp16, the chunk outputs
+// MFMA operand), S <- S * decay[c] + dS[c] in fp32 from the incoming state, the final state
+// written back. A thread carries 4 consecutive (h, p, n) elements; the dS of all chunks are
+// requested before the first step (only the recurrence is serial).
+__global__ void __launch_bounds__(256) k_ssd_state_pass(float* __restrict__ state, const float* __restrict__ dS,
+                                                        const float* __restrict__ decay, _Float16* __restrict__ Sin16,
+                                                        int nch, int H, int PN) {
+    const int64_t i4 = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index into [H][PN]
+    if (i4 >= (int64_t)H * PN / 4) return;
+    const int h = (int)(4 * i4 / PN);
+    float4 s = ((const float4*)state)[i4];
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        float4 dv[16];
+        float dc[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
             const int c = c0 + j;
-            dv[j] = c < nchunks ? dS[(size_t)c * H * PN + i] : 0.f;
-            dc[j] = c < nchunks ? decay[(size_t)c * H + h] : 0.f;
+            if (c < nch) {
+                dv[j] = ((const float4*)(dS + (size_t)c * H * PN))[i4];
+                dc[j] = decay[(size_t)c * H + h];
+            }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
             const int c = c0 + j;
-            if (c < nchunks) {
-                Sin[(size_t)c * H * PN + i] = s;
-                s = s * dc[j] + dv[j];
+            if (c < nch) {
+                f16x4 hv;
+                hv[0] = (_Float16)s.x; hv[1] = (_Float16)s.y; hv[2] = (_Float16)s.z; hv[3] = (_Float16)s.w;
+                ((f16x4*)(Sin16 + (size_t)c * H * PN))[i4] = hv;
+                s = make_float4(s.x * dc[j] + dv[j].x, s.y * dc[j] + dv[j].y, s.z * dc[j] + dv[j].z,
+                                s.w * dc[j] + dv[j].w);
             }
         }
     }
-    state[i] = s;
+    ((float4*)state)[i4] = s;
 }
 
 // Chunk outputs: y[t][p] = sum_{tau<=t} G[t][tau] e^(cum_t-cum_tau) dt_tau x_tau[p]
-//                 + e^(cum_t) sum_n C_t[n] S_in[p][n] + D x_t[p].
-// Block = (chunk, head, 64-row t tile): 4 waves x (32 t rows x 32 p cols),
-// MFMA 32x32x16 with fp16 operands and fp32 accumulation. Every operand goes
-// through LDS with coalesced 16-byte loads: the C rows (pre-scaled by
-// e^(cum_t)) with S_in for the inter-chunk term, then per 64-wide tau tile the
-// decay-masked A = G e^(cum_t-cum_tau) dt_tau (fp16) with X^T. G and C are the
-// same for every head, so head h walks the tau tiles from tile h mod ntk (the
-// blocks of one chunk then do not all read the same lines at once).
+//                         + e^(cum_t) sum_n C_t[n] S_in[p][n] + D x_t[p].
+// A block takes one (chunk, head) and one half of its 64 p columns, all 256 rows: it reads
+// the chunk's X columns once (a block per 64-row tile re-read the X rows, G rows and S_in
+// each tile needed), and two blocks fit a CU, so one block's loads overlap the other's
+// compute. X^T [p][tau] and S_in [p][n] of the block's columns sit in LDS as fp16 (the MFMA B
+// operands), D x in fp32 for the epilogue; the A operands come straight from the fp16 G / C
+// fragments in global memory (shared by all heads, one contiguous 1 KB load per wave and
+// step) and are weighted in registers. Wave w owns the 32-row block w (32 t rows x 32 p, one
+// 32x32 MFMA tile, fp32 accumulation). The decay factor is split per 16-position step (one
+// exponential per row and step rather than per element).
 template <int N>
-__global__ void __launch_bounds__(256) k_ssd_chunk_out(const float* __restrict__ xs, int ldx,
-                                                       const float* __restrict__ Cm, int ldc,
-                                                       const float* __restrict__ G, const float* __restrict__ dt,
-                                                       const float* __restrict__ cum, const float* __restrict__ Sin,
-                                                       const float* __restrict__ D, float* __restrict__ y, int ldy,
-                                                       int T, int H, int L) {
-    constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
-    // phase 1 (inter-chunk term): sC [t][n] and sS [p][n]; phase 2: sA [t][tau] and sXt [p][tau]
-    // sDx [t][p] fp32: D x_t of the block's rows, kept from the diagonal tile's X rows for the
-    // epilogue (after sA / sXt; no second read of X)
-    constexpr int U1 = (64 * SN + P * SN) * 2, U2 = (64 * S + P * S) * 2, U3 = U2 + 64 * P * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[U1 > U3 ? U1 : U3];
-    float* sDx = (float*)(smem + U2);
-    _Float16* sC = (_Float16*)smem;
-    _Float16* sS = sC + 64 * SN;
-    _Float16* sA = (_Float16*)smem;
-    _Float16* sXt = sA + 64 * S;
-    __shared__ float scum[TK], sdt[TK], srow[64];
-    const int c = blockIdx.x, h = blockIdx.y, tt = blockIdx.z * 64;
+__global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, int ldx,
+                                                 const _Float16* __restrict__ C16, const _Float16* __restrict__ G,
+                                                 const float* __restrict__ dt, const float* __restrict__ cum,
+                                                 const _Float16* __restrict__ Sin16, const float* __restrict__ D,
+                                                 float* __restrict__ y, int ldy, int T, int H, int L) {
+    constexpr int P = 64, PH = 32, PN = P * N, SX = 256 + 8, SS = N + 8, SD = PH + 4;
+    __shared__ __attribute__((aligned(16))) _Float16 sXt[PH * SX];
+    __shared__ __attribute__((aligned(16))) _Float16 sS[PH * SS];
+    __shared__ __attribute__((aligned(16))) float sDx[256 * SD];
+    __shared__ float scum[256], sdt[256], sw[256];
+    __shared__ int sfast[16];
+    const int nch = (T + L - 1) / L, nitems = nch * H;
+    // block b -> item (chunk, head) and p half: the two halves of an item are blocks b and b + 8,
+    // which the dispatcher places on the same XCD (one L2 for the shared G / C / X reads)
+    const int b = blockIdx.x, it = (b / 16) * 8 + (b % 8), ph = (b / 8) % 2;
+    if (it >= nitems) return;
+    const int c = nch - 1 - it / H, h = it % H, pc0 = PH * ph;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = c * L, len = min(L, T - t0);
-    if (tt >= len) return;
-    const int wt = (wave >> 1) * 32, wp = (wave & 1) * 32;  // wave tile: t rows tt+wt.., p cols wp..
-    const int ar = wt + (lane & 31);                          // A-operand row (local) of this lane
-    if (tid < 64) srow[tid] = tt + tid < len ? cum[(size_t)(t0 + tt + tid) * H + h] * 1.4426950408889634f : 0.f;
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int rb = wave, kh = 8 * (lane >> 5), col = lane & 31;
+    const bool active = 32 * rb < len;  // wave-uniform
+    const int t = 32 * rb + col;        // this lane's A row (chunk-local)
+    const bool trow = t < len;
+    const int nk = 2 * (rb + 1);        // 16-wide tau steps of the causal range
+
+    // ---- this wave's C fragments and the first 8 G fragments of its causal range, requested first
+    f16x8 craw[N / 16], graw[8];
+    const _Float16* gr = G + ssd_frag(c, rb, 0, L / 32, L / 16) + 8 * lane;
+    if (active) {
+        const _Float16* cr = C16 + ssd_frag(c, rb, 0, L / 32, N / 16) + 8 * lane;
+#pragma unroll
+        for (int ks = 0; ks < N / 16; ++ks) craw[ks] = *(const f16x8*)(cr + 512 * ks);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+            if (ks < nk) graw[ks] = *(const f16x8*)(gr + 512 * ks);
+    }
+    // ---- block staging: the chunk's X rows, columns pc0 .. pc0 + 31 -> X^T [p][tau] fp16 and
+    // D x [tau][p] fp32; S_in rows pc0 .. -> sS [p][n]; cum (log2 units) / dt
+    {
+        const int cq = tid % 8, g = tid / 8;  // 4 columns, rows 4 g .. 4 g + 3
+        float4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i;
+            v[i] = r < len ? *(const float4*)(xs + (size_t)(t0 + r) * ldx + h * P + pc0 + 4 * cq)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const uint2* src = (const uint2*)(Sin16 + ((size_t)c * H + h) * PN + (size_t)pc0 * N);
+        constexpr int SJ = PH * N / 4 / 512;  // uint2 (4 halves) per thread
+        uint2 sv[SJ];
+#pragma unroll
+        for (int j = 0; j < SJ; ++j) sv[j] = src[tid + 512 * j];
+        if (tid < L) {
+            // e^(cum_t - cum_tau) = e^(cum_t - r_s) e^(r_s - cum_tau) with r_s = cum at the first
+            // position of tau's 16-step: the second factor (times dt_tau) is sw[tau], the first is
+            // one exponential per (row, step). A step whose decay spread makes e^(r_s - cum_tau)
+            // too large for fp32 marks its row blocks for the element-by-element form.
+            const int s0 = tid & ~15, s15 = s0 + 15;
+            const float cv = tid < len ? cum[(size_t)(t0 + tid) * H + h] * LOG2E : 0.f;
+            const float rs = s0 < len ? cum[(size_t)(t0 + s0) * H + h] * LOG2E : 0.f;
+            const float d = tid < len ? dt[(size_t)(t0 + tid) * H + h] : 0.f;
+            scum[tid] = cv;
+            sdt[tid] = d;
+            sw[tid] = tid < len ? __builtin_amdgcn_exp2f(rs - cv) * d : 0.f;
+            if (tid == min(s15, len - 1)) sfast[tid >> 4] = (rs - cv) < 100.0f;
+            if (tid == s15 && s15 >= len) sfast[tid >> 4] = 1;
+        }
+#pragma unroll
+        for (int j = 0; j < SJ; ++j) {
+            const int e = 4 * (tid + 512 * j), p = e / N, n = e % N;
+            *(uint2*)(sS + p * SS + n) = sv[j];
+        }
+        typedef _Float16 hrun __attribute__((ext_vector_type(4)));
+        hrun h0, h1, h2, h3;
+        const float Dh = D[h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h0[i] = (_Float16)v[i].x;
+            h1[i] = (_Float16)v[i].y;
+            h2[i] = (_Float16)v[i].z;
+            h3[i] = (_Float16)v[i].w;
+            *(float4*)(sDx + (4 * g + i) * SD + 4 * cq) = make_float4(Dh * v[i].x, Dh * v[i].y, Dh * v[i].z, Dh * v[i].w);
+        }
+        _Float16* d = sXt + (4 * cq) * SX + 4 * g;
+        *(hrun*)d = h0;
+        *(hrun*)(d + SX) = h1;
+        *(hrun*)(d + 2 * SX) = h2;
+        *(hrun*)(d + 3 * SX) = h3;
+    }
+    __syncthreads();
+    if (!active) return;
+
+    const float ct = scum[t];
+    const float et = trow ? __builtin_amdgcn_exp2f(ct) : 0.f;
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-
-    // ---- inter-chunk term: (e^(cum_t) C_t) S_in^T
-    const float* Sc = Sin + ((size_t)c * H + h) * P * N;
-    // every C / S_in piece of the block is requested before the first one is converted (one
-    // memory round trip instead of one per loop step)
-    constexpr int CPT = 64 * N / 4 / 256;  // float4 pieces per thread (4 or 8)
-    float4 cv[CPT], sv[CPT];
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
-        cv[j] = tt + r < len ? *(const float4*)(Cm + (size_t)(t0 + tt + r) * ldc + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
-        sv[j] = ((const float4*)Sc)[e];  // P * N / 4 == 64 * N / 4
-    }
-    // ---- intra-chunk term over tau tiles up to the last row of this block. The next tile's
-    // operands (cum / dt of its positions, the X rows, this block's G rows) are loaded into
-    // registers while the current tile is multiplied: no global round trip inside the loop.
-    const int kend = min(len, tt + 64);
-    const int ntk = (kend + TK - 1) / TK;
-    constexpr int XR = 4;  // X^T staging: thread = (4 columns xq, rows 4 xg .. 4 xg + 3)
-    const int xq = tid % 16, xg = tid / 16;
-    float4 px[XR], pg[4];
-    float pcum = 0.f, pdt = 0.f;
-    auto prefetch = [&](int kk) {
-        const int k0 = ((kk + h) % ntk) * TK;
-        if (tid < TK) {
-            const int tau = k0 + tid;
-            pcum = tau < len ? cum[(size_t)(t0 + tau) * H + h] * 1.4426950408889634f : 0.f;  // log2 units
-            pdt = tau < len ? dt[(size_t)(t0 + tau) * H + h] : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < XR; ++i) {
-            const int r = xg * XR + i;
-            px[i] = r < len - k0 ? *(const float4*)(xs + (size_t)(t0 + k0 + r) * ldx + h * P + 4 * xq)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = tid + 256 * j, r = e >> 4, q = (e & 15) * 4;
-            const int t = tt + r;
-            pg[j] = t < len ? *(const float4*)(G + ((size_t)c * L + t) * L + k0 + q) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int e = tid + 256 * j, r = (4 * e) / N, cc = (4 * e) % N;
-        const float sc = tt + r < len ? __builtin_amdgcn_exp2f(srow[r]) : 0.f;
-        const float4 v = cv[j], w = sv[j];
-        f16x4 hv, hw;
-        hv[0] = (_Float16)(v.x * sc); hv[1] = (_Float16)(v.y * sc); hv[2] = (_Float16)(v.z * sc); hv[3] = (_Float16)(v.w * sc);
-        *(f16x4*)(sC + r * SN + cc) = hv;
-        hw[0] = (_Float16)w.x; hw[1] = (_Float16)w.y; hw[2] = (_Float16)w.z; hw[3] = (_Float16)w.w;
-        *(f16x4*)(sS + r * SN + cc) = hw;
-    }
-    __syncthreads();
+    // inter-chunk term: A = e^(cum_t) C_t, B = S_in
 #pragma unroll
     for (int ks = 0; ks < N / 16; ++ks) {
-        const int ko = ks * 16 + 8 * (lane >> 5);
-        const f16x8 a = *(const f16x8*)(sC + ar * SN + ko);
-        const f16x8 b = *(const f16x8*)(sS + (wp + (lane & 31)) * SN + ko);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (_Float16)((float)craw[ks][i] * et);
+        const f16x8 bo = *(const f16x8*)(sS + col * SS + 16 * ks + kh);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc, 0, 0, 0);
     }
-    prefetch(0);
-    for (int kk = 0; kk < ntk; ++kk) {
-        const int k0 = ((kk + h) % ntk) * TK;
-        __syncthreads();  // previous tile (or the inter-chunk operands) consumed
-        if (tid < TK) {
-            scum[tid] = pcum;
-            sdt[tid] = pdt;
-        }
-        {
-            typedef _Float16 hrun __attribute__((ext_vector_type(XR)));
-            hrun h0, h1, h2, h3;
+    // intra-chunk term over tau < 32 (rb + 1): A = G e^(cum_t - cum_tau) dt_tau (tau <= t). No
+    // branch per element (the LDS operands read as vectors, the causal mask a select on the two
+    // diagonal steps only: a conditional load per element serialises the wave).
+    auto mma = [&](const f16x8& a, int tau0) {
+        const f16x8 bo = *(const f16x8*)(sXt + col * SX + tau0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bo, acc, 0, 0, 0);
+    };
+    f16x8 gn[8];
+    const _Float16* gr2 = gr + 512 * 8;
 #pragma unroll
-            for (int i = 0; i < XR; ++i) {
-                h0[i] = (_Float16)px[i].x;
-                h1[i] = (_Float16)px[i].y;
-                h2[i] = (_Float16)px[i].z;
-                h3[i] = (_Float16)px[i].w;
+    for (int ks = 0; ks < 8; ++ks)
+        if (8 + ks < nk) gn[ks] = *(const f16x8*)(gr2 + 512 * ks);
+    bool fast = true;  // wave-uniform: every step of this row block takes the factored form
+    for (int ks = 0; ks < nk; ++ks) fast = fast && sfast[ks] != 0;
+    auto gfrag = [&](int ks) -> const f16x8& { return ks < 8 ? graw[ks] : gn[ks - 8]; };
+    if (fast) {
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+            if (ks >= nk) continue;
+            const int tau0 = 16 * ks + kh;
+            const float rf = trow ? __builtin_amdgcn_exp2f(ct - scum[16 * ks]) : 0.f;
+            const float4 w0 = *(const float4*)(sw + tau0), w1 = *(const float4*)(sw + tau0 + 4);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            const f16x8 g = gfrag(ks);
+            f16x8 a;
+            if (ks >= nk - 2) {  // the two steps that cross the diagonal
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = (_Float16)(tau0 + i <= t ? (float)g[i] * rf * wv[i] : 0.f);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = (_Float16)((float)g[i] * rf * wv[i]);
             }
-            _Float16* d = sXt + (4 * xq) * S + xg * XR;
-            if (k0 == tt) {  // the diagonal tile: these X rows are the block's own rows
-                const float Dh = D[h];
-#pragma unroll
-                for (int i = 0; i < XR; ++i)
-                    *(float4*)(sDx + (xg * XR + i) * P + 4 * xq) =
-                        make_float4(Dh * px[i].x, Dh * px[i].y, Dh * px[i].z, Dh * px[i].w);
-            }
-            *(hrun*)d = h0;
-            *(hrun*)(d + S) = h1;
-            *(hrun*)(d + 2 * S) = h2;
-            *(hrun*)(d + 3 * S) = h3;
+            mma(a, tau0);
         }
-        float4 gcur[4];
+    } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gcur[j] = pg[j];
-        __syncthreads();
-        if (kk + 1 < ntk) prefetch(kk + 1);
-        // A[t][tau] = G e^(cum_t - cum_tau) dt_tau for tau <= t (both inside the chunk), fp16
+        for (int ks = 0; ks < 16; ++ks) {
+            if (ks >= nk) continue;
+            const int tau0 = 16 * ks + kh;
+            const float4 c0 = *(const float4*)(scum + tau0), c1 = *(const float4*)(scum + tau0 + 4);
+            const float4 d0 = *(const float4*)(sdt + tau0), d1 = *(const float4*)(sdt + tau0 + 4);
+            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float dv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+            const f16x8 g = gfrag(ks);
+            f16x8 a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = tid + 256 * j, r = e >> 4, q = (e & 15) * 4;
-            const int t = tt + r;
-            const float gv[4] = {gcur[j].x, gcur[j].y, gcur[j].z, gcur[j].w};
-            f16x4 hv;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tau = k0 + q + i;
-                const bool vis = t < len && tau <= t && tau < len;
-                hv[i] = (_Float16)(vis ? gv[i] * __builtin_amdgcn_exp2f(srow[r] - scum[q + i]) * sdt[q + i] : 0.f);
+            for (int i = 0; i < 8; ++i) {
+                const float e = __builtin_amdgcn_exp2f(fminf(ct - cv[i], 0.f));  // tau <= t: <= 0
+                a[i] = (_Float16)(trow && tau0 + i <= t ? (float)g[i] * e * dv[i] : 0.f);
             }
-            *(f16x4*)(sA + r * S + q) = hv;
-        }
-        __syncthreads();
-        if (k0 > tt + wt + 31) continue;  // wave-uniform: tile entirely in this wave's future
-#pragma unroll
-        for (int ks = 0; ks < TK / 16; ++ks) {
-            const int ko = ks * 16 + 8 * (lane >> 5);
-            const f16x8 a = *(const f16x8*)(sA + ar * S + ko);
-            const f16x8 b = *(const f16x8*)(sXt + (wp + (lane & 31)) * S + ko);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+            mma(a, tau0);
         }
     }
-    // ---- + D x, store. acc element e: t row wt + 8(e/4)+4(lane/32)+e%4, p col wp + lane%32
-    __syncthreads();  // sDx complete
-    const int p = wp + (lane & 31);
+    // + D x, store. acc element e: t row 32 rb + 8(e/4) + 4(lane/32) + e%4, p col pc0 + lane%32
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        const int tl = wt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), t = tt + tl;
-        if (t < len) y[(size_t)(t0 + t) * ldy + h * P + p] = acc[e] + sDx[tl * P + p];
+        const int tl = 32 * rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (tl < len) y[(size_t)(t0 + tl) * ldy + h * P + pc0 + col] = acc[e] + sDx[tl * SD + col];
     }
 }
 
@@ -535,35 +566,36 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     GH_REQUIRE(ldx % 4 == 0 && ldbc % 4 == 0, "ssd scan: row strides must be multiples of 4");
     const int nch = cdiv(T, L);
     const size_t PN = (size_t)P * N;
-    // workspace: dt, cum [T][H]; G [nch][L][L]; dS, Sin [nch][H][P][N]; decay [nch][H]
-    const size_t f_dt = (size_t)T * H, f_G = (size_t)nch * L * L, f_S = (size_t)nch * H * PN;
-    float* ws = (float*)workspace(WS_MAMBA_CHUNK, (2 * f_dt + f_G + 2 * f_S + (size_t)nch * H + 64) * 4);
+    // workspace: dt, cum [T][H] fp32; dS [nch][H][P][N] fp32; decay [nch][H] fp32;
+    // Sin [nch][H][P][N], G [nch][L][L] and C16 [nch][L][N] fp16 (G, C16 in fragment order)
+    const size_t f_dt = (size_t)T * H, f_S = (size_t)nch * H * PN;
+    const size_t f_dec = ((size_t)nch * H + 63) / 64 * 64;
+    const size_t h_G = (size_t)nch * L * L, h_C = (size_t)nch * L * N;
+    float* ws = (float*)workspace(WS_MAMBA_CHUNK, (2 * f_dt + f_S + f_dec) * 4 + (f_S + h_G + h_C) * 2 + 256);
     if (!ws) return fail(GH_ENOMEM, "ssd scan: workspace");
     float* dt = ws;
     float* cum = dt + f_dt;
-    float* G = cum + f_dt;
-    float* dS = G + f_G;
-    float* Sin = dS + f_S;
-    float* decay = Sin + f_S;
+    float* dS = cum + f_dt;
+    float* decay = dS + f_S;
+    _Float16* Sin16 = (_Float16*)(decay + f_dec);
+    _Float16* G = Sin16 + f_S;
+    _Float16* C16 = G + h_G;
     const unsigned nb1 = (unsigned)(nch * H + nch * (L / 64) * (L / 64));  // chunk states, then G tiles
-    const bool one = nch == 1;  // a single chunk: the state pass runs in the chunk-state blocks
+    const unsigned nbp = (unsigned)(((size_t)H * PN / 4 + 255) / 256);
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_state_cb<128>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L, one ? state : nullptr, Sin);
+                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L);
+        hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
+                           (int)PN);
+        hipLaunchKernelGGL(k_ssd_out<128>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
+                           Sin16, D, y, ldy, T, H, L);
     } else {
         hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, dS, decay, T, H, L, one ? state : nullptr, Sin);
-    }
-    const int64_t nst = (int64_t)H * PN;
-    if (!one)
-        hipLaunchKernelGGL(k_ssd_state_pass, dim3((unsigned)((nst + 255) / 256)), dim3(256), 0, stream(), state, dS,
-                           decay, Sin, nch, H, (int)PN);
-    if (N == 128) {
-        hipLaunchKernelGGL(k_ssd_chunk_out<128>, dim3(nch, H, L / 64), dim3(256), 0, stream(), xs, ldx, Cm, ldbc, G,
-                           dt, cum, Sin, D, y, ldy, T, H, L);
-    } else {
-        hipLaunchKernelGGL(k_ssd_chunk_out<64>, dim3(nch, H, L / 64), dim3(256), 0, stream(), xs, ldx, Cm, ldbc, G,
-                           dt, cum, Sin, D, y, ldy, T, H, L);
+                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L);
+        hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
+                           (int)PN);
+        hipLaunchKernelGGL(k_ssd_out<64>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
+                           Sin16, D, y, ldy, T, H, L);
     }
     GH_LAUNCHED("k_ssd_*");
     return GH_OK;
