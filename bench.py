@@ -156,8 +156,8 @@ def kernel_suite(gh):
                         "k_gemv8_q4k" if (kind == 3 and 2 <= M <= 8 and K <= 4096) else "k_gemv_mfma")
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
-                res[tag] = entry("k_to_f16+k_gemm_q4", ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K,
-                                 bound="mfma")
+                res[tag] = entry("k_dequant_bf16+k_to_bf16+hipBLASLt bf16 GEMM (fp32 out)", ms,
+                                 bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K, bound="mfma")
             del dw, dx, y
     # ---------------- c3: SSD scan T=4096 + decode state update
     T, H, P, N = 4096, 48, 64, 128
@@ -171,7 +171,8 @@ def kernel_suite(gh):
     ms = time_launches(gh, lambda: gh.call("gh_ssd_scan", *[b.p for b in bufs], st.p, yb.p, T, H, P, N, 256), 10)
     scan_bytes = 2 * (T * H * P + 2 * T * N + T * H + T * H * P) + 2 * H * P * N * 4  # fp16-equivalent I/O + state
     flops = 2.0 * (16 * 256 * 256 * N) + H * 16 * (2.0 * 256 * 256 * P + 4.0 * 256 * N * P)
-    res["c3_ssd_scan_T4096"] = entry("k_ssd_state_cb+k_ssd_state_pass+k_ssd_chunk_out (3 launches)", ms, bytes_=scan_bytes, flops=flops, bound="hbm")
+    res["c3_ssd_scan_T4096"] = entry("k_ssd_state_cb+k_ssd_state_pass+k_ssd_out (3 launches)", ms, bytes_=scan_bytes,
+                                     flops=flops, bound="hbm")
     del bufs, st, yb
     d, di, nh, ds, kk = 1536, 3072, 48, 128, 4
     conv_dim = di + 2 * ds
@@ -258,7 +259,7 @@ def kernel_suite(gh):
         ms = time_launches(gh, run, 100 if N == 1 else 10)
         fl = 2.0 * N * (K5 * 3 * E5 * d5 + 3 * SH5 * d5)
         if N == 1:
-            res[tag] = entry("moe route+gemv x2+combine", ms, bytes_=K5 * expert_bytes + 3 * SH5 * d5 * 144 // 256,
+            res[tag] = entry("k_route_chain+k_moe_gemv (selection inside)+k_moe_down_par", ms, bytes_=K5 * expert_bytes + 3 * SH5 * d5 * 144 // 256,
                              flops=fl)
         else:
             res[tag] = entry("moe route+permute+group gemm x2+shared+combine", ms,

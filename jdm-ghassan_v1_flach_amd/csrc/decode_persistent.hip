@@ -121,7 +121,7 @@ __device__ bool pd_wait_n(const PdRange (&r)[NR], PD_G int32_t* abort, PD_L uint
                     const uint32_t lds = (uint32_t)(uintptr_t)(stage + 2 * (PD_T * j + wave_base));
                     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(g),
                                  "s"(__builtin_amdgcn_readfirstlane(lds))
-                                 : "memory", "m0");
+                                 : "memory");
                 }
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -312,7 +312,7 @@ constexpr size_t G4_LDS = 4 * 256 * 128;  // A[2], B[2]: 256 rows x 128 bytes
 __device__ __forceinline__ void g4_dma(const void* base, uint32_t voff, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
                  "s"(__builtin_amdgcn_readfirstlane(lds_base))
-                 : "memory", "m0");
+                 : "memory");
 }
 
 struct G4Scale {
@@ -797,7 +797,13 @@ static int gemm2_launch(const float* x, const void* w, float* y, int M, int K, i
     return finish_acc();
 }
 
+int gemm_lib(const float* x, const void* w, float* y, int M, int K, int N, int kind, int accumulate);  // gemm_lib.hip
+
 int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int accumulate) {
+    {
+        const int rc = gemm_lib(x, w, y, M, K, N, kind, accumulate);
+        if (rc != GH_EUNSUPPORTED) return rc;
+    }
     const int blocks = cdiv(M, BM) * cdiv(N, BN);
     size_t rowb = kind == 4 ? (size_t)K * 2 : kind == 5 ? (size_t)K * 4 : row_bytes(kind, K);
     const dim3 g(blocks), b(256);

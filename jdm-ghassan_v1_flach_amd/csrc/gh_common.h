@@ -233,11 +233,13 @@ enum WsSlot {
     WS_QUANT0 = 16,     // 16 quant_materialize slots: 16..31
     WS_MOE_XG = 32,     // gathered rows for the grouped prefill GEMM
     WS_MOE_H = 33,
-    WS_MOE_TERMS = 34,  // router group terms (large routers, few tokens)
+    WS_MOE_TERMS = 34,  // router logits (large routers)
     WS_GEMM_PART = 35,  // split-K partial tiles of the small-M prefill GEMM
     WS_GEMM_ACC = 36,   // product before an accumulating add (paths without an in-place sum)
     WS_HEAD_CTL = 37,   // argmax key / counter block of a standalone lm-head + greedy call
     WS_TOPK = 38,       // top-K survivors of each 4096-logit chunk
     WS_PEN_HIST = 39,   // device copy of the penalty history
+    WS_GEMM_W16 = 40,   // large-M prefill: the weights decoded to bf16 for the library GEMM
+    WS_BLASLT = 41,     // hipBLASLt workspace
 };
 }  // namespace gh

@@ -5,6 +5,9 @@
 // kernels wait for them with explicit s_waitcnt vmcnt(n), counting their own
 // transfers in issue order (the counter is in-order), and synchronise with
 // lds_barrier(), which unlike __syncthreads does not drain them.
+// M0 is a register the compiler reserves (it rejects a clobber on it): the code relies on no
+// compiler-generated instruction using M0 in the kernels that call these, which
+// tests/test_abi_cpu.py checks on the generated code of every such file.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -13,11 +16,11 @@ namespace gh {
 
 // 64-bit address per lane
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
 }
 // 64-bit base in SGPRs + 32-bit per-lane offset (no per-lane address arithmetic)
 __device__ __forceinline__ void lds_dma16s(const void* base, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_base) : "memory");
 }
 // wave-uniform LDS byte address of p
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {

@@ -258,7 +258,8 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
                                                       const float* __restrict__ a_log, float* __restrict__ dt,
                                                       float* __restrict__ cum, _Float16* __restrict__ G,
                                                       _Float16* __restrict__ C16, float* __restrict__ dS,
-                                                      float* __restrict__ decay, int T, int H, int L) {
+                                                      float* __restrict__ decay, int T, int H, int L,
+                                                      float* __restrict__ state, _Float16* __restrict__ Sin16) {
     constexpr int P = 64, TK = 64, S = TK + 8, SN = N + 8;
     constexpr int U_STATE = (P * S + N * S) * 2, U_CB = 2 * 64 * SN * 2;
     __shared__ __attribute__((aligned(16))) unsigned char smem[U_STATE > U_CB ? U_STATE : U_CB];
@@ -325,6 +326,8 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
     }
     float* out = dS + ((size_t)c * H + h) * P * N;
     const float dec = expf(cend);
+    // a single chunk (state != null): the inter-chunk pass of this head runs here, with
+    // k_ssd_state_pass's arithmetic: S_in = state (fp16 for the outputs), state = state dec + dS
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
         const int tile = wave * TPW + i;
@@ -333,7 +336,14 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
         for (int e = 0; e < 16; ++e) {
             const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
             const int n = nt * 32 + (lane & 31);
-            out[(size_t)p * N + n] = acc[i][e];
+            if (state) {
+                const size_t si = ((size_t)h * P + p) * N + n;
+                const float s0 = state[si];
+                Sin16[si] = (_Float16)s0;
+                state[si] = s0 * dec + acc[i][e];
+            } else {
+                out[(size_t)p * N + n] = acc[i][e];
+            }
         }
     }
     if (threadIdx.x == 0) decay[(size_t)c * H + h] = dec;
@@ -582,18 +592,21 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     _Float16* C16 = G + h_G;
     const unsigned nb1 = (unsigned)(nch * H + nch * (L / 64) * (L / 64));  // chunk states, then G tiles
     const unsigned nbp = (unsigned)(((size_t)H * PN / 4 + 255) / 256);
+    const bool one = nch == 1;  // a single chunk: the state pass runs in the chunk-state blocks
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_state_cb<128>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L);
-        hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
-                           (int)PN);
+                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
+        if (!one)
+            hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
+                               (int)PN);
         hipLaunchKernelGGL(k_ssd_out<128>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
                            Sin16, D, y, ldy, T, H, L);
     } else {
         hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L);
-        hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
-                           (int)PN);
+                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
+        if (!one)
+            hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
+                               (int)PN);
         hipLaunchKernelGGL(k_ssd_out<64>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
                            Sin16, D, y, ldy, T, H, L);
     }

@@ -36,110 +36,77 @@ static size_t route_lds(int d, int ne, int N) {
     return ((size_t)d + (size_t)ne * (route_window(d, ne, N) + 1)) * 4;
 }
 
-// Router of a large expert set for few tokens, over many blocks: block
-// (x, t) computes the group terms of groups [gpb x, gpb x + gpb) of token t
-// for every expert (same arithmetic as k_route) into terms
-// [t][group/4][expert][group%4]; k_route_select then adds each expert's terms in group
-// order and finishes. gpb is chosen so that the router matrix is spread over
-// about 64 blocks (one batch of weight loads each).
-__global__ void __launch_bounds__(256) k_route_terms(const float* __restrict__ x, const float* __restrict__ rw,
-                                                     float* __restrict__ terms, int d, int ne,
-                                                     const float* __restrict__ nw, float eps,
-                                                     float* __restrict__ xn, int RT_G) {
+// Router logits of a large expert set for few tokens: one wave per (expert e, token t). Lane
+// l holds the group terms of groups l, l + 64, ... (the reference's group term
+// ((x0 w0 + x1 w1) + x2 w2) + x3 w3, core/moe_cpu.cpp:76-83, no fused multiply-add), read
+// with coalesced 16-byte loads; the sequential sum over the groups in order then runs as one
+// chain of adds whose operands come by readlane (no memory round trip inside the chain).
+// With `nw` the token row is RMS-normalised first (double sum of squares, the k_rmsnorm
+// statistic) and the wave of expert 0 writes the normalised row to xn. Requires d % 4 == 0
+// and d <= 4096.
+constexpr int RC_J = 16;  // groups per lane (d <= 4096)
+__global__ void __launch_bounds__(64) k_route_chain(const float* __restrict__ x, const float* __restrict__ rw,
+                                                    float* __restrict__ logits, int d, int ne,
+                                                    const float* __restrict__ nw, float eps,
+                                                    float* __restrict__ xn) {
 #pragma clang fp contract(off)
-    extern __shared__ float rt_sx[];  // [d]
-    __shared__ double dred[4];
-    const int t = blockIdx.y, tid = threadIdx.x;
-    const int ngroups = d / 4, g0 = blockIdx.x * RT_G, gw = min(RT_G, ngroups - g0);
-    const float4* xt = (const float4*)(x + (size_t)t * d);
-    const float4* rw4 = (const float4*)rw;
-    float4 wreg[ROUTE_RB];
+    const int e = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int G = d / 4, J = (G + 63) / 64;
+    const float4* x4 = (const float4*)(x + (size_t)t * d);
+    const float4* w4 = (const float4*)(rw + (size_t)e * d);
+    float4 xv[RC_J], wv[RC_J];
 #pragma unroll
-    for (int b = 0; b < ROUTE_RB; ++b) {
-        const int q = tid + b * 256;
-        if (q < ne * gw) {
-            const int e = q / gw;
-            wreg[b] = rw4[(size_t)e * ngroups + g0 + (q - e * gw)];
+    for (int j = 0; j < RC_J; ++j) {
+        const int g = 64 * j + lane;
+        if (j < J) {
+            xv[j] = g < G ? x4[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[j] = g < G ? w4[g] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    }
-    double ss = 0.0;
-    for (int g = tid; g < ngroups; g += 256) {
-        const float4 v = xt[g];
-        *(float4*)(rt_sx + 4 * g) = v;
-        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
     }
     if (nw) {
-        ss = wave_sum(ss);
-        if ((tid & 63) == 0) dred[tid >> 6] = ss;
-        __syncthreads();
-        const double tot = dred[0] + dred[1] + dred[2] + dred[3];
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < RC_J; ++j)
+            if (j < J) ss += (double)xv[j].x * xv[j].x + (double)xv[j].y * xv[j].y + (double)xv[j].z * xv[j].z +
+                             (double)xv[j].w * xv[j].w;
+        const double tot = wave_sum(ss);
         const double invd = 1.0 / sqrt(tot / (double)d + (double)eps);
         const float inv = isfinite(invd) ? (float)invd : 0.0f;
-        for (int i = tid; i < d; i += 256) {
-            const float v = rt_sx[i] * inv * nw[i];
-            rt_sx[i] = v;
-            if (blockIdx.x == 0) xn[(size_t)t * d + i] = v;
-        }
-    }
-    __syncthreads();
-    float* tt = terms + (size_t)t * (size_t)cdiv(ngroups, 4) * 4 * ne;  // [t][group/4][expert][4]
-    for (int q0 = 0; q0 < ne * gw; q0 += ROUTE_RB * 256) {
-        if (q0 > 0) {
+        const float4* n4 = (const float4*)nw;
 #pragma unroll
-            for (int b = 0; b < ROUTE_RB; ++b) {
-                const int q = q0 + tid + b * 256;
-                if (q < ne * gw) {
-                    const int e = q / gw;
-                    wreg[b] = rw4[(size_t)e * ngroups + g0 + (q - e * gw)];
-                }
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < ROUTE_RB; ++b) {
-            const int q = q0 + tid + b * 256;
-            if (q < ne * gw) {
-                const int e = q / gw, gl = q - e * gw;
-                const int i = 4 * (g0 + gl);
-                const float4 w = wreg[b];
-                const float p0 = rt_sx[i] * w.x, p1 = rt_sx[i + 1] * w.y, p2 = rt_sx[i + 2] * w.z,
-                            p3 = rt_sx[i + 3] * w.w;
-                const int g = g0 + gl;
-                tt[((size_t)(g >> 2) * ne + e) * 4 + (g & 3)] = ((p0 + p1) + p2) + p3;
+        for (int j = 0; j < RC_J; ++j) {
+            const int g = 64 * j + lane;
+            if (j < J && g < G) {
+                const float4 wn = n4[g];
+                xv[j] = make_float4(xv[j].x * inv * wn.x, xv[j].y * inv * wn.y, xv[j].z * inv * wn.z,
+                                    xv[j].w * inv * wn.w);
+                if (e == 0 && xn) ((float4*)(xn + (size_t)t * d))[g] = xv[j];
             }
         }
     }
-}
-
-// The sequential per-expert sums (the reference's rounding order) are one
-// dependent chain of ngroups additions per expert: lane e runs expert e's
-// chain; its terms arrive by coalesced 16-byte loads (4 groups per lane, the
-// 64 lanes of a load cover one run of 4 groups), 96 loads in flight.
-constexpr int RS_C = 96;  // float4 per chunk
-__global__ void __launch_bounds__(64) k_route_select(const float* __restrict__ terms, int ngroups, int ne, int K,
-                                                     const float* __restrict__ bias, int32_t* __restrict__ idx,
-                                                     float* __restrict__ wout, float* __restrict__ probs) {
-#pragma clang fp contract(off)
-    __shared__ float sp[64];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const int e = lane < ne ? lane : 0;
-    const float* tt = terms + (size_t)t * (size_t)cdiv(ngroups, 4) * 4 * ne;  // 16-byte aligned per token
-    const float4* t4 = (const float4*)tt + e;  // run r of expert e at t4[r * ne]
-    const int nq = ngroups / 4;
+    float term[RC_J];
+#pragma unroll
+    for (int j = 0; j < RC_J; ++j)
+        if (j < J) {
+            const float p0 = xv[j].x * wv[j].x, p1 = xv[j].y * wv[j].y, p2 = xv[j].z * wv[j].z, p3 = xv[j].w * wv[j].w;
+            term[j] = ((p0 + p1) + p2) + p3;
+        }
     float s = 0.0f;
-    float4 R[RS_C];
-    for (int c = 0; c < nq; c += RS_C) {
 #pragma unroll
-        for (int j = 0; j < RS_C; ++j)
-            if (c + j < nq) R[j] = t4[(size_t)(c + j) * ne];
+    for (int j = 0; j < RC_J; ++j) {
+        if (j < J) {
+            const int cnt = min(64, G - 64 * j);  // wave-uniform
+            const int tb = __builtin_bit_cast(int, term[j]);
+            if (cnt == 64) {
 #pragma unroll
-        for (int j = 0; j < RS_C; ++j)
-            if (c + j < nq) s = (((s + R[j].x) + R[j].y) + R[j].z) + R[j].w;
+                for (int l = 0; l < 64; ++l) s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(tb, l));
+            } else {
+                // a partial last run: readlane needs a wave-uniform lane index, here a loop counter
+                for (int l = 0; l < cnt; ++l) s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(tb, l));
+            }
+        }
     }
-    for (int g = 4 * nq; g < ngroups; ++g) s += tt[((size_t)(g >> 2) * ne + e) * 4 + (g & 3)];
-    if (lane < ne) sp[lane] = s;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    route_finish(sp, bias, ne, K, t, idx, wout, probs);
+    if (lane == 0) logits[(size_t)t * ne + e] = s;
 }
 
 // Router of many tokens (prefill), no norm, in two kernels.
@@ -229,15 +196,13 @@ __global__ void __launch_bounds__(256) k_route_finish(const float* __restrict__ 
 // router matrix and few tokens
 static int launch_route(const float* x, const float* rw, const float* bias, float* probs, int32_t* idx, float* w,
                         int N, int d, int ne, int K, const float* nw, float eps, float* xn) {
-    if (N <= 8 && (size_t)ne * d > 16384 && ne <= 64) {
-        const int ngroups = d / 4, gpb = std::max(4, cdiv(ngroups, 64));
-        float* terms = (float*)workspace(WS_MOE_TERMS, (size_t)N * cdiv(ngroups, 4) * 4 * ne * 4);
-        if (!terms) return fail(GH_ENOMEM, "moe route: workspace");
-        hipLaunchKernelGGL(k_route_terms, dim3(cdiv(ngroups, gpb), N), dim3(256), (size_t)d * 4, stream(), x, rw,
-                           terms, d, ne, nw, eps, xn, gpb);
-        hipLaunchKernelGGL(k_route_select, dim3(N), dim3(64), 0, stream(), terms, ngroups, ne, K, bias, idx, w,
-                           probs);
-        GH_LAUNCHED("k_route_terms/select");
+    if (N <= 8 && (size_t)ne * d > 16384 && ne <= 64 && d % 4 == 0 && d <= 4096) {
+        float* lg = (float*)workspace(WS_MOE_TERMS, (size_t)N * ne * 4);
+        if (!lg) return fail(GH_ENOMEM, "moe route: workspace");
+        hipLaunchKernelGGL(k_route_chain, dim3(ne, N), dim3(64), 0, stream(), x, rw, lg, d, ne, nw, eps, xn);
+        hipLaunchKernelGGL(k_route_finish, dim3(cdiv(N, 4)), dim3(256), 0, stream(), lg, bias, probs, idx, w, N, ne,
+                           K);
+        GH_LAUNCHED("k_route_chain/finish");
         return GH_OK;
     }
     const size_t rl_lds = (size_t)RL_E * (d / 4 + 1) * 16;
@@ -448,6 +413,8 @@ struct GemvJobs {
     int ne, gw;
     int32_t* ridx;
     float* rwout;
+    const float* rlogits;  // router logits [N][ne] (k_moe_gemv<.., LOGITS>)
+    float* rprobs;         // probabilities out [N][ne] (LOGITS, may be null)
     // gate/up of EVERY expert (small expert sets): activations [N][ne][rows_r]; the down
     // kernel then gathers the rows of the selected experts (0: rows in slot order)
     int gather_ne;
@@ -458,7 +425,11 @@ struct GemvJobs {
 // blocks route token j (block x = 0 only, writing idx / w): the routing runs
 // beside the GEMVs instead of in front of them, and the down kernel gathers
 // the selected experts' activations.
-template <int KIND, bool DUAL, bool ROUTE = false, bool ALLEXP = false>
+// LOGITS (large routers, decode): the router logits come from k_route_chain; every routed
+// block picks its token's experts from them itself (route_finish, one wave), the first block
+// of each token writing idx / w for the down kernel, so no launch sits between the router and
+// the expert weights. Shared-expert blocks start at once.
+template <int KIND, bool DUAL, bool ROUTE = false, bool ALLEXP = false, bool LOGITS = false>
 __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
     int job = blockIdx.y;
     if constexpr (ALLEXP) {
@@ -488,6 +459,21 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
         extern __shared__ float msm_n[];
         route_norm(J.rx, shared ? job - J.S : job / J.ne, J.d, J.rnw, J.reps, nullptr, msm_n);
     }
+    if (LOGITS && !shared) {
+        if (blockIdx.x * 4 * RP >= rows) return;
+        __shared__ float slg[64];
+        const int token = job / J.K;
+        const bool writer = blockIdx.x == 0 && job % J.K == 0;
+        if (threadIdx.x < 64) {
+            if (threadIdx.x < J.ne) slg[threadIdx.x] = J.rlogits[(size_t)token * J.ne + threadIdx.x];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            route_finish(slg, J.rbias, J.ne, J.K, token, writer ? J.ridx : nullptr, writer ? J.rwout : nullptr,
+                         writer ? J.rprobs : nullptr, ssel);
+        }
+        __syncthreads();
+    }
     if (ROUTE) {
         if (blockIdx.x * 4 * RP >= rows) return;  // no rows here (block 0, the writer, always has some)
         // every block routes its token (identical arithmetic, so all agree); the normalised row
@@ -510,7 +496,7 @@ __global__ void __launch_bounds__(256) k_moe_gemv(GemvJobs J) {
         Wa = J.sa;
         if (DUAL) Wb = J.sb;
     } else {
-        const int e = ALLEXP ? job % J.ne : ROUTE ? ssel[job % J.K] : J.idx[job];
+        const int e = ALLEXP ? job % J.ne : (ROUTE || LOGITS) ? ssel[job % J.K] : J.idx[job];
         const int tok = ALLEXP ? job / J.ne : job / J.K;
         xin = (ROUTE || ALLEXP) ? msm : (DUAL ? J.x + (size_t)tok * J.d : J.x + (size_t)job * kin);
         Wa = J.wa + (size_t)e * J.estride;
@@ -1228,7 +1214,8 @@ __global__ void k_single_group_tiles(int32_t* tiles, int32_t* offs, int N, int b
 template <int KIND>
 static int moe_kind(const float* x, const float* w_route, const int32_t* idx, const void* gates, const void* ups,
                     const void* downs, const void* sh_g, const void* sh_u, const void* sh_d, float* out, float* acc_dst,
-                    int* added, int N, int d, int E, int ne, int K, int SH) {
+                    int* added, int N, int d, int E, int ne, int K, int SH, const float* rlogits = nullptr,
+                    const float* rbias = nullptr, float* rprobs = nullptr) {
     const int S = N * K;
     const bool has_sh = sh_g && sh_u && sh_d;
     const size_t rowb_d = KIND == 4 ? (size_t)d * 2 : row_bytes(KIND, d);
@@ -1256,7 +1243,13 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             return 4 * (64 / LPR);
         };
         dim3 g1(cdiv(maxrows, rows_per_block(d)), S + J.N);
-        hipLaunchKernelGGL((k_moe_gemv<KIND, true>), g1, dim3(256), 0, stream(), J);
+        if (rlogits) {  // the selection runs in the gate/up blocks, which write idx / w (/ probs)
+            J.rlogits = rlogits; J.rbias = rbias; J.ne = ne; J.ridx = const_cast<int32_t*>(idx);
+            J.rwout = const_cast<float*>(w_route); J.rprobs = rprobs;
+            hipLaunchKernelGGL((k_moe_gemv<KIND, true, false, false, true>), g1, dim3(256), 0, stream(), J);
+        } else {
+            hipLaunchKernelGGL((k_moe_gemv<KIND, true>), g1, dim3(256), 0, stream(), J);
+        }
         GH_LAUNCHED("k_moe_gemv(gate/up)");
         GemvJobs D{};
         D.x = act; D.idx = idx; D.S = S; D.N = J.N; D.K = K; D.d = d;
@@ -1449,7 +1442,15 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
     // small expert sets: every expert's gate/up is computed (at most a few MB of weights) so the
     // routing runs beside the GEMVs instead of in front of them
     const bool allexp = fused_route && has_sh && ne > K && (size_t)ne * E * d <= ((size_t)4 << 20);
-    if (!fused_route) {
+    // a large router: its logits by k_route_chain, the selection inside the gate/up blocks
+    const bool chain = !fused_route && ne <= 64 && d % 4 == 0 && d <= 4096;
+    float* logits = nullptr;
+    if (chain) {
+        logits = (float*)workspace(WS_MOE_TERMS, (size_t)N * ne * 4);
+        if (!logits) return fail(GH_ENOMEM, "moe: workspace");
+        hipLaunchKernelGGL(k_route_chain, dim3(ne, N), dim3(64), 0, stream(), xres, rw, logits, d, ne, nw, eps, xn);
+        GH_LAUNCHED("k_route_chain");
+    } else if (!fused_route) {
         const int rc = launch_route(xres, rw, bias, nullptr, idx, w, N, d, ne, K, nw, eps, xn);
         if (rc) return rc;
     }
@@ -1475,6 +1476,9 @@ static int moe_decode_fused_kind(float* xres, const float* nw, float eps, const 
         J.rx = xres; J.rw = rw; J.rbias = bias; J.rnw = nw; J.reps = eps; J.ne = ne; J.gw = gw;
         J.ridx = idx; J.rwout = w;
         hipLaunchKernelGGL((k_moe_gemv<KIND, true, true>), g1, dim3(256), rlds, stream(), J);
+    } else if (chain) {
+        J.rlogits = logits; J.rbias = bias; J.ne = ne; J.ridx = idx; J.rwout = w;
+        hipLaunchKernelGGL((k_moe_gemv<KIND, true, false, false, true>), g1, dim3(256), 0, stream(), J);
     } else {
         hipLaunchKernelGGL((k_moe_gemv<KIND, true>), g1, dim3(256), 0, stream(), J);
     }
@@ -1555,6 +1559,24 @@ int moe_forward_acc(const float* x, const float* router_w, const float* router_b
         if (!r) return fail(GH_ENOMEM, "moe: workspace");
         if (!idx) idx = (int32_t*)r;
         if (!w) w = (float*)(r + (size_t)S * 4);
+    }
+    // few tokens, a large router: logits by k_route_chain, the selection inside the gate/up blocks
+    const bool chain = N <= 8 && (size_t)ne * d > 16384 && d % 4 == 0 && d <= 4096 && qkind >= 0;
+    if (chain) {
+        GH_REQUIRE(!nw || xn, "moe_forward: a normalised-row buffer is needed with the norm");
+        float* lg = (float*)workspace(WS_MOE_TERMS, (size_t)N * ne * 4);
+        if (!lg) return fail(GH_ENOMEM, "moe: workspace");
+        hipLaunchKernelGGL(k_route_chain, dim3(ne, (unsigned)N), dim3(64), 0, stream(), x, router_w, lg, d, ne, nw, eps,
+                           xn);
+        GH_LAUNCHED("k_route_chain");
+        const float* xi = nw ? xn : x;
+        const int n = (int)N;
+        switch (qkind) {
+            case 0: return moe_kind<0>(xi, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH, lg, router_bias, probs_cache);
+            case 1: return moe_kind<1>(xi, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH, lg, router_bias, probs_cache);
+            case 2: return moe_kind<2>(xi, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH, lg, router_bias, probs_cache);
+            default: return moe_kind<3>(xi, w, idx, gates, ups, downs, sh_g, sh_u, sh_d, out, acc_dst, added, n, d, E, ne, K, SH, lg, router_bias, probs_cache);
+        }
     }
     int rc;
     if (nw) {

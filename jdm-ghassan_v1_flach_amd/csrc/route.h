@@ -25,50 +25,93 @@ __device__ __forceinline__ void route_finish(float* sp, const float* __restrict_
                              int32_t* __restrict__ idx, float* __restrict__ wout, float* __restrict__ probs,
                              int* sel_lds = nullptr, float* wsel_lds = nullptr) {
 #pragma clang fp contract(off)
-    // one wave per token (K <= 8, ne <= 64, at most 16 waves per block)
+    // one wave per token (K <= 8, ne <= 64, at most 16 waves per block). The serial parts (the
+    // sums in expert order) read their operands as LDS vectors, every lane running the same
+    // chain (a readlane per operand stalls on the scalar-register hazard each step); the rank
+    // of each candidate is counted by every lane over LDS vectors of all keys.
     __shared__ int rf_sel_all[16][8];
-    int* rf_sel = rf_sel_all[threadIdx.x >> 6];
+    __shared__ __attribute__((aligned(16))) float rf_p_all[16][64];
+    __shared__ __attribute__((aligned(16))) uint32_t rf_k_all[16][64];
+    const int wv_id = threadIdx.x >> 6;
+    int* rf_sel = rf_sel_all[wv_id];
+    float* rf_p = rf_p_all[wv_id];
+    uint32_t* rf_k = rf_k_all[wv_id];
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     const int lane = threadIdx.x & 63;
     const float lg = lane < ne ? sp[lane] : -INFINITY;
+    const float bl = (lane < ne && bias) ? bias[lane] : 0.0f;
     const float mx = wave_max(lg);  // order-free
     const float ev = lane < ne ? (float)exp((double)(lg - mx)) : 0.f;
-    // sequential sum in expert order (the reference's rounding), operands by readlane
+    rf_p[lane] = ev;
+    wave_sync();
+    // sequential sum in expert order (the reference's rounding); the zeros past ne add nothing
+    const int nq = (ne + 3) >> 2;  // wave-uniform
     float sum = 0.f;
-    for (int i = 0; i < ne; ++i) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ev), i));
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        if (q < nq) {
+            const float4 v = ((const float4*)rf_p)[q];
+            sum = (((sum + v.x) + v.y) + v.z) + v.w;
+        }
+    }
     const float inv = (sum > 1e-12f) ? (1.0f / sum) : 0.0f;
     const float p = ev * inv;
-    const float sel = lane < ne ? p + (bias ? bias[lane] : 0.0f) : -INFINITY;
+    const float sel = lane < ne ? p + bl : -INFINITY;
     // K rounds of "largest value, lowest index among the rest" pick the candidates in the
     // order of this key: the value in an order-preserving unsigned form, ties by index.
     // Each candidate's rank (number of candidates before it) is its round.
     const bool cand = lane < ne && sel > -1e30f;
     const uint32_t u = __builtin_bit_cast(uint32_t, sel);
     const uint32_t key = cand ? ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) : 0u;
-    int r0 = 0, r1 = 0;
-    for (int j = 0; j < ne; j += 2) {
-        const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
-        const uint32_t k1 = j + 1 < ne ? (uint32_t)__builtin_amdgcn_readlane((int)key, j + 1) : 0u;
-        r0 += (k0 > key || (k0 == key && j < lane)) ? 1 : 0;
-        r1 += (k1 > key || (k1 == key && j + 1 < lane)) ? 1 : 0;
+    wave_sync();  // every lane has read rf_p
+    rf_p[lane] = p;
+    rf_k[lane] = key;
+    wave_sync();
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        if (q >= nq) continue;
+        const uint4 k4 = ((const uint4*)rf_k)[q];
+        const int j = 4 * q;
+        rank += (k4.x > key || (k4.x == key && j < lane)) ? 1 : 0;
+        rank += (k4.y > key || (k4.y == key && j + 1 < lane)) ? 1 : 0;
+        rank += (k4.z > key || (k4.z == key && j + 2 < lane)) ? 1 : 0;
+        rank += (k4.w > key || (k4.w == key && j + 3 < lane)) ? 1 : 0;
     }
-    const int rank = r0 + r1;
     const int ncand = __popcll(__ballot(cand));
     if (cand && rank < K) rf_sel[rank] = lane;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // lane k < K: the expert of round k (a round without candidates takes expert 0, as the reference)
-    const int mine = (lane < K && lane < ncand) ? rf_sel[lane] : 0;
-    const float wv = __shfl(p, mine, 64);
+    wave_sync();
+    // round k: expert rf_sel[k] (a round without candidates takes expert 0, as the reference)
+    int selk[8];
+    float wk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        selk[k] = (k < K && k < ncand) ? rf_sel[k] : 0;
+        wk[k] = k < K ? rf_p[selk[k]] : 0.f;
+    }
     // weights from the unbiased probabilities, renormalised in round order
     float sw = 0.f;
-    for (int k = 0; k < K; ++k) sw += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wv), k));
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        if (k < K) sw += wk[k];
     if (lane < K) {
-        const float wk = (sw > 1e-8f) ? wv * (1.0f / sw) : 1.0f / (float)K;
+        int mine = 0;
+        float wv = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k == lane) {
+                mine = selk[k];
+                wv = wk[k];
+            }
+        const float w = (sw > 1e-8f) ? wv * (1.0f / sw) : 1.0f / (float)K;
         if (idx) idx[(size_t)t * K + lane] = mine;
-        if (wout) wout[(size_t)t * K + lane] = wk;
+        if (wout) wout[(size_t)t * K + lane] = w;
         if (sel_lds) sel_lds[lane] = mine;
-        if (wsel_lds) wsel_lds[lane] = wk;
+        if (wsel_lds) wsel_lds[lane] = w;
     }
     if (probs && lane < ne) probs[(size_t)t * ne + lane] = p;
 }

@@ -71,3 +71,28 @@ def test_product_has_no_cpu_fallback():
         pytest.skip("a GPU is present")
     lib = gh.load(init_device=False)
     assert lib.gh_init(0) != 0
+
+
+def test_m0_only_set_for_lds_transfers(tmp_path):
+    """The direct global -> LDS transfers set M0 from inline assembly. M0 is a register the
+    compiler reserves (a clobber on it is rejected), so the guard is the generated code: in
+    every file that issues such transfers, each M0 write is ours, immediately followed by its
+    global_load_lds_dwordx4, and no compiler-generated instruction reads or writes M0."""
+    import os
+    import re
+    import subprocess
+    src = os.path.join(os.path.dirname(gh.LIB_PATH), "csrc")
+    for f in ("gemv_mfma", "attention", "gemm", "decode_persistent"):
+        out = tmp_path / (f + ".s")
+        subprocess.run(["/opt/rocm/bin/hipcc", "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang",
+                        "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+                        os.path.join(src, f + ".hip"), "-o", str(out)], check=True, capture_output=True)
+        lines = [ln.strip() for ln in out.read_text().splitlines()]
+        n = 0
+        for i, ln in enumerate(lines):
+            if ln.startswith(";") or not re.search(r"\bm0\b", ln):
+                continue
+            assert ln.startswith("s_mov_b32 m0,"), f"{f}: compiler use of m0: {ln}"
+            assert lines[i + 1].startswith("global_load_lds_dwordx4"), f"{f}: {ln} / {lines[i + 1]}"
+            n += 1
+        assert n > 0, f
