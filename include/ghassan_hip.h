@@ -212,9 +212,11 @@ int gh_gguf_get_u64(const gh_gguf* f, const char* key, uint64_t* out);
 int gh_gguf_get_f32(const gh_gguf* f, const char* key, float* out);
 int gh_gguf_get_str(const gh_gguf* f, const char* key, char* buf, size_t cap);
 /* read_tensor_quant (gguf_codec.cpp:1450-1501): kind 0 Q4_0, 1 Q4_1, 2 Q8_0, 3 Q4_K. A file
- * tensor of that GGML type is copied verbatim; an F32/F16 one is quantised on the host. */
+ * tensor of that GGML type is copied verbatim; any other decodable type (F32, F16, Q4_0,
+ * Q4_1, Q8_0, Q4_K, Q5_K, Q6_K) is decoded to fp32 and quantised on the host. */
 int gh_gguf_read_packed(const gh_gguf* f, const char* name, int kind, void* dst, int dst_dev, size_t cap_bytes);
-/* read_tensor_f32 for F32 / F16 tensors; read_f16: the same as fp16 (F16 verbatim). */
+/* read_tensor_f32 (F32 / F16 in the reference), here for every decodable type above;
+ * read_f16: the same rounded to fp16 (F16 verbatim). */
 int gh_gguf_read_f32(const gh_gguf* f, const char* name, float* dst, int dst_dev, size_t cap_elems);
 int gh_gguf_read_f16(const gh_gguf* f, const char* name, uint16_t* dst, int dst_dev, size_t cap_elems);
 /* GGUFWriter (gguf_codec.h:64-130) for already-packed host data: GGUF v3, types as above,

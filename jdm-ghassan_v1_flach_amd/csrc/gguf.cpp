@@ -28,7 +28,7 @@
 
 namespace {
 
-enum : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q4_0 = 2, GT_Q4_1 = 3, GT_Q8_0 = 8, GT_Q4_K = 12 };
+enum : uint32_t { GT_F32 = 0, GT_F16 = 1, GT_Q4_0 = 2, GT_Q4_1 = 3, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14 };
 enum : uint32_t {
     KV_U8 = 0, KV_I8 = 1, KV_U16 = 2, KV_I16 = 3, KV_U32 = 4, KV_I32 = 5, KV_F32 = 6, KV_BOOL = 7,
     KV_STR = 8, KV_ARR = 9, KV_U64 = 10, KV_I64 = 11, KV_F64 = 12
@@ -46,6 +46,8 @@ void ggml_block(uint32_t t, uint64_t& vals, uint64_t& bytes) {
         case GT_Q4_1: vals = 32; bytes = 20; break;
         case GT_Q8_0: vals = 32; bytes = 34; break;
         case GT_Q4_K: vals = 256; bytes = 144; break;
+        case GT_Q5_K: vals = 256; bytes = 176; break;
+        case GT_Q6_K: vals = 256; bytes = 210; break;
         default: break;
     }
 }
@@ -167,21 +169,124 @@ int copy_out(void* dst, int dst_dev, const void* src, size_t bytes) {
     return GH_OK;
 }
 
-// F32 / F16 tensor -> fp32 host values
+// ---- block decoders (host), fp32 arithmetic without fused multiply-add. Q4_0 / Q4_1 /
+// Q8_0 as quantization/quantize.cpp:114-133 dequantizes them; the K-quants (absent from the
+// reference) by the GGML block layouts: 256 values per super-block, fp16 d (and dmin), 32- or
+// 16-value sub-blocks with their own scales.
+#pragma clang fp contract(off)
+float h16(const uint8_t* p) {
+    uint16_t h;
+    memcpy(&h, p, 2);
+    return half_bits_to_f32(h);
+}
+// the 6-bit (scale, min) pair j of a Q4_K / Q5_K header's 12 scale bytes
+void k_scale_min(const uint8_t* sc, int j, int& s, int& m) {
+    if (j < 4) {
+        s = sc[j] & 63;
+        m = sc[j + 4] & 63;
+    } else {
+        s = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
+        m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+}
+// Q4_K (144 B): d, dmin, scales[12], qs[128]; byte 32 i + l holds value l of sub-block 2 i
+// (low nibble) and of sub-block 2 i + 1 (high nibble); v = (d s_j) q - dmin m_j.
+void dec_q4_k(const uint8_t* b, float* y) {
+    const float d = h16(b), dmin = h16(b + 2);
+    for (int j = 0; j < 8; ++j) {
+        int s, m;
+        k_scale_min(b + 4, j, s, m);
+        const float d1 = d * (float)s, m1 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t q = b[16 + 32 * (j >> 1) + l];
+            y[32 * j + l] = d1 * (float)((j & 1) ? (q >> 4) : (q & 0xF)) - m1;
+        }
+    }
+}
+// Q5_K (176 B): d, dmin, scales[12], qh[32], qs[128]: as Q4_K, the fifth bit of value l of
+// sub-block j is bit j of qh[l].
+void dec_q5_k(const uint8_t* b, float* y) {
+    const float d = h16(b), dmin = h16(b + 2);
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48;
+    for (int j = 0; j < 8; ++j) {
+        int s, m;
+        k_scale_min(b + 4, j, s, m);
+        const float d1 = d * (float)s, m1 = dmin * (float)m;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t q = qs[32 * (j >> 1) + l];
+            const int v = ((j & 1) ? (q >> 4) : (q & 0xF)) | (((qh[l] >> j) & 1) << 4);
+            y[32 * j + l] = d1 * (float)v - m1;
+        }
+    }
+}
+// Q6_K (210 B): ql[128], qh[64], scales[16] (int8), d. In each half (128 values) h, value
+// 32 r + l (r = 0..3) takes the low nibble of ql[64 h + l] (r = 0), of ql[64 h + 32 + l]
+// (r = 1), the high nibbles of the same bytes (r = 2, 3), and bits 2 r, 2 r + 1 of
+// qh[32 h + l] above them; v = (d sc) (q - 32) with sc = scales[8 h + 2 r + l / 16].
+void dec_q6_k(const uint8_t* b, float* y) {
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    const int8_t* sc = (const int8_t*)(b + 192);
+    const float d = h16(b + 208);
+    for (int h = 0; h < 2; ++h)
+        for (int r = 0; r < 4; ++r)
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t lb = ql[64 * h + 32 * (r & 1) + l];
+                const int lo = (r < 2) ? (lb & 0xF) : (lb >> 4);
+                const int q = lo | (((qh[32 * h + l] >> (2 * r)) & 3) << 4);
+                y[128 * h + 32 * r + l] = (d * (float)sc[8 * h + 2 * r + l / 16]) * (float)(q - 32);
+            }
+}
+void dec_q8_0(const uint8_t* b, float* y) {
+    const float d = h16(b);
+    for (int i = 0; i < 32; ++i) y[i] = (float)(int8_t)b[2 + i] * d;
+}
+void dec_q4_0(const uint8_t* b, float* y) {
+    const float d = h16(b);
+    for (int i = 0; i < 16; ++i) {
+        y[i] = (float)((b[2 + i] & 0xF) - 8) * d;
+        y[i + 16] = (float)((b[2 + i] >> 4) - 8) * d;
+    }
+}
+void dec_q4_1(const uint8_t* b, float* y) {
+    const float d = h16(b), m = h16(b + 2);
+    for (int i = 0; i < 16; ++i) {
+        y[i] = (float)(b[4 + i] & 0xF) * d + m;
+        y[i + 16] = (float)(b[4 + i] >> 4) * d + m;
+    }
+}
+#pragma clang fp contract(on)
+
+// any supported tensor -> fp32 host values (the reference's read_tensor_f32 / the decode step
+// of read_tensor_quant's slow path, gguf_codec.cpp:1495-1500)
 int decode_f32(const gh_gguf* g, const Tensor& t, std::vector<float>& out) {
     const uint8_t* src = g->map + g->data_start + t.offset;
     out.resize((size_t)t.numel);
     if (t.type == GT_F32) {
         memcpy(out.data(), src, (size_t)t.numel * 4);
-    } else if (t.type == GT_F16) {
-        for (uint64_t i = 0; i < t.numel; ++i) {
-            uint16_t h;
-            memcpy(&h, src + 2 * i, 2);
-            out[(size_t)i] = half_bits_to_f32(h);
-        }
-    } else {
-        return gh::fail(GH_EUNSUPPORTED, "gguf: tensor '%s' is GGML type %u, not F32/F16", t.name.c_str(), t.type);
+        return GH_OK;
     }
+    if (t.type == GT_F16) {
+        for (uint64_t i = 0; i < t.numel; ++i) out[(size_t)i] = h16(src + 2 * i);
+        return GH_OK;
+    }
+    void (*dec)(const uint8_t*, float*) = nullptr;
+    switch (t.type) {
+        case GT_Q4_0: dec = dec_q4_0; break;
+        case GT_Q4_1: dec = dec_q4_1; break;
+        case GT_Q8_0: dec = dec_q8_0; break;
+        case GT_Q4_K: dec = dec_q4_k; break;
+        case GT_Q5_K: dec = dec_q5_k; break;
+        case GT_Q6_K: dec = dec_q6_k; break;
+        default:
+            return gh::fail(GH_EUNSUPPORTED, "gguf: tensor '%s' has GGML type %u, which cannot be decoded",
+                            t.name.c_str(), t.type);
+    }
+    uint64_t bv, bb;
+    ggml_block(t.type, bv, bb);
+    const uint64_t nb = t.numel / bv;
+    for (uint64_t i = 0; i < nb; ++i) dec(src + i * bb, out.data() + i * bv);
     return GH_OK;
 }
 

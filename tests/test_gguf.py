@@ -16,7 +16,7 @@ import oracle_lib as O
 from conftest import GOLDEN, golden
 
 REF_FILE = os.path.join(GOLDEN, "ref_small.gguf")
-GT = dict(F32=0, F16=1, Q4_0=2, Q4_1=3, Q8_0=8, Q4_K=12)
+GT = dict(F32=0, F16=1, Q4_0=2, Q4_1=3, Q8_0=8, Q4_K=12, Q5_K=13, Q6_K=14)
 
 
 @pytest.fixture(scope="module")
@@ -200,9 +200,10 @@ def test_write_read_q4k_roundtrip(lib, tmp_path, align):
         u = C.c_uint64()
         check(lib, lib.gh_gguf_get_u64(h, b"ghassan.context_length", C.byref(u)))
         assert u.value == 4096
-        # a Q4_K tensor asked for as Q8_0 is not decoded here: an error, not a silent conversion
-        with pytest.raises(RuntimeError, match="not F32/F16"):
-            read_packed(lib, h, "layers.3.mamba.in_proj", 2, 12 * 16 * 34)
+        # a Q4_K tensor asked for as Q8_0: decoded and quantised again (read_tensor_quant's
+        # slow path, format/gguf_codec.cpp:1495-1500)
+        want = O.quantize(2, O.dequantize(3, w4, 12 * 512))
+        assert np.array_equal(read_packed(lib, h, "layers.3.mamba.in_proj", 2, 12 * 16 * 34), want.view(np.uint8))
         with pytest.raises(RuntimeError, match="needs"):
             read_packed(lib, h, "layers.3.mamba.in_proj", 3, w4.nbytes - 1)
     finally:
@@ -221,19 +222,156 @@ def test_rejects_bad_files(lib, tmp_path):
     p.write_bytes(good[:4] + struct.pack("<I", 4) + good[8:])
     assert lib.gh_gguf_open(str(p).encode(), C.byref(h)) != 0
     assert "unsupported version" in lib.gh_last_error().decode()
-    # a Q6_K (type 14) tensor: refused by name, like the reference
-    q6 = np.zeros(210, np.uint8)
+    # a tensor of a GGML type the backend does not decode (15, Q8_K): refused by name
     write(lib, str(p), [("x", GT["Q8_0"], [256], np.zeros(8 * 34, np.uint8))], [])
     b = bytearray(open(p, "rb").read())
     _, _, infos, _, _ = parse(str(p))
     i = b.find(b"x") + 1 + 4 + 8  # name, ndims, dims -> type
-    b[i:i + 4] = struct.pack("<I", 14)
+    b[i:i + 4] = struct.pack("<I", 15)
     p.write_bytes(bytes(b))
     assert lib.gh_gguf_open(str(p).encode(), C.byref(h)) != 0
-    assert "unsupported GGML type 14" in lib.gh_last_error().decode()
-    del q6
+    assert "unsupported GGML type 15" in lib.gh_last_error().decode()
     # a tensor whose data would run past the end of the file
     write(lib, str(p), [("x", GT["F32"], [64], np.zeros(64, np.float32))], [])
     p.write_bytes(open(p, "rb").read()[:-8])
     assert lib.gh_gguf_open(str(p).encode(), C.byref(h)) != 0
     assert "overruns" in lib.gh_last_error().decode()
+
+
+# ---- K-quant super-blocks of real Granite-4.0-H files (Q4_K_M carries Q6_K tensors). The
+# reference has no K-quant decoder: these are pinned by hand-built blocks with closed-form
+# values and by an independent numpy decoder written from the GGML block layouts.
+def f16b(v):
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def pack_k_scales(sc, mn):
+    """The 12-byte (6-bit scale, 6-bit min) packing of Q4_K / Q5_K."""
+    s12 = np.zeros(12, np.int64)
+    for j in range(4):
+        s12[j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        s12[j + 4] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        s12[j + 8] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    return s12.astype(np.uint8)
+
+
+def np_q5_k(b):
+    """float32 arithmetic in the decoder's order: (d s) q - dmin m."""
+    b = b.reshape(-1, 176)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    s = b[:, 4:16].astype(np.int64)
+    qh, qs = b[:, 16:48].astype(np.int64), b[:, 48:176].astype(np.int64)
+    out = np.empty((b.shape[0], 256), np.float32)
+    for j in range(8):
+        if j < 4:
+            sc, mn = s[:, j] & 63, s[:, j + 4] & 63
+        else:
+            sc = (s[:, j + 4] & 0xF) | ((s[:, j - 4] >> 6) << 4)
+            mn = (s[:, j + 4] >> 4) | ((s[:, j] >> 6) << 4)
+        q = qs[:, 32 * (j // 2): 32 * (j // 2) + 32]
+        q = (q >> 4) if j % 2 else (q & 0xF)
+        q = q | (((qh >> j) & 1) << 4)
+        d1 = (d * sc.astype(np.float32)).astype(np.float32)
+        m1 = (dmin * mn.astype(np.float32)).astype(np.float32)
+        out[:, 32 * j: 32 * j + 32] = (d1[:, None] * q.astype(np.float32)).astype(np.float32) - m1[:, None]
+    return out.ravel()
+
+
+def np_q6_k(b):
+    """float32 arithmetic in the decoder's order: (d sc) (q - 32)."""
+    b = b.reshape(-1, 210)
+    ql, qh = b[:, 0:128].astype(np.int64), b[:, 128:192].astype(np.int64)
+    sc = b[:, 192:208].view(np.int8).astype(np.float32)
+    d = b[:, 208:210].copy().view(np.float16).astype(np.float32)[:, 0]
+    out = np.empty((b.shape[0], 256), np.float32)
+    for h in range(2):
+        for r in range(4):
+            lb = ql[:, 64 * h + 32 * (r % 2): 64 * h + 32 * (r % 2) + 32]
+            lo = (lb & 0xF) if r < 2 else (lb >> 4)
+            q = lo | (((qh[:, 32 * h: 32 * h + 32] >> (2 * r)) & 3) << 4)
+            s = np.repeat(sc[:, 8 * h + 2 * r: 8 * h + 2 * r + 2], 16, axis=1)
+            out[:, 128 * h + 32 * r: 128 * h + 32 * r + 32] = ((d[:, None] * s).astype(np.float32) *
+                                                               (q - 32).astype(np.float32))
+    return out.ravel()
+
+
+def decode_via_file(lib, tmp_path, gtype, blocks, nvals):
+    p = str(tmp_path / "k.gguf")
+    write(lib, p, [("t", gtype, [256, nvals // 256], blocks)], [])
+    h = open_file(lib, p)
+    try:
+        return read_f32(lib, h, "t", nvals)
+    finally:
+        lib.gh_gguf_close(h)
+
+
+def test_q6_k_closed_form(lib, tmp_path):
+    """d = 0.5, scales[i] = i - 8, and value v of the super-block carrying code (v * 7) % 64:
+    every value is 0.5 * sc * (code - 32) with its scale picked by the layout."""
+    codes = (np.arange(256) * 7) % 64
+    blk = np.zeros(210, np.uint8)
+    for h in range(2):
+        for r in range(4):
+            for l in range(32):
+                c = int(codes[128 * h + 32 * r + l])
+                i = 64 * h + 32 * (r % 2) + l
+                blk[i] |= (c & 0xF) << (0 if r < 2 else 4)
+                blk[128 + 32 * h + l] |= (c >> 4) << (2 * r)
+    blk[192:208] = (np.arange(16) - 8).astype(np.int8).view(np.uint8)
+    blk[208:210] = f16b(0.5)
+    want = np.array([0.5 * ((v // 128) * 8 + 2 * ((v % 128) // 32) + (v % 32) // 16 - 8) * (codes[v] - 32)
+                     for v in range(256)], np.float64)
+    got = decode_via_file(lib, tmp_path, GT["Q6_K"], blk, 256)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_q5_k_closed_form(lib, tmp_path):
+    """d = 2, dmin = 0.25, scale j = 2 j + 1, min j = 3 j, code of value v = v % 32 (the
+    fifth bit in qh): value = 2 (2 j + 1) code - 0.25 (3 j)."""
+    codes = np.arange(256) % 32
+    blk = np.zeros(176, np.uint8)
+    blk[0:2], blk[2:4] = f16b(2.0), f16b(0.25)
+    blk[4:16] = pack_k_scales(2 * np.arange(8) + 1, 3 * np.arange(8))
+    for j in range(8):
+        for l in range(32):
+            c = int(codes[32 * j + l])
+            blk[48 + 32 * (j // 2) + l] |= (c & 0xF) << (4 if j % 2 else 0)
+            blk[16 + l] |= (c >> 4) << j
+    want = np.array([2.0 * (2 * (v // 32) + 1) * codes[v] - 0.25 * 3 * (v // 32) for v in range(256)])
+    got = decode_via_file(lib, tmp_path, GT["Q5_K"], blk, 256)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("gtype,nb,dec", [("Q5_K", 176, np_q5_k), ("Q6_K", 210, np_q6_k)])
+def test_k_quant_random_blocks(lib, tmp_path, gtype, nb, dec):
+    """Random super-blocks (finite fp16 scales) decode bit-exactly as the independent numpy
+    decoder computes them in fp32."""
+    rs = np.random.RandomState(7)
+    blocks = rs.randint(0, 256, size=(24, nb)).astype(np.uint8)
+    dpos = [0, 2] if gtype == "Q5_K" else [208]
+    for o in dpos:
+        blocks[:, o:o + 2] = np.float16(rs.uniform(-0.05, 0.05, 24)).view(np.uint8).reshape(24, 2)
+    got = decode_via_file(lib, tmp_path, GT[gtype], blocks.ravel(), 24 * 256)
+    assert np.array_equal(got.view(np.uint32), dec(blocks.ravel()).view(np.uint32))
+
+
+def test_k_quant_read_as_model_kind(lib, tmp_path):
+    """A Q6_K tensor read as the model's Q4_K / Q8_0 storage: decoded, then quantised by the
+    backend's own quantiser (read_tensor_quant's slow path), and as fp16 for the lm head."""
+    rs = np.random.RandomState(8)
+    blocks = rs.randint(0, 256, size=(8, 210)).astype(np.uint8)
+    blocks[:, 208:210] = np.float16(rs.uniform(0.001, 0.01, 8)).view(np.uint8).reshape(8, 2)
+    vals = np_q6_k(blocks.ravel())
+    p = str(tmp_path / "q6.gguf")
+    write(lib, p, [("output.weight", GT["Q6_K"], [512, 4], blocks.ravel())], [])
+    h = open_file(lib, p)
+    try:
+        for kind in (3, 2):
+            nbytes = O.quantize(kind, vals).nbytes
+            assert np.array_equal(read_packed(lib, h, "lm_head", kind, nbytes), O.quantize(kind, vals).view(np.uint8))
+        out = np.zeros(2048, np.uint16)
+        check(lib, lib.gh_gguf_read_f16(h, b"lm_head", out.ctypes.data_as(C.c_void_p), 0, C.c_size_t(2048)))
+        assert np.array_equal(out, O.f32_to_f16(vals))
+    finally:
+        lib.gh_gguf_close(h)
