@@ -342,6 +342,42 @@ def cpu_baseline(prompt, n_prefill=PROMPT, n_new=N_NEW):
                       f"prefill {secs[0]:.2f} s, decode {secs[1]:.2f} s"}
 
 
+def calibrate(n_prefill=PROMPT, n_new=N_NEW):
+    """Calibration row: the genuine reference CPU Generator (oracle/_ref, compiled from the
+    reference sources in the build container; test infrastructure) and the CPU oracle timed on
+    the same c1 Q8_0 workload (the reference has no K-quants), with equal greedy ids checked.
+    The ratio says how closely the restated port's speed tracks the original's."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    if not O.ref_available():
+        return {"skipped": "oracle/_ref/libgai_ref.so is not built here"}
+    w = O.granite_weights(O.C1, 2)
+    names, ptrs, npar = O._param_arrays(w)
+    cfg, fcfg = O.granite_cfg(O.C1, 2)
+    pr = O.rng_below(1, n_prefill, O.C1["V"])
+    out = {}
+    for kind, fn in (("reference", O.ref().ref_granite_generate_timed),
+                     ("port", O.oracle().orc_granite_generate_timed)):
+        ids = np.zeros(n_new, np.int32)
+        mg = np.zeros(n_new, np.float32)
+        secs = np.zeros(2, np.float64)
+        rc = fn(O.P(cfg), O.P(fcfg), names, ptrs, npar, O.P(pr), n_prefill, n_new, MAX_CTX, O.P(ids), O.P(mg),
+                secs.ctypes.data_as(C.c_void_p))
+        assert rc == 0, (kind, rc)
+        out[kind] = {"decode_tok_s": round((n_new - 1) / secs[1], 3), "prefill_tok_s": round(n_prefill / secs[0], 3),
+                     "ids": ids}
+    same = int(np.argmin(out["reference"]["ids"] == out["port"]["ids"])) if not np.array_equal(
+        out["reference"]["ids"], out["port"]["ids"]) else n_new
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    for v in out.values():
+        v.pop("ids")
+    return {"workload": f"c1 Q8_0, {n_prefill}-token prompt prefill + {n_new - 1} greedy decode steps",
+            "threads": threads, "reference": out["reference"], "port": out["port"],
+            "port_over_reference_decode": round(out["port"]["decode_tok_s"] / out["reference"]["decode_tok_s"], 4),
+            "port_over_reference_prefill": round(out["port"]["prefill_tok_s"] / out["reference"]["prefill_tok_s"], 4),
+            "equal_ids": same}
+
+
 COLD_COPIES = 10  # 10 x 33 MB of weights > the 256 MB Infinity Cache (MALL)
 
 
@@ -486,7 +522,12 @@ def main():
                          "5 launches each, for rocprofv3 --pmc runs")
     ap.add_argument("--probe", action="store_true",
                     help="only run the roofline GEMV and a plain copy of known size (for rocprofv3 --pmc)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="CPU only: time the compiled reference (oracle/_ref) and the CPU oracle on c1 Q8_0")
     args = ap.parse_args()
+    if args.calibrate:
+        print(json.dumps({"calibration": calibrate()}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); multi-GPU sharding is a "
               "design note, not a measured path", file=sys.stderr)
