@@ -552,7 +552,9 @@ int gh_lm_head_greedy_dev(const float* x, const float* norm_w, float eps, const 
     GH_REQUIRE(x && norm_w && tab && logits && out_dev && d > 0 && V > 0, "lm_head_greedy: bad arguments");
     int32_t* ctl = (int32_t*)workspace(WS_HEAD_CTL, CTL_N * 4);
     if (!ctl) return fail(GH_ENOMEM, "lm_head_greedy: workspace");
-    GH_HIP(hipMemsetAsync(ctl, 0, CTL_N * 4, stream()));
+    // a fill kernel, not a memset node: this entry point is meant for captured graphs
+    const int zrc = gh_zero((float*)ctl, CTL_N);
+    if (zrc) return zrc;
     if (!launch_head_argmax(x, norm_w, eps, tab, logits, d, V, ctl, nullptr, 0, true))
         return fail(GH_EUNSUPPORTED, "lm_head_greedy: d=%d (needs d %% 8 == 0, d <= 2048, 16-byte aligned rows)", d);
     GH_HIP(hipMemcpyAsync(out_dev, ctl + CTL_TOKEN, 4, hipMemcpyDeviceToDevice, stream()));
