@@ -43,7 +43,8 @@ struct GmFuse {
     int c0 = 0, cdim = 0, ck = 0;
     // start of a decode step folded into the first layer's norm prologue: the activation is the
     // fp16 embedding row of token bctl[0] (zero if out of range), block 0 also stores it to
-    // emb_out and takes the step's cache slot (decode_alloc_slot). Only the int8 Q4_K path.
+    // emb_out and takes the step's cache slot (decode_alloc_slot). Nothing else in that launch
+    // may read the slot: layer 0 must be a Mamba layer (its in_proj takes the fold).
     const uint16_t* emb = nullptr;
     float* emb_out = nullptr;
     int32_t* bctl = nullptr;

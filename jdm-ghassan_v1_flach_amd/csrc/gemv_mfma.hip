@@ -223,8 +223,33 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
         const bool gated = f.pro == GM_PRO_GATED;
         const int c0 = 8 * tid;
         const bool mine = c0 < K;
+        // the step's start folded in (layer 0 of a decode step): the input is the fp16
+        // embedding row of token bctl[0] (elementwise.hip k_embed_half: zero out of range), and
+        // the first block stores it as the step's residual stream
+        const bool emb = f.emb != nullptr;
+        const int tok = emb ? f.bctl[0] : 0;
+        const bool tok_ok = tok >= 0 && tok < f.vocab;
+        const bool emb_writer = emb && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+        auto emb8 = [&](int c, float* o) {
+            uint4 h = make_uint4(0, 0, 0, 0);
+            if (tok_ok) h = *(const uint4*)(f.emb + (size_t)tok * K + c);
+            const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                o[2 * j] = f16_to_f32((uint16_t)(hw[j] & 0xFFFF));
+                o[2 * j + 1] = f16_to_f32((uint16_t)(hw[j] >> 16));
+            }
+            if (emb_writer) {
+                *(float4*)(f.emb_out + c) = make_float4(o[0], o[1], o[2], o[3]);
+                *(float4*)(f.emb_out + c + 4) = make_float4(o[4], o[5], o[6], o[7]);
+            }
+        };
         float xr[8], wr[8], zr[8];
-        if (mine) {
+        if (mine && emb) {
+            const float4 w0 = *(const float4*)(f.pw + c0), w1 = *(const float4*)(f.pw + c0 + 4);
+            emb8(c0, xr);
+            wr[0] = w0.x; wr[1] = w0.y; wr[2] = w0.z; wr[3] = w0.w; wr[4] = w1.x; wr[5] = w1.y; wr[6] = w1.z; wr[7] = w1.w;
+        } else if (mine) {
             const float4 x0 = *(const float4*)(x + c0), x1 = *(const float4*)(x + c0 + 4);
             const float4 w0 = *(const float4*)(f.pw + c0), w1 = *(const float4*)(f.pw + c0 + 4);
             xr[0] = x0.x; xr[1] = x0.y; xr[2] = x0.z; xr[3] = x0.w; xr[4] = x1.x; xr[5] = x1.y; xr[6] = x1.z; xr[7] = x1.w;
@@ -244,13 +269,18 @@ __device__ void gm_prologue(const float* __restrict__ x, int K, const GmFuse& f,
                 ss += (double)v * v;
             }
         }
-        for (int c = c0 + 8 * nth; c < K; c += 8 * nth)  // chunks beyond the registers
+        for (int c = c0 + 8 * nth; c < K; c += 8 * nth) {  // chunks beyond the registers
+            float er[8];
+            if (emb) emb8(c, er);
             for (int j = 0; j < 8; ++j) {
-                float v = x[c + j];
+                float v = emb ? er[j] : x[c + j];
                 if (gated) v = v * (f.pz[c + j] / (1.0f + expf(-f.pz[c + j])));
                 xf[c + j] = v;
                 ss += (double)v * v;
             }
+        }
+        // the step's cache slot, taken once (nothing in this launch reads it)
+        if (emb_writer && tid == 0) decode_alloc_slot(f.bctl);
         const double tot = gm_block_sum_dpp(ss, red);
         float inv;
         if (gated) {
@@ -706,9 +736,10 @@ constexpr int GD_NB = 2;     // ring depth: tiles in flight per wave
 constexpr int GD_EARLY = 1;  // tiles requested before x is converted (more delay x itself)
 typedef int gd_i4 __attribute__((ext_vector_type(4)));
 
-template <int SBW>
+template <int SBW, bool Q8 = false>
 struct GdCfg {
-    static constexpr int PR = 9 * SBW;          // 16-byte pieces per row of a wave's column
+    static constexpr int SBB = Q8 ? 272 : 144;  // bytes per 256 values: 8 Q8_0 blocks / 1 Q4_K super-block
+    static constexpr int PR = SBB / 16 * SBW;   // 16-byte pieces per row of a wave's column
     static constexpr int NP = 16 * PR;          // pieces per column (16 rows)
     static constexpr int PPL = (NP + 63) / 64;  // transfers per wave and tile (the last one partial)
 };
@@ -728,11 +759,12 @@ __device__ __forceinline__ uint32_t gd_pack4(int a, int b, int c, int d) {
 __host__ __device__ constexpr size_t gd_xred_bytes(int K, int WB) {
     return (size_t)K * 4 + (size_t)2 * GD_S * (WB + 1) * 64 * 4;
 }
-static size_t gd_lds_bytes(int K, int SBW, int NB) {
+static size_t gd_lds_bytes(int K, int SBW, int NB, bool q8 = false) {
     const int WB = K / (256 * SBW);
-    return (size_t)NB * WB * 144 * SBW * 16 + gd_xred_bytes(K, WB) + 3 * (size_t)K + (size_t)K / 32 * 12 +
-           (size_t)K / 32 * 8;
+    return (size_t)NB * WB * (q8 ? 272 : 144) * SBW * 16 + gd_xred_bytes(K, WB) + 3 * (size_t)K +
+           (size_t)K / 32 * 12 + (size_t)K / 32 * 8;
 }
+constexpr int GD_Q8_KMAX = 2048;  // Q8_0 rows take 1.9x the ring of Q4_K: two tiles fit LDS up to here
 
 constexpr int GD_ATT_MAX = 1024;  // heads x splits of the attention-merge prologue
 constexpr int GD_ATT_PT = 8;      // (max, sum) pairs per thread: GD_ATT_MAX / 128 threads
@@ -741,12 +773,16 @@ constexpr int GD_ATT_PT = 8;      // (max, sum) pairs per thread: GD_ATT_MAX / 1
 // attention merge, the arithmetic of gm_prologue) straight into the staging
 // area instead of being copied, and every output goes through gm_epilogue
 // (STORE / ADD / CONV / QKV).
-template <int SBW, int NB, bool FUSED = false>
+// Q8: the same kernel for Q8_0 rows (34-byte blocks of 32 int8 codes and an fp16 scale, read
+// as 8-block groups of 272 bytes in place of a 144-byte super-block): lane (n, g) takes blocks
+// 2g and 2g + 1 of a group as 17 dwords, the codes realigned with alignbyte; they are int8
+// already, so no nibble or offset work, and no min term.
+template <int SBW, int NB, bool FUSED = false, bool Q8 = false>
 __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                            float* __restrict__ y, int K, int N, size_t rowb,
                                                            int rpb, GmFuse f) {
-    using C = GdCfg<SBW>;
-    constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL;
+    using C = GdCfg<SBW, Q8>;
+    constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL, SBB = C::SBB;
     extern __shared__ __attribute__((aligned(16))) uint4 gd_lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -827,7 +863,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
 #pragma unroll
     for (int i = 0; i < PPL; ++i) {
         const int q = lane + 64 * i, r = q / PR, j = q - r * PR;
-        voff[i] = (uint32_t)(r * rowb) + wave * (144 * SBW) + 16 * j;
+        voff[i] = (uint32_t)(r * rowb) + wave * (SBB * SBW) + 16 * j;
     }
     // tile it of the block -> ring slice b
     auto dma = [&](int it, int b) {
@@ -852,7 +888,7 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
                 const int q = lane + 64 * i;
                 if (NP % 64 == 0 || i + 1 < PPL || q < NP) {
                     const int r = q / PR;
-                    lds_dma16s(base, r < nv ? voff[i] : (uint32_t)(wave * (144 * SBW)), lds_addr(dst + 64 * i));
+                    lds_dma16s(base, r < nv ? voff[i] : (uint32_t)(wave * (SBB * SBW)), lds_addr(dst + 64 * i));
                 }
             }
         }
@@ -1026,19 +1062,55 @@ __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restr
         // tiles issued after this one: it+1 .. min(it+NB-1, nt-1)
         const int ahead = min(NB - 1, nt - 1 - it);
         lds_dma_wait<PPL>(ahead);
-        const unsigned char* rowp = (const unsigned char*)(ring + ((size_t)b * WB + wave) * NP) + n16 * (144 * SBW);
+        const unsigned char* rowp = (const unsigned char*)(ring + ((size_t)b * WB + wave) * NP) + n16 * (SBB * SBW);
         uint4 hd[SBW], qa[SBW], qb[SBW];
+        uint32_t q8w[Q8 ? SBW : 1][17];
+        if constexpr (Q8) {
 #pragma unroll
-        for (int sbl = 0; sbl < SBW; ++sbl) {
-            hd[sbl] = *(const uint4*)(rowp + 144 * sbl);
-            qa[sbl] = *(const uint4*)(rowp + 144 * sbl + 16 + 32 * g);
-            qb[sbl] = *(const uint4*)(rowp + 144 * sbl + 32 + 32 * g);
+            for (int sbl = 0; sbl < SBW; ++sbl) {
+                const uint32_t* rp = (const uint32_t*)(rowp + SBB * sbl + 68 * g);  // blocks 2g, 2g + 1
+#pragma unroll
+                for (int k = 0; k < 17; ++k) q8w[sbl][k] = rp[k];
+            }
+        } else {
+#pragma unroll
+            for (int sbl = 0; sbl < SBW; ++sbl) {
+                hd[sbl] = *(const uint4*)(rowp + 144 * sbl);
+                qa[sbl] = *(const uint4*)(rowp + 144 * sbl + 16 + 32 * g);
+                qb[sbl] = *(const uint4*)(rowp + 144 * sbl + 32 + 32 * g);
+            }
         }
         if (it + NB < nt) {  // slice read: refill it
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             dma(it + NB, b);
         }
         float acc = 0.f;
+        if constexpr (Q8) {
+#pragma unroll
+            for (int sbl = 0; sbl < SBW; ++sbl) {
+                const uint32_t* w = q8w[sbl];
+                // block 2g: d in bytes 0-1, codes in bytes 2-33; block 2g + 1: d in 34-35, codes 36-67
+                gd_i4 c0[2], c1[2];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    c0[r] = gd_i4{(int)__builtin_amdgcn_alignbyte(w[4 * r + 1], w[4 * r], 2),
+                                  (int)__builtin_amdgcn_alignbyte(w[4 * r + 2], w[4 * r + 1], 2),
+                                  (int)__builtin_amdgcn_alignbyte(w[4 * r + 3], w[4 * r + 2], 2),
+                                  (int)__builtin_amdgcn_alignbyte(w[4 * r + 4], w[4 * r + 3], 2)};
+                    c1[r] = gd_i4{(int)w[9 + 4 * r], (int)w[10 + 4 * r], (int)w[11 + 4 * r], (int)w[12 + 4 * r]};
+                }
+                gd_i4 Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][0][0], c0[0], gd_i4{0, 0, 0, 0}, 0, 0, 0);
+                gd_i4 Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][1][0], c1[0], gd_i4{0, 0, 0, 0}, 0, 0, 0);
+                Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][0][1], c0[1], Dl, 0, 0, 0);
+                Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[sbl][1][1], c1[1], Dh, 0, 0, 0);
+                const float d0 = gm_lo16(w[0]), d1 = gm_hi16(w[8]);
+                // |D0| <= 32 * 127 * 127 < 2^24: each part sum is exact in fp32, and so are the
+                // power-of-two weights of 16384 D0 + 128 D1 + D2 (their sum rounds once or twice)
+                const float il = (float)Dl[0] * 16384.f + (float)Dl[1] * 128.f + (float)Dl[2];
+                const float ih = (float)Dh[0] * 16384.f + (float)Dh[1] * 128.f + (float)Dh[2];
+                acc += d0 * s_lo[sbl] * il + d1 * s_hi[sbl] * ih;
+            }
+        } else
 #pragma unroll
         for (int sbl = 0; sbl < SBW; ++sbl) {
             const gd_i4 la = gd_lo_codes(qa[sbl]), lb = gd_lo_codes(qb[sbl]);
@@ -1174,21 +1246,24 @@ static int gm_kind(const float* x, const void* w, float* y, int M, int K, int N)
     return gm_ss<KIND, 4>(x, w, y, M, K, N);
 }
 
-template <int SBW, int NB, bool FUSED = false>
+template <int SBW, int NB, bool FUSED = false, bool Q8 = false>
 static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, const GmFuse& f = GmFuse{}) {
     static int configured = 0;
     static int per_cu[17];  // resident blocks per CU by K / (256 SBW)
-    const size_t lds = gd_lds_bytes(K, SBW, NB);
+    if (K > (Q8 ? GD_Q8_KMAX : 4096) || K % (256 * SBW) != 0)
+        return fail(GH_EUNSUPPORTED, "k_gemv_q4k_i8: K=%d", K);
+    const size_t lds = gd_lds_bytes(K, SBW, NB, Q8);
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB, FUSED>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)gd_lds_bytes(4096, SBW, NB));
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB, FUSED, Q8>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)gd_lds_bytes(Q8 ? GD_Q8_KMAX : 4096, SBW, NB, Q8));
         if (e != hipSuccess) return fail(GH_EHIP, "k_gemv_q4k_i8 LDS attribute: %s", hipGetErrorString(e));
         configured = 1;
     }
     const int wb = K / (256 * SBW);
     if (!per_cu[wb]) {
         int nb = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED>, 64 * wb, lds);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED, Q8>, 64 * wb, lds);
         per_cu[wb] = e == hipSuccess && nb > 0 ? nb : 1;
     }
     // contiguous row ranges, equal up to 8 rows (16 with weight segments): every block
@@ -1197,8 +1272,8 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, c
     const int align = FUSED && f.w1 ? 16 : 8;
     const int rpb = ((N + slots - 1) / slots + align - 1) / align * align;
     const int blocks = (N + rpb - 1) / rpb;
-    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K, N,
-                       row_bytes(3, K), rpb, f);
+    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED, Q8>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K,
+                       N, row_bytes(Q8 ? 2 : 3, K), rpb, f);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
 }
@@ -1248,7 +1323,8 @@ int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, 
         // streaming GEMV
         return gd_launch<1, GD_NB, true>(x, (const uint8_t*)w, y, K, N, f);
     }
-    if (f.emb) return GH_EUNSUPPORTED;  // the folded step start exists on the int8 path only (no launch made)
+    // the folded step start needs the norm prologue and aligned rows (no launch made otherwise)
+    if (f.emb && !emb_ok) return GH_EUNSUPPORTED;
     if (f.w1 && (f.n0 % 16 || f.n1 % 16)) return fail(GH_EINVAL, "gemv_fused: segments must be multiples of 16 rows");
     if (f.pro == GM_PRO_ATTN && (f.splits > 64 || f.H * f.hd != K))
         return fail(GH_EUNSUPPORTED, "gemv_fused: attention merge of %d splits", f.splits);

@@ -265,7 +265,14 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
     __shared__ __attribute__((aligned(16))) unsigned char smem[U_STATE > U_CB ? U_STATE : U_CB];
     const int nch = (T + L - 1) / L;
     if ((int)blockIdx.x >= nch * H) {
-        const int b = blockIdx.x - nch * H, nt = L / 64;
+        const int nt = L / 64;
+        int b = blockIdx.x - nch * H;
+        if (nch % 8 == 0 && (nch * H) % 8 == 0) {
+            // the tiles of chunk c on XCD c % 8 (block index modulo 8), so one L2 holds that
+            // chunk's B and C rows for all its tiles
+            const int x = b % 8, k = b / 8;
+            b = (x + 8 * (k / (nt * nt))) * nt * nt + k % (nt * nt);
+        }
         ssd_cb_block<N>(Bm, Cm, ldb, G, C16, T, L, b / (nt * nt), (b / nt) % nt * 64, b % nt * 64,
                         (_Float16*)smem, (_Float16*)smem + 64 * SN);
         return;
@@ -410,11 +417,27 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
     __shared__ float scum[256], sdt[256], sw[256];
     __shared__ int sfast[16];
     const int nch = (T + L - 1) / L, nitems = nch * H;
-    // block b -> item (chunk, head) and p half: the two halves of an item are blocks b and b + 8,
-    // which the dispatcher places on the same XCD (one L2 for the shared G / C / X reads)
-    const int b = blockIdx.x, it = (b / 16) * 8 + (b % 8), ph = (b / 8) % 2;
-    if (it >= nitems) return;
-    const int c = nch - 1 - it / H, h = it % H, pc0 = PH * ph;
+    // block b -> item (chunk, head) and p half. The dispatcher places block b on XCD b % 8. With
+    // nch a multiple of 8, XCD x takes the chunks x, x + 8, ... of every head (its L2 then
+    // fetches only those chunks' G / C fragments, which all heads share), the two halves of an
+    // item on its consecutive blocks b, b + 8; otherwise items go round the XCDs, halves again
+    // on blocks b and b + 8 (one L2 for the item's X reads).
+    const int b = blockIdx.x;
+    int c, h, ph;
+    if (nch % 8 == 0) {
+        const int k = b / 8;  // the block's place on its XCD
+        ph = k % 2;
+        h = (k / 2) % H;
+        c = b % 8 + 8 * (k / (2 * H));
+        if (c >= nch) return;
+    } else {
+        const int it = (b / 16) * 8 + (b % 8);
+        ph = (b / 8) % 2;
+        if (it >= nitems) return;
+        c = nch - 1 - it / H;
+        h = it % H;
+    }
+    const int pc0 = PH * ph;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = c * L, len = min(L, T - t0);
     constexpr float LOG2E = 1.4426950408889634f;

@@ -42,7 +42,8 @@ def oracle_scan(case, T, H, P, N):
     return y, st
 
 
-@pytest.mark.parametrize("T,H,N,chunk", [(1, 2, 64, 256), (100, 3, 64, 64), (300, 4, 128, 256), (513, 2, 128, 128)])
+@pytest.mark.parametrize("T,H,N,chunk", [(1, 2, 64, 256), (100, 3, 64, 64), (300, 4, 128, 256), (513, 2, 128, 128),
+                                         (1000, 3, 64, 128), (2048, 5, 128, 256)])
 def test_ssd_scan_small(gh, T, H, N, chunk):
     case = scan_case(T, H, 64, N, 10 + T)
     y, st = gpu_scan(gh, case, T, H, 64, N, chunk)
