@@ -1295,6 +1295,10 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
         *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, 1);
         return 1;
     }
+    if (M == 1 && kind == 2 && K % 256 == 0 && K <= GD_Q8_KMAX && ((uintptr_t)w & 15) == 0) {
+        *rc = gd_launch<1, GD_NB, false, true>(x, (const uint8_t*)w, y, K, N);
+        return 1;
+    }
     if ((kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
     int mc = M;
     while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc, false) : gm_fits<2>(K, mc, false))) --mc;
@@ -1317,11 +1321,15 @@ int gemv_fused(const float* x, const void* w, float* y, int K, int N, int kind, 
                                                  f.H * f.splits <= GD_ATT_MAX && (((uintptr_t)f.o_part) & 15) == 0);
     const bool emb_ok = !f.emb || (f.pro == GM_PRO_RMSNORM && f.bctl && f.emb_out && f.vocab > 0 &&
                                    (((uintptr_t)f.emb | (uintptr_t)f.emb_out) & 15) == 0);
-    if (kind == 3 && K <= 4096 && att_ok && emb_ok && (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
-        (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz) & 15) == 0) {
+    const bool i8_ok = (kind == 3 ? K <= 4096 : K <= GD_Q8_KMAX) && att_ok && emb_ok &&
+                       (!f.w1 || (f.n0 % 16 == 0 && f.n1 % 16 == 0)) &&
+                       (((uintptr_t)x | (uintptr_t)f.pw | (uintptr_t)f.pz | (uintptr_t)w | (uintptr_t)f.w1 |
+                         (uintptr_t)f.w2) & 15) == 0;
+    if (i8_ok) {
         // norm prologue, weight segments, residual / conv / K-V cache epilogue on the int8-MFMA
         // streaming GEMV
-        return gd_launch<1, GD_NB, true>(x, (const uint8_t*)w, y, K, N, f);
+        return kind == 3 ? gd_launch<1, GD_NB, true>(x, (const uint8_t*)w, y, K, N, f)
+                         : gd_launch<1, GD_NB, true, true>(x, (const uint8_t*)w, y, K, N, f);
     }
     // the folded step start needs the norm prologue and aligned rows (no launch made otherwise)
     if (f.emb && !emb_ok) return GH_EUNSUPPORTED;

@@ -28,8 +28,11 @@ def _run_linear(gh, x, w, M, K, N, kind):
 
 
 @pytest.mark.parametrize("kind", [2, 3])
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096),
+                                   (1, 512, 2192), (1, 1024, 520), (1, 2048, 4100)])
 def test_gemv_c2_vs_exact(gh, kind, M, K, N):
+    """c2 shapes and the decode shapes of the int8 single-token GEMV (K <= 2048 for Q8_0, with a
+    short last tile at N = 520 / 4100)."""
     w = O.quantize(kind, O.rng_normal(2, N * K, 0, 0.02))
     x = O.rng_normal(8, M * K)
     got = _run_linear(gh, x, w, M, K, N, kind)
