@@ -156,7 +156,7 @@ def kernel_suite(gh):
                         "k_gemv8_q4k" if (kind == 3 and 2 <= M <= 8 and K <= 4096) else "k_gemv_mfma")
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
-                res[tag] = entry("k_dequant_bf16+k_to_bf16+hipBLASLt bf16 GEMM (fp32 out)", ms,
+                res[tag] = entry("k_dequant_fused (weights + x to bf16)+hipBLASLt bf16 GEMM (fp32 out)", ms,
                                  bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K, bound="mfma")
             del dw, dx, y
     # ---------------- c3: SSD scan T=4096 + decode state update
