@@ -264,44 +264,69 @@ __global__ void __launch_bounds__(256) k_perm_count(const int32_t* __restrict__ 
 
 // counts[c][e] -> base[c][e] (first grouped position of expert e's slots in
 // chunk c); offsets = exclusive scan of the totals; tile table for the
-// grouped GEMM (tiles of `bm` rows per expert segment).
+// grouped GEMM (tiles of `bm` rows per expert segment, experts in order). Wave w scans its
+// quarter of the chunks per expert, the earlier quarters' totals are added after; the tile
+// table is written by every thread (tile j belongs to the last expert whose first tile is
+// <= j).
 __global__ void __launch_bounds__(256) k_perm_scan(int32_t* __restrict__ counts, int nchunks, int ne, int S,
                                                    int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
                                                    int bm) {
     __shared__ int cnt[PERM_MAX_CHUNKS * 64];
-    __shared__ int offs[65];
-    const int n = nchunks * ne;
-    for (int i = threadIdx.x; i < n; i += 256) cnt[i] = counts[i];
+    __shared__ int part[4][64];
+    __shared__ int offs[65], tfirst[65];
+    const int n = nchunks * ne, tid = threadIdx.x, wave = tid >> 6, e = tid & 63;
+    for (int i = tid; i < n; i += 256) cnt[i] = counts[i];
     __syncthreads();
-    const int e = threadIdx.x;
+    const int q = (nchunks + 3) / 4, c0 = min(nchunks, wave * q), c1 = min(nchunks, c0 + q);
     int run = 0;
     if (e < ne)
-        for (int c = 0; c < nchunks; ++c) {
+        for (int c = c0; c < c1; ++c) {
             const int v = cnt[c * ne + e];
             cnt[c * ne + e] = run;
             run += v;
         }
-    if (e < 64) {
-        int incl = (e < ne) ? run : 0;
+    part[wave][e] = run;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += part[w][e];
+    if (e < ne && before)
+        for (int c = c0; c < c1; ++c) cnt[c * ne + e] += before;
+    if (wave == 0) {
+        const int tot = e < ne ? part[0][e] + part[1][e] + part[2][e] + part[3][e] : 0;
+        const int nt = bm > 0 ? (tot + bm - 1) / bm : 0;
+        int incl = tot, tincl = nt;
         for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o, 64);
-            if (e >= o) incl += v;
+            const int v = __shfl_up(incl, o, 64), tv = __shfl_up(tincl, o, 64);
+            if (e >= o) {
+                incl += v;
+                tincl += tv;
+            }
         }
-        if (e < ne) offs[e] = incl - run;
-        if (e == 0) offs[ne] = S;
+        if (e < ne) {
+            offs[e] = incl - tot;
+            tfirst[e] = tincl - nt;
+        }
+        if (e == ne - 1) {
+            offs[ne] = S;
+            tfirst[ne] = tincl;
+        }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) counts[i] = cnt[i] + offs[i % ne];
-    for (int i = threadIdx.x; i <= ne; i += 256) offsets[i] = offs[i];
-    if (threadIdx.x == 0 && tiles) {
-        int nt = 0;
-        for (int g = 0; g < ne; ++g)
-            for (int m0 = offs[g]; m0 < offs[g + 1]; m0 += bm) {
-                tiles[1 + 2 * nt] = g;
-                tiles[2 + 2 * nt] = m0;
-                ++nt;
+    for (int i = tid; i < n; i += 256) counts[i] = cnt[i] + offs[i % ne];
+    for (int i = tid; i <= ne; i += 256) offsets[i] = offs[i];
+    if (tiles) {
+        const int ntiles = tfirst[ne];
+        for (int j = tid; j < ntiles; j += 256) {
+            int lo = 0, hi = ne - 1;  // the last g with tfirst[g] <= j
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (tfirst[mid] <= j) lo = mid;
+                else hi = mid - 1;
             }
-        tiles[0] = nt;
+            tiles[1 + 2 * j] = lo;
+            tiles[2 + 2 * j] = offs[lo] + (j - tfirst[lo]) * bm;
+        }
+        if (tid == 0) tiles[0] = ntiles;
     }
 }
 
