@@ -211,6 +211,14 @@ int64_t gh_gguf_find_tensor(const gh_gguf* f, const char* name);
 int gh_gguf_get_u64(const gh_gguf* f, const char* key, uint64_t* out);
 int gh_gguf_get_f32(const gh_gguf* f, const char* key, float* out);
 int gh_gguf_get_str(const gh_gguf* f, const char* key, char* buf, size_t cap);
+/* GGUFReader::model_config (gguf_codec.cpp:1083-1180) for the Granite hybrid: the native
+ * ghassan.* keys to the gh_granite_create_ex arrays (cfg with cfg[15] = qkind, then the L layer
+ * kinds, tie_embeddings, moe_aux_free: *ncfg = 18 + L ints; fcfg: 5 floats). Missing keys take
+ * the ModelConfig defaults; a file that is not a hybrid, or asks for what this backend does not
+ * run (dense FFN, no shared expert, n_groups != 1, qk-norm, qkv / Mamba projection bias, a conv
+ * without bias, positional embeddings, a sliding window), returns GH_EUNSUPPORTED. */
+int gh_gguf_granite_config(const gh_gguf* f, int qkind, int32_t* cfg, int cfg_cap, float* fcfg, int fcfg_cap,
+                           int* ncfg);
 /* read_tensor_quant (gguf_codec.cpp:1450-1501): kind 0 Q4_0, 1 Q4_1, 2 Q8_0, 3 Q4_K. A file
  * tensor of that GGML type is copied verbatim; any other decodable type (F32, F16, Q4_0,
  * Q4_1, Q8_0, Q4_K, Q5_K, Q6_K) is decoded to fp32 and quantised on the host. */
@@ -265,6 +273,10 @@ int gh_granite_reset(gh_granite* g);
  * the model's kind (verbatim when the file holds that kind, including Q4_K),
  * fp16 / fp32 vectors decoded. Shapes must match the model's configuration. */
 int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f);
+/* The reference's load path in one call (gguf_codec.cpp:1083-1180 model_config, then Model
+ * construction and load_model_from_gguf, 1507-1564): open the file, build the model from its
+ * metadata with weights packed as qkind, load every parameter, close the file. */
+int gh_granite_open_gguf(const char* path, int qkind, int max_ctx, gh_granite** out);
 /* Generator::prefill + first logits (inference/generator.cpp:917-983).
  * logits_host may be NULL. mamba_mode: 0 token-by-token state updates
  * (the reference's order), 1 chunked SSD scan. */

@@ -14,6 +14,7 @@
 // uses 32, which is the same for files without the key), tensor offsets
 // relative to the data section.
 #include <fcntl.h>
+#include <math.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -591,6 +592,100 @@ int gh_gguf_write(const char* path, int n_tensors, const char* const* names, con
     }
     ok = (fclose(f) == 0) && ok;
     GH_REQUIRE(ok, "gguf_write: short write to %s", path);
+    return GH_OK;
+}
+
+
+// GGUFReader::model_config (format/gguf_codec.cpp:1083-1180) for the Granite hybrid this backend
+// runs, from the native ghassan.* keys the reference's exporter writes (gguf_codec.cpp:1749-1824):
+// the gh_granite_create_ex arrays. A key the file lacks takes the ModelConfig default
+// (model/model.h), as the reference's get_uint / get_float / get_bool do; features the backend
+// does not implement are refused by name. The shared expert width falls back to the routed width
+// (model.h:126-129); the attention scale 0 means 1 / sqrt(head_dim) (model.h:103).
+int gh_gguf_granite_config(const gh_gguf* g, int qkind, int32_t* cfg, int cfg_cap, float* fcfg, int fcfg_cap,
+                           int* ncfg) {
+    GH_REQUIRE(g && cfg && fcfg && ncfg && fcfg_cap >= 5, "gguf_granite_config: bad arguments");
+    auto has = [&](const char* k) { return g->kv.count(k) != 0; };
+    GH_REQUIRE(has("ghassan.block_count"),
+               "GGUF has no architecture keys (ghassan.block_count / llama.block_count): not a Ghassan model file");
+    auto u = [&](const char* k, uint64_t def) -> int64_t {
+        uint64_t v = def;
+        if (has(k) && gh_gguf_get_u64(g, k, &v) != GH_OK) v = def;
+        return (int64_t)v;
+    };
+    auto f32 = [&](const char* k, float def) -> float {
+        float v = def;
+        if (has(k) && gh_gguf_get_f32(g, k, &v) != GH_OK) v = def;
+        return v;
+    };
+    auto b = [&](const char* k, bool def) -> bool {
+        auto it = g->kv.find(k);
+        if (it == g->kv.end() || it->second.type != KV_BOOL) return def;
+        return g->map[it->second.off] != 0;
+    };
+    const bool hybrid = b("ghassan.hybrid", b("ghassan.granite", false));
+    if (!hybrid) return fail(GH_EUNSUPPORTED, "gguf_granite_config: not a Granite hybrid file (ghassan.hybrid)");
+    // defaults of ModelConfig (model/model.h:14-48, 100-113) for keys the file lacks
+    const int64_t V = u("ghassan.vocab_size", 16000), d = u("ghassan.embedding_length", 768),
+                  L = u("ghassan.block_count", 26);
+    const int64_t H = u("ghassan.attention.head_count", 12), KV = u("ghassan.attention.head_count_kv", 4);
+    GH_REQUIRE(V > 0 && d > 0 && L > 0 && L <= 1024 && H > 0 && KV > 0, "gguf_granite_config: bad model dimensions");
+    GH_REQUIRE(cfg_cap >= 18 + L, "gguf_granite_config: %lld layers need %lld ints", (long long)L,
+               (long long)(18 + L));
+    const int64_t hd_o = u("ghassan.attention.head_dim", 0), hd = hd_o > 0 ? hd_o : d / H;
+    // the parts of ModelConfig this backend does not implement
+    const struct {
+        bool bad;
+        const char* what;
+    } refuse[] = {
+        {!b("ghassan.use_moe", false), "a dense FFN (ghassan.use_moe false)"},
+        {!b("ghassan.moe.shared_expert", true), "MoE without the shared expert"},
+        {u("ghassan.mamba.n_groups", 1) != 1, "mamba.n_groups != 1"},
+        {b("ghassan.use_qk_norm", false), "use_qk_norm"},
+        {b("ghassan.use_qkv_bias", false), "use_qkv_bias"},
+        {b("ghassan.mamba.proj_bias", false), "mamba.proj_bias"},
+        {!b("ghassan.mamba.conv_bias", true), "a Mamba conv without bias"},
+        {u("ghassan.position_embedding", 0) != 1, "positional embeddings (the Granite hybrid is NoPE: position_embedding 1)"},
+        {u("ghassan.sliding_window", 0) != 0, "a sliding window"},
+    };
+    for (const auto& r : refuse)
+        if (r.bad) return fail(GH_EUNSUPPORTED, "gguf_granite_config: %s is not supported", r.what);
+    // model.cpp:407-420 requires one kind per layer for the hybrid: the list is mandatory here
+    GH_REQUIRE(has("ghassan.layer_types"), "GGUF has no ghassan.layer_types: a Granite hybrid needs one kind per layer");
+    std::vector<int32_t> lt;
+    {
+        char buf[8192];
+        const int rc = gh_gguf_get_str(g, "ghassan.layer_types", buf, sizeof buf);
+        if (rc != GH_OK) return rc;
+        // comma separated "0" (mamba) / "1" (attention); each item is read by its first character
+        for (const char* p = buf; *p;) {
+            GH_REQUIRE(*p == '0' || *p == '1', "GGUF ghassan.layer_types: expected '0' or '1', got '%c'", *p);
+            lt.push_back(*p == '1');
+            const char* comma = strchr(p, ',');
+            if (!comma) break;
+            p = comma + 1;
+        }
+        GH_REQUIRE(lt.size() == (size_t)L, "GGUF ghassan.layer_types: length does not match num_layers");
+    }
+    const int64_t ffe = u("ghassan.moe.expert_feed_forward_length", 768), sh = u("ghassan.moe.shared_intermediate_size", 0);
+    const int32_t v[16] = {(int32_t)V, (int32_t)d, (int32_t)L, (int32_t)H, (int32_t)KV, (int32_t)hd,
+                           (int32_t)ffe,
+                           (int32_t)u("ghassan.moe.expert_count", 8), (int32_t)u("ghassan.moe.experts_used_count", 2),
+                           (int32_t)(sh > 0 ? sh : ffe),
+                           (int32_t)(u("ghassan.mamba.expand", 2) * d), (int32_t)u("ghassan.mamba.n_heads", 48),
+                           (int32_t)u("ghassan.mamba.d_head", 64), (int32_t)u("ghassan.mamba.d_state", 128),
+                           (int32_t)u("ghassan.mamba.d_conv", 4), (int32_t)qkind};
+    memcpy(cfg, v, sizeof v);
+    for (int64_t l = 0; l < L; ++l) cfg[16 + l] = lt[(size_t)l];
+    cfg[16 + L] = b("ghassan.tie_word_embeddings", true) ? 1 : 0;
+    cfg[17 + L] = b("ghassan.moe.aux_free", false) ? 1 : 0;
+    const float am = f32("ghassan.attention_multiplier", 0.0f);  // 0: 1 / sqrt(head_dim)
+    fcfg[0] = f32("ghassan.attention.layer_norm_rms_epsilon", 1e-5f);
+    fcfg[1] = am != 0.0f ? am : 1.0f / sqrtf((float)hd);
+    fcfg[2] = f32("ghassan.embedding_multiplier", 1.0f);
+    fcfg[3] = f32("ghassan.residual_multiplier", 1.0f);
+    fcfg[4] = f32("ghassan.logits_scaling", 1.0f);
+    *ncfg = (int)(18 + L);
     return GH_OK;
 }
 

@@ -744,6 +744,28 @@ int gh_granite_load_gguf(gh_granite* g, const gh_gguf* f) {
     return GH_OK;
 }
 
+int gh_granite_open_gguf(const char* path, int qkind, int max_ctx, gh_granite** out) {
+    GH_REQUIRE(path && out, "granite_open_gguf: null argument");
+    *out = nullptr;
+    gh_gguf* f = nullptr;
+    int rc = gh_gguf_open(path, &f);
+    if (rc != GH_OK) return rc;
+    int32_t cfg[18 + 1024];
+    float fcfg[5];
+    int ncfg = 0;
+    gh_granite* g = nullptr;
+    rc = gh_gguf_granite_config(f, qkind, cfg, (int)(sizeof cfg / sizeof cfg[0]), fcfg, 5, &ncfg);
+    if (rc == GH_OK) rc = gh_granite_create_ex(cfg, ncfg, fcfg, 5, max_ctx, &g);
+    if (rc == GH_OK) rc = gh_granite_load_gguf(g, f);
+    gh_gguf_close(f);
+    if (rc != GH_OK) {
+        if (g) gh_granite_destroy(g);  // keeps the first failure's message: destroy does not fail here
+        return rc;
+    }
+    *out = g;
+    return GH_OK;
+}
+
 int gh_granite_get_param(gh_granite* g, const char* name, void* host, size_t nbytes) {
     GH_REQUIRE(g && name && host, "granite_get_param: null argument");
     auto it = g->by_name.find(name);

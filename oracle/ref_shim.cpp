@@ -340,4 +340,105 @@ long ref_gguf_read_f32(const char* path, const char* name, float* out, long cap)
     std::memcpy(out, t.data_ptr(), sizeof(float) * (size_t)t.numel());
     return (long)t.numel();
 }
+// The model of ref_granite_generate_ex written by the reference's own exporter
+// (format/gguf_codec.cpp:1672 export_model_gguf: native ghassan.* keys, the "q8_k" profile with
+// the hybrid precision policy), with an empty tokenizer.
+int ref_granite_export_gguf(const i32* cfg, int ncfg, const float* fcfg, int nfcfg, const char** names,
+                            const void** ptrs, int nparams, int max_ctx, const char* path) {
+    try {
+        ModelConfig c;
+        c.arch = ModelConfig::ArchGranite;
+        c.vocab_size = cfg[0]; c.hidden_size = cfg[1]; c.num_layers = cfg[2]; c.num_heads = cfg[3];
+        c.num_kv_heads = cfg[4]; c.head_dim_override = cfg[5]; c.moe_expert_dim = cfg[6]; c.num_experts = cfg[7];
+        c.moe_top_k = cfg[8]; c.shared_expert_intermediate_size = cfg[9]; c.use_moe = true; c.moe_shared = true;
+        c.mamba_expand = cfg[10] / cfg[1]; c.mamba_n_heads = cfg[11]; c.mamba_d_head = cfg[12];
+        c.mamba_d_state = cfg[13]; c.mamba_n_groups = 1; c.mamba_d_conv = cfg[14];
+        c.layer_types.assign(cfg + 16, cfg + 16 + cfg[2]); c.position_embedding = 1; c.rms_eps = fcfg[0];
+        c.attention_multiplier = fcfg[1]; c.intermediate_size = cfg[6]; c.max_seq_len = max_ctx;
+        c.tie_embeddings = true;
+        granite_options(c, cfg, ncfg, fcfg, nfcfg);
+        Model m(c, Device::CPU, false, cfg[15]);
+        std::map<std::string, const void*> pm;
+        for (int i = 0; i < nparams; ++i) pm[names[i]] = ptrs[i];
+        for (Parameter* p : m.parameters()) {
+            auto it = pm.find(p->name);
+            if (it == pm.end()) return -3;
+            std::memcpy(p->w.data_ptr(), it->second, p->w.nbytes());
+        }
+        if (c.moe_aux_free) {
+            for (int l = 0; l < c.num_layers; ++l) {
+                auto it = pm.find("layers." + std::to_string(l) + ".moe_bias");
+                if (it != pm.end()) m.set_moe_bias(l, (const float*)it->second, (size_t)c.num_experts);
+            }
+        }
+        ExportProfileGGUF prof = gguf_profile_for("q8_k");
+        prof.hybrid = true;
+        Tokenizer tok;
+        export_model_gguf(path, m, tok, prof, {}, "native");
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_granite_export_gguf: %s\n", e.what());
+        return -2;
+    }
+    return 0;
+}
+
+// A model file as the reference loads it -- GGUFReader::model_config(), then
+// load_model_from_gguf with storage kind qkind (format/gguf_codec.cpp:1083-1180, 1507-1563) --
+// and its greedy run (the loop of ref_granite_generate_ex). cfg_out (16 + L + 2 ints) and
+// fcfg_out (5 floats) receive the parsed configuration in the layout of
+// orc_granite_generate_ex.
+int ref_granite_generate_gguf(const char* path, int qkind, const i32* prompt, int P, int n_new, int max_ctx,
+                              i32* out_ids, float* out_margins, i32* cfg_out, int cfg_cap, float* fcfg_out) {
+    try {
+        GGUFReader r;
+        if (!r.open(path)) return -4;
+        const ModelConfig c = r.model_config();
+        if (cfg_out) {
+            if (cfg_cap < 18 + c.num_layers) return -5;
+            const i32 v[16] = {c.vocab_size, c.hidden_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim(),
+                               c.moe_expert_dim, c.num_experts, c.moe_top_k, c.shared_expert_intermediate_size,
+                               c.mamba_expand * c.hidden_size, c.mamba_n_heads, c.mamba_d_head, c.mamba_d_state,
+                               c.mamba_d_conv, qkind};
+            std::memcpy(cfg_out, v, sizeof v);
+            for (int l = 0; l < c.num_layers; ++l) cfg_out[16 + l] = c.layer_types[l];
+            cfg_out[16 + c.num_layers] = c.tie_embeddings ? 1 : 0;
+            cfg_out[17 + c.num_layers] = c.moe_aux_free ? 1 : 0;
+        }
+        if (fcfg_out) {
+            fcfg_out[0] = c.rms_eps;
+            fcfg_out[1] = c.attention_multiplier;
+            fcfg_out[2] = c.embedding_multiplier;
+            fcfg_out[3] = c.residual_multiplier;
+            fcfg_out[4] = c.logits_scaling;
+        }
+        Model m(c, Device::CPU, false, qkind);
+        if (!load_model_from_gguf(path, m, qkind)) return -6;
+        ops::set_fused_q4(true);
+        Tokenizer tok;
+        Generator g(m, tok, max_ctx);
+        std::vector<i32> pr(prompt, prompt + P);
+        g.prefill(pr);
+        const int V = c.vocab_size;
+        for (int step = 0; step < n_new; ++step) {
+            const float* lg = g.logits_host_.data();
+            const i32 next = ops::argmax_token(Device::CPU, lg, V);
+            float best = -std::numeric_limits<float>::infinity(), second = best;
+            for (int i = 0; i < V; ++i) {
+                if (!std::isfinite(lg[i])) continue;
+                if (lg[i] > best) { second = best; best = lg[i]; }
+                else if (lg[i] > second) second = lg[i];
+            }
+            out_ids[step] = next;
+            out_margins[step] = best - second;
+            if (step == n_new - 1) break;
+            g.push_history(next);
+            g.decode_step(next, (int)g.absolute_pos_);
+            ++g.absolute_pos_;
+        }
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_granite_generate_gguf: %s\n", e.what());
+        return -2;
+    }
+    return 0;
+}
 }  // extern "C"

@@ -9,6 +9,20 @@ import oracle_lib as O
 # (tests/golden/granite_c1_q8_opts.npz is the compiled reference Generator on it, Q8_0).
 C1_OPTS = dict(O.C1, tied=0, aux_free=1, emb_mult=12.0, res_mult=0.22, logits_scaling=8.0)
 
+# A small Granite hybrid with every optional field set, written to GGUF by the reference's own
+# exporter (tests/golden/granite_small.gguf): the loader builds the model from its metadata.
+G_SMALL = dict(V=256, d=256, L=2, H=4, KV=2, hd=64, E=128, ne=4, K=2, SH=128, d_inner=512, m_heads=8, m_dhead=64,
+               m_dstate=64, conv_k=4, layer_types=[0, 1], eps=1e-5, scale=0.125, tied=0, aux_free=1, emb_mult=4.0,
+               res_mult=0.5, logits_scaling=2.0)
+
+
+def g_small_weights(qkind=2):
+    """Synthetic weights of G_SMALL (the shared recipe, seed 3) with router biases N(0, 0.05)."""
+    w = O.granite_weights(G_SMALL, qkind, seed=3)
+    for layer in range(G_SMALL["L"]):
+        w[f"layers.{layer}.moe_bias"] = O.rng_normal(95 + layer, G_SMALL["ne"], 0, 0.05)
+    return w
+
 
 def granite_opts_weights(qkind=2):
     """Synthetic weights of C1_OPTS (the shared recipe) with router biases N(0, 0.05)

@@ -375,3 +375,74 @@ def test_k_quant_read_as_model_kind(lib, tmp_path):
         assert np.array_equal(out, O.f32_to_f16(vals))
     finally:
         lib.gh_gguf_close(h)
+
+
+def granite_config(lib, path, qkind=2):
+    f = open_file(lib, path)
+    try:
+        cfg = np.zeros(18 + 1024, np.int32)
+        fcfg = np.zeros(5, np.float32)
+        n = C.c_int()
+        check(lib, lib.gh_gguf_granite_config(f, qkind, cfg.ctypes.data_as(C.c_void_p), len(cfg),
+                                              fcfg.ctypes.data_as(C.c_void_p), len(fcfg), C.byref(n)))
+        return cfg[: n.value], fcfg
+    finally:
+        lib.gh_gguf_close(f)
+
+
+def test_granite_config_from_reference_file(lib):
+    """The model configuration read from the exporter's ghassan.* keys of a file the compiled
+    reference wrote (export_model_gguf, hybrid profile) equals the configuration the reference's
+    GGUFReader::model_config returned for the same file (tests/golden/granite_small_gguf.npz)."""
+    g = golden("granite_small_gguf")
+    path = os.path.join(GOLDEN, "granite_small.gguf")
+    import hashlib
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(g["file_sha256"])
+    for qkind in (2, 3):
+        cfg, fcfg = granite_config(lib, path, qkind)
+        want = g["cfg"].copy()
+        want[15] = qkind
+        assert np.array_equal(cfg, want), (cfg, want)
+        assert np.array_equal(fcfg.view(np.uint32), g["fcfg"].view(np.uint32))
+
+
+HYBRID_META = [("ghassan.block_count", 4, 2), ("ghassan.hybrid", 7, 1), ("ghassan.use_moe", 7, 1),
+               ("ghassan.layer_types", 8, "0,1"), ("ghassan.position_embedding", 4, 1)]
+
+
+def test_granite_config_defaults(lib, tmp_path):
+    """Keys the file lacks take the ModelConfig defaults (model/model.h): dims, experts, Mamba
+    sizes, multipliers 1, attention scale 1/sqrt(head_dim), shared width = routed width, tied."""
+    p = str(tmp_path / "m.gguf")
+    write(lib, p, [], HYBRID_META + [("ghassan.moe.expert_feed_forward_length", 4, 512)])
+    cfg, fcfg = granite_config(lib, p, 3)
+    assert list(cfg) == [16000, 768, 2, 12, 4, 64, 512, 8, 2, 512, 1536, 48, 64, 128, 4, 3, 0, 1, 1, 0]
+    assert list(fcfg) == [np.float32(1e-5), np.float32(1 / 8), 1, 1, 1]
+
+
+@pytest.mark.parametrize("meta,err", [
+    ([("ghassan.hybrid", 7, 0)], "not a Granite hybrid"),
+    ([("ghassan.use_moe", 7, 0)], "dense FFN"),
+    ([("ghassan.moe.shared_expert", 7, 0)], "shared expert"),
+    ([("ghassan.mamba.n_groups", 4, 2)], "n_groups"),
+    ([("ghassan.use_qk_norm", 7, 1)], "use_qk_norm"),
+    ([("ghassan.mamba.proj_bias", 7, 1)], "proj_bias"),
+    ([("ghassan.position_embedding", 4, 0)], "NoPE"),
+    ([("ghassan.sliding_window", 4, 128)], "sliding window"),
+    ([("ghassan.layer_types", 8, "0,1,1")], "length does not match"),
+    ([("ghassan.layer_types", 8, "0,2")], "expected '0' or '1'"),
+    ([("ghassan.block_count", 4, 3)], "length does not match"),
+])
+def test_granite_config_rejects(lib, tmp_path, meta, err):
+    p = str(tmp_path / "m.gguf")
+    keys = {k for k, _, _ in meta}
+    write(lib, p, [], [m for m in HYBRID_META if m[0] not in keys] + meta)
+    with pytest.raises(RuntimeError, match=err):
+        granite_config(lib, p)
+
+
+def test_granite_config_needs_architecture_keys(lib, tmp_path):
+    p = str(tmp_path / "m.gguf")
+    write(lib, p, [], [("general.architecture", 8, "ghassan")])
+    with pytest.raises(RuntimeError, match="no architecture keys"):
+        granite_config(lib, p)

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from conftest import golden
 from test_gguf import GT, check, open_file, write
 from test_gpu_granite import Granite
 
@@ -82,3 +83,27 @@ def test_load_gguf_shape_mismatch(gh, tmp_path):
     finally:
         m.close()
         lib.gh_gguf_close(f)
+
+
+@pytest.mark.parametrize("use_graph", [0, 1])
+def test_open_reference_gguf_generates_reference_ids(gh, use_graph):
+    """A file the compiled reference exported (export_model_gguf, hybrid profile: Q8_0 matrices,
+    F16 in_proj, F32 vectors, untied lm_head, router biases, Granite multipliers), opened with
+    gh_granite_open_gguf alone (configuration from its metadata, then every weight): the greedy
+    ids equal those the reference generated after its own load_model_from_gguf of the same
+    file, up to the first near-tie of the reference's top-2 margin."""
+    import os
+    from conftest import GOLDEN
+    from test_gpu_granite import compare
+    g = golden("granite_small_gguf")
+    from cases import G_SMALL
+    h = C.c_void_p()
+    gh.call("gh_granite_open_gguf", os.path.join(GOLDEN, "granite_small.gguf").encode(), 2, int(g["max_ctx"]),
+            C.byref(h))
+    m = Granite.__new__(Granite)
+    m.gh, m.c, m.h = gh, dict(G_SMALL), h
+    try:
+        ids, _ = m.generate(g["prompt"], len(g["ids"]), 1, use_graph)
+        assert compare(ids, g["ids"], g["margins"]) == len(g["ids"])
+    finally:
+        m.close()
