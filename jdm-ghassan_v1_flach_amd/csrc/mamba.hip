@@ -60,14 +60,19 @@ __global__ void k_conv1d(const float* __restrict__ proj, int proj_ld, int col0, 
     }
 }
 
-// dt = softplus(dt_raw + dt_bias), A = -exp(A_log), and the chunk-local
-// inclusive cumulative sums of A*dt of (chunk c, head h), by one wave; also into
-// the LDS arrays ldt / lcum ([L]) of the calling block.
+// The per-position decay data of (chunk c, head h), by one wave: dt = softplus(dt_raw +
+// dt_bias), A = -exp(A_log), cum = the chunk-local inclusive sums of A dt. Into the LDS arrays
+// ldt / lcum ([L]) of the calling block, and for the chunk-output blocks as four contiguous
+// arrays of 256 (log2 units, zeros past the sequence end) that they load whole: W[0] cum,
+// W[1] dt, W[2] the factored intra-chunk weight e^(r_s - cum_tau) dt_tau (r_s = cum at the first
+// position of tau's 16-step); F[s] = 1 when every position of 16-step s keeps
+// r_s - cum_tau < 100 (log2), i.e. the factored form cannot overflow (one writer per step).
 __device__ __forceinline__ void ssd_prep_wave(const float* __restrict__ dt_in, int dt_ld,
                                               const float* __restrict__ dt_bias, const float* __restrict__ A_in,
-                                              const float* __restrict__ a_log, float* __restrict__ dt_out,
-                                              float* __restrict__ cum, int T, int H, int L, int c, int h, int lane,
-                                              float* ldt, float* lcum) {
+                                              const float* __restrict__ a_log, float* __restrict__ W,
+                                              int* __restrict__ F, int T, int L, int c, int h, int lane, float* ldt,
+                                              float* lcum) {
+    constexpr float LOG2E = 1.4426950408889634f;
     const int t0 = c * L, len = min(L, T - t0);
     const float A = A_in ? A_in[h] : -expf(a_log[h]);
     // the raw dt of all positions (up to 4 per lane) are requested before the first scan step
@@ -80,11 +85,10 @@ __device__ __forceinline__ void ssd_prep_wave(const float* __restrict__ dt_in, i
     float carry = 0.f;  // L <= 256 (ssd_run checks it): at most 4 steps
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int base = 64 * j;
-        if (base >= len) break;
-        const int i = base + lane;
+        const int i = 64 * j + lane;
+        const bool v = i < len;
         float dt = 0.f, a = 0.f;
-        if (i < len) {
+        if (v) {
             const float raw = raws[j];
             dt = dt_bias ? softplus_ref(raw + dt_bias[h]) : raw;
             a = A * dt;
@@ -92,15 +96,21 @@ __device__ __forceinline__ void ssd_prep_wave(const float* __restrict__ dt_in, i
         float inc = a;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const float v = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += v;
+            const float u = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += u;
         }
-        if (i < len) {
-            dt_out[(size_t)(t0 + i) * H + h] = dt;
-            cum[(size_t)(t0 + i) * H + h] = carry + inc;
+        const float cm = carry + inc;
+        if (v) {
             ldt[i] = dt;
-            lcum[i] = carry + inc;
+            lcum[i] = cm;
         }
+        const float cv = v ? cm * LOG2E : 0.f;
+        const float rs = __shfl(cv, lane & ~15, 64);  // cum at the step's first position (0 past the end)
+        W[i] = cv;
+        W[256 + i] = v ? dt : 0.f;
+        W[512 + i] = v ? __builtin_amdgcn_exp2f(rs - cv) * dt : 0.f;
+        const uint64_t bad = __ballot(v && !((rs - cv) < 100.0f));
+        if ((lane & 15) == 0) F[4 * j + (lane >> 4)] = ((bad >> (lane & 48)) & 0xFFFFull) == 0;
         carry += __shfl(inc, 63, 64);
     }
 }
@@ -255,8 +265,8 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
                                                       const float* __restrict__ Bm, const float* __restrict__ Cm,
                                                       int ldb, const float* __restrict__ dt_in, int dt_ld,
                                                       const float* __restrict__ dt_bias, const float* __restrict__ A_in,
-                                                      const float* __restrict__ a_log, float* __restrict__ dt,
-                                                      float* __restrict__ cum, _Float16* __restrict__ G,
+                                                      const float* __restrict__ a_log, float* __restrict__ W,
+                                                      int* __restrict__ F, _Float16* __restrict__ G,
                                                       _Float16* __restrict__ C16, float* __restrict__ dS,
                                                       float* __restrict__ decay, int T, int H, int L,
                                                       float* __restrict__ state, _Float16* __restrict__ Sin16) {
@@ -283,7 +293,9 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
     const int c = blockIdx.x % nch, h = blockIdx.x / nch;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t0 = c * L, len = min(L, T - t0);
-    if (wave == 0) ssd_prep_wave(dt_in, dt_ld, dt_bias, A_in, a_log, dt, cum, T, H, L, c, h, lane, ldt, lcum);
+    if (wave == 0)
+        ssd_prep_wave(dt_in, dt_ld, dt_bias, A_in, a_log, W + ((size_t)c * H + h) * 768, F + ((size_t)c * H + h) * 16,
+                      T, L, c, h, lane, ldt, lcum);
     constexpr int NT = (P / 32) * (N / 32);  // output tiles
     constexpr int TPW = NT / 4;              // tiles per wave
     f32x16 acc[TPW];
@@ -407,15 +419,18 @@ __global__ void __launch_bounds__(256) k_ssd_state_pass(float* __restrict__ stat
 template <int N>
 __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, int ldx,
                                                  const _Float16* __restrict__ C16, const _Float16* __restrict__ G,
-                                                 const float* __restrict__ dt, const float* __restrict__ cum,
+                                                 const float* __restrict__ W, const int* __restrict__ F,
                                                  const _Float16* __restrict__ Sin16, const float* __restrict__ D,
                                                  float* __restrict__ y, int ldy, int T, int H, int L) {
     constexpr int P = 64, PH = 32, PN = P * N, SX = 256 + 8, SS = N + 8, SD = PH + 4;
     __shared__ __attribute__((aligned(16))) _Float16 sXt[PH * SX];
     __shared__ __attribute__((aligned(16))) _Float16 sS[PH * SS];
     __shared__ __attribute__((aligned(16))) float sDx[256 * SD];
-    __shared__ float scum[256], sdt[256], sw[256];
+    __shared__ __attribute__((aligned(16))) float sWt[768];
     __shared__ int sfast[16];
+    float* scum = sWt;  // cum (log2 units), dt, factored intra-chunk weight: 256 each
+    float* sdt = sWt + 256;
+    float* sw = sWt + 512;
     const int nch = (T + L - 1) / L, nitems = nch * H;
     // block b -> item (chunk, head) and p half. The dispatcher places block b on XCD b % 8. With
     // nch a multiple of 8, XCD x takes the chunks x, x + 8, ... of every head (its L2 then
@@ -440,7 +455,6 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
     const int pc0 = PH * ph;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = c * L, len = min(L, T - t0);
-    constexpr float LOG2E = 1.4426950408889634f;
     const int rb = wave, kh = 8 * (lane >> 5), col = lane & 31;
     const bool active = 32 * rb < len;  // wave-uniform
     const int t = 32 * rb + col;        // this lane's A row (chunk-local)
@@ -474,21 +488,13 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
         uint2 sv[SJ];
 #pragma unroll
         for (int j = 0; j < SJ; ++j) sv[j] = src[tid + 512 * j];
-        if (tid < L) {
-            // e^(cum_t - cum_tau) = e^(cum_t - r_s) e^(r_s - cum_tau) with r_s = cum at the first
-            // position of tau's 16-step: the second factor (times dt_tau) is sw[tau], the first is
-            // one exponential per (row, step). A step whose decay spread makes e^(r_s - cum_tau)
-            // too large for fp32 marks its row blocks for the element-by-element form.
-            const int s0 = tid & ~15, s15 = s0 + 15;
-            const float cv = tid < len ? cum[(size_t)(t0 + tid) * H + h] * LOG2E : 0.f;
-            const float rs = s0 < len ? cum[(size_t)(t0 + s0) * H + h] * LOG2E : 0.f;
-            const float d = tid < len ? dt[(size_t)(t0 + tid) * H + h] : 0.f;
-            scum[tid] = cv;
-            sdt[tid] = d;
-            sw[tid] = tid < len ? __builtin_amdgcn_exp2f(rs - cv) * d : 0.f;
-            if (tid == min(s15, len - 1)) sfast[tid >> 4] = (rs - cv) < 100.0f;
-            if (tid == s15 && s15 >= len) sfast[tid >> 4] = 1;
-        }
+        // e^(cum_t - cum_tau) = e^(cum_t - r_s) e^(r_s - cum_tau) with r_s = cum at the first
+        // position of tau's 16-step: the second factor (times dt_tau) is sw[tau], the first is
+        // one exponential per (row, step); a step whose decay spread makes e^(r_s - cum_tau) too
+        // large for fp32 is marked in sfast and takes the element-by-element form. All of it
+        // comes precomputed from the chunk-state launch, as contiguous arrays.
+        if (tid < 384) ((float2*)sWt)[tid] = ((const float2*)(W + ((size_t)c * H + h) * 768))[tid];
+        if (tid < 16) sfast[tid] = F[((size_t)c * H + h) * 16 + tid];
 #pragma unroll
         for (int j = 0; j < SJ; ++j) {
             const int e = 4 * (tid + 512 * j), p = e / N, n = e % N;
@@ -599,16 +605,17 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     GH_REQUIRE(ldx % 4 == 0 && ldbc % 4 == 0, "ssd scan: row strides must be multiples of 4");
     const int nch = cdiv(T, L);
     const size_t PN = (size_t)P * N;
-    // workspace: dt, cum [T][H] fp32; dS [nch][H][P][N] fp32; decay [nch][H] fp32;
-    // Sin [nch][H][P][N], G [nch][L][L] and C16 [nch][L][N] fp16 (G, C16 in fragment order)
-    const size_t f_dt = (size_t)T * H, f_S = (size_t)nch * H * PN;
+    // workspace: decay data W [nch][H][3][256] fp32 + fast flags F [nch][H][16]; dS
+    // [nch][H][P][N] fp32; decay [nch][H] fp32; Sin [nch][H][P][N], G [nch][L][L] and C16
+    // [nch][L][N] fp16 (G, C16 in fragment order)
+    const size_t f_W = (size_t)nch * H * 768, f_F = (size_t)nch * H * 16, f_S = (size_t)nch * H * PN;
     const size_t f_dec = ((size_t)nch * H + 63) / 64 * 64;
     const size_t h_G = (size_t)nch * L * L, h_C = (size_t)nch * L * N;
-    float* ws = (float*)workspace(WS_MAMBA_CHUNK, (2 * f_dt + f_S + f_dec) * 4 + (f_S + h_G + h_C) * 2 + 256);
+    float* ws = (float*)workspace(WS_MAMBA_CHUNK, (f_W + f_F + f_S + f_dec) * 4 + (f_S + h_G + h_C) * 2 + 256);
     if (!ws) return fail(GH_ENOMEM, "ssd scan: workspace");
-    float* dt = ws;
-    float* cum = dt + f_dt;
-    float* dS = cum + f_dt;
+    float* W = ws;
+    int* F = (int*)(W + f_W);
+    float* dS = (float*)(F + f_F);
     float* decay = dS + f_S;
     _Float16* Sin16 = (_Float16*)(decay + f_dec);
     _Float16* G = Sin16 + f_S;
@@ -618,19 +625,19 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
     const bool one = nch == 1;  // a single chunk: the state pass runs in the chunk-state blocks
     if (N == 128) {
         hipLaunchKernelGGL(k_ssd_state_cb<128>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
+                           dt_bias, A, a_log, W, F, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
         if (!one)
             hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
                                (int)PN);
-        hipLaunchKernelGGL(k_ssd_out<128>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
+        hipLaunchKernelGGL(k_ssd_out<128>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, W, F,
                            Sin16, D, y, ldy, T, H, L);
     } else {
         hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
-                           dt_bias, A, a_log, dt, cum, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
+                           dt_bias, A, a_log, W, F, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
         if (!one)
             hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
                                (int)PN);
-        hipLaunchKernelGGL(k_ssd_out<64>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, dt, cum,
+        hipLaunchKernelGGL(k_ssd_out<64>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, W, F,
                            Sin16, D, y, ldy, T, H, L);
     }
     GH_LAUNCHED("k_ssd_*");
