@@ -850,169 +850,177 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
     const int nqt = cdiv(T, PF_BQ);
-    const int qt = nqt - 1 - (int)blockIdx.x;  // heavy (late) tiles first
-    const int h = blockIdx.y, b = blockIdx.z;
-    const int G = H / KV, kvh = h / G;
-    const int q0 = qt * PF_BQ + wave * 32;
-    const size_t qs = (size_t)T * H * HD;
-    const float* qb = q + b * qs;
-    const _Float16* kbase = K16 + ((size_t)b * KV + kvh) * Tp * HD;
-    const _Float16* vbase = Vt16 + ((size_t)b * KV + kvh) * HD * Tp;
+    // block bx takes q-tile nqt - 1 - bx (late, heavy) and then q-tile bx (early, light): every
+    // block does the same causal work, in one round of the grid
+    for (int pass = 0; pass < 2; ++pass) {
+        const int qt = pass == 0 ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
+        if (pass == 1) {
+            if (qt >= nqt - 1 - (int)blockIdx.x) break;
+            __syncthreads();  // every wave is done with the first tile's LDS buffers
+        }
+        const int h = blockIdx.y, b = blockIdx.z;
+        const int G = H / KV, kvh = h / G;
+        const int q0 = qt * PF_BQ + wave * 32;
+        const size_t qs = (size_t)T * H * HD;
+        const float* qb = q + b * qs;
+        const _Float16* kbase = K16 + ((size_t)b * KV + kvh) * Tp * HD;
+        const _Float16* vbase = Vt16 + ((size_t)b * KV + kvh) * HD * Tp;
 
-    const int kend = min(T, qt * PF_BQ + PF_BQ);
-    int kbeg = 0;
-    if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
-    // per-thread piece coordinates (fixed): K row kr, dims kc; V^T dim vc, keys vr
-    int kr[KPT], kc[KPT], vc[KPT], vr[KPT];
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-        const int e = tid + 256 * i;
-        kr[i] = e / (HD / 8); kc[i] = (e % (HD / 8)) * 8;
-        vc[i] = e / (PF_BK / 8); vr[i] = (e % (PF_BK / 8)) * 8;
-    }
-    gh_u32x4 pk[KPT], pv[KPT];  // (ext-vector: an array of uint4 structs stays in scratch)
-    if (kbeg < kend) {
-#pragma unroll
+        const int kend = min(T, qt * PF_BQ + PF_BQ);
+        int kbeg = 0;
+        if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
+        // per-thread piece coordinates (fixed): K row kr, dims kc; V^T dim vc, keys vr
+        int kr[KPT], kc[KPT], vc[KPT], vr[KPT];
+    #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kbeg + kr[i]) * HD + kc[i]);
-            pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kbeg + vr[i]);
+            const int e = tid + 256 * i;
+            kr[i] = e / (HD / 8); kc[i] = (e % (HD / 8)) * 8;
+            vc[i] = e / (PF_BK / 8); vr[i] = (e % (PF_BK / 8)) * 8;
         }
-    }
-
-    const int qj = q0 + (lane & 31), hf = lane >> 5;
-    f16x8 qreg[HD / 16];
-#pragma unroll
-    for (int s = 0; s < HD / 16; ++s) {
-        if (qj < T) {
-            const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
-            // q pre-multiplied by scale * log2(e): the scores come out of the MFMA in log2 units
-            const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
-            const float c = scale * 1.4426950408889634f;
-            qreg[s][0] = (_Float16)(a0.x * c); qreg[s][1] = (_Float16)(a0.y * c); qreg[s][2] = (_Float16)(a0.z * c);
-            qreg[s][3] = (_Float16)(a0.w * c); qreg[s][4] = (_Float16)(a1.x * c); qreg[s][5] = (_Float16)(a1.y * c);
-            qreg[s][6] = (_Float16)(a1.z * c); qreg[s][7] = (_Float16)(a1.w * c);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
-        }
-    }
-    f32x16 oacc[HD / 32];
-#pragma unroll
-    for (int c = 0; c < HD / 32; ++c)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
-
-    int buf = 0;
-    for (int k0 = kbeg; k0 < kend; k0 += PF_BK, buf ^= 1) {
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            *(gh_u32x4*)(sK[buf] + kr[i] * KS + kc[i]) = pk[i];
-            *(gh_u32x4*)(sVt[buf] + vc[i] * VS + vr[i]) = pv[i];
-        }
-        __syncthreads();
-        if (k0 + PF_BK < kend) {
-            const int kn = k0 + PF_BK;
-#pragma unroll
+        gh_u32x4 pk[KPT], pv[KPT];  // (ext-vector: an array of uint4 structs stays in scratch)
+        if (kbeg < kend) {
+    #pragma unroll
             for (int i = 0; i < KPT; ++i) {
-                pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kn + kr[i]) * HD + kc[i]);
-                pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kn + vr[i]);
+                pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kbeg + kr[i]) * HD + kc[i]);
+                pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kbeg + vr[i]);
             }
         }
-        if (k0 > q0 + 31) continue;  // whole tile in this wave's future (uniform per wave)
-        const _Float16* cK = sK[buf];
-        const _Float16* cV = sVt[buf];
-        f32x16 st[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
-#pragma unroll
-            for (int s = 0; s < HD / 16; ++s) {
-                const f16x8 ka = *(const f16x8*)(cK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
-                st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[s], st[t], 0, 0, 0);
+
+        const int qj = q0 + (lane & 31), hf = lane >> 5;
+        f16x8 qreg[HD / 16];
+    #pragma unroll
+        for (int s = 0; s < HD / 16; ++s) {
+            if (qj < T) {
+                const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
+                // q pre-multiplied by scale * log2(e): the scores come out of the MFMA in log2 units
+                const float4 a0 = *(const float4*)src, a1 = *(const float4*)(src + 4);
+                const float c = scale * 1.4426950408889634f;
+                qreg[s][0] = (_Float16)(a0.x * c); qreg[s][1] = (_Float16)(a0.y * c); qreg[s][2] = (_Float16)(a0.z * c);
+                qreg[s][3] = (_Float16)(a0.w * c); qreg[s][4] = (_Float16)(a1.x * c); qreg[s][5] = (_Float16)(a1.y * c);
+                qreg[s][6] = (_Float16)(a1.z * c); qreg[s][7] = (_Float16)(a1.w * c);
+            } else {
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
             }
         }
-        // masks only where the tile crosses the diagonal, the sequence end or the window
-        const bool edge = (k0 + PF_BK > q0) || (k0 + PF_BK > T) || (window > 0 && k0 <= q0 + 31 - window + 1);
-        if (edge) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
-                    const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
-                    if (!vis) st[t][e] = -INFINITY;
+        f32x16 oacc[HD / 32];
+    #pragma unroll
+        for (int c = 0; c < HD / 32; ++c)
+    #pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
+        float m_run = -INFINITY, l_run = 0.f;
+
+        int buf = 0;
+        for (int k0 = kbeg; k0 < kend; k0 += PF_BK, buf ^= 1) {
+    #pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                *(gh_u32x4*)(sK[buf] + kr[i] * KS + kc[i]) = pk[i];
+                *(gh_u32x4*)(sVt[buf] + vc[i] * VS + vr[i]) = pv[i];
+            }
+            __syncthreads();
+            if (k0 + PF_BK < kend) {
+                const int kn = k0 + PF_BK;
+    #pragma unroll
+                for (int i = 0; i < KPT; ++i) {
+                    pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kn + kr[i]) * HD + kc[i]);
+                    pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kn + vr[i]);
                 }
+            }
+            if (k0 > q0 + 31) continue;  // whole tile in this wave's future (uniform per wave)
+            const _Float16* cK = sK[buf];
+            const _Float16* cV = sVt[buf];
+            f32x16 st[2];
+    #pragma unroll
+            for (int t = 0; t < 2; ++t) {
+    #pragma unroll
+                for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
+    #pragma unroll
+                for (int s = 0; s < HD / 16; ++s) {
+                    const f16x8 ka = *(const f16x8*)(cK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
+                    st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[s], st[t], 0, 0, 0);
+                }
+            }
+            // masks only where the tile crosses the diagonal, the sequence end or the window
+            const bool edge = (k0 + PF_BK > q0) || (k0 + PF_BK > T) || (window > 0 && k0 <= q0 + 31 - window + 1);
+            if (edge) {
+    #pragma unroll
+                for (int t = 0; t < 2; ++t)
+    #pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
+                        const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
+                        if (!vis) st[t][e] = -INFINITY;
+                    }
+            }
+            // row maximum over the lane's 32 keys as a tree (no 32-long dependent chain)
+            float mx[16];
+    #pragma unroll
+            for (int e = 0; e < 16; ++e) mx[e] = fmaxf(st[0][e], st[1][e]);
+    #pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+    #pragma unroll
+                for (int e = 0; e < w; ++e) mx[e] = fmaxf(mx[e], mx[e + w]);
+            float tmax = mx[0];
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float m_new = fmaxf(m_run, tmax);
+            const float msub = (m_new == -INFINITY) ? 0.f : m_new;  // fully masked row: exp2(-inf) = 0
+            const float alpha = __builtin_amdgcn_exp2f(m_run - msub);
+            f16x8 pa[4];
+            float ps[16];
+    #pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p0 = __builtin_amdgcn_exp2f(st[0][e] - msub), p1 = __builtin_amdgcn_exp2f(st[1][e] - msub);
+                pa[e >> 3][e & 7] = (_Float16)p0;
+                pa[2 + (e >> 3)][e & 7] = (_Float16)p1;
+                ps[e] = p0 + p1;
+            }
+    #pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+    #pragma unroll
+                for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
+            float psum = ps[0];
+            psum += __shfl_xor(psum, 32, 64);
+            l_run = l_run * alpha + psum;
+            const bool moved = m_new != m_run;
+            m_run = m_new;
+            if (__ballot(moved)) {  // some row maximum moved: rescale (alpha = 1 for the others)
+                // the alphas of the wave's 32 rows through LDS: a lane needs rows 8j + 4hf + 0..3
+                if (hf == 0) salpha[wave][lane & 31] = alpha;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float4 a4 = *(const float4*)&salpha[wave][8 * j + 4 * hf];
+                    const float ar[4] = {a4.x, a4.y, a4.z, a4.w};
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i)
+    #pragma unroll
+                        for (int c = 0; c < HD / 32; ++c) oacc[c][4 * j + i] *= ar[i];
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+            }
+    #pragma unroll
+            for (int u = 0; u < 4; ++u) {
+    #pragma unroll
+                for (int c = 0; c < HD / 32; ++c) {
+                    const f16x8 vb8 = *(const f16x8*)(cV + (32 * c + (lane & 31)) * VS + 16 * u + 8 * hf);
+                    oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
+                }
+            }
         }
-        // row maximum over the lane's 32 keys as a tree (no 32-long dependent chain)
-        float mx[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx[e] = fmaxf(st[0][e], st[1][e]);
-#pragma unroll
-        for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-            for (int e = 0; e < w; ++e) mx[e] = fmaxf(mx[e], mx[e + w]);
-        float tmax = mx[0];
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float msub = (m_new == -INFINITY) ? 0.f : m_new;  // fully masked row: exp2(-inf) = 0
-        const float alpha = __builtin_amdgcn_exp2f(m_run - msub);
-        f16x8 pa[4];
-        float ps[16];
-#pragma unroll
+        const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const float p0 = __builtin_amdgcn_exp2f(st[0][e] - msub), p1 = __builtin_amdgcn_exp2f(st[1][e] - msub);
-            pa[e >> 3][e & 7] = (_Float16)p0;
-            pa[2 + (e >> 3)][e & 7] = (_Float16)p1;
-            ps[e] = p0 + p1;
+            const int r = 8 * (e >> 2) + 4 * hf + (e & 3);
+            const float inv = __shfl(linv, r, 64);
+            const int qi = q0 + r;
+            if (qi >= T) continue;
+            float* dst = out + b * qs + ((size_t)qi * H + h) * HD;
+    #pragma unroll
+            for (int c = 0; c < HD / 32; ++c) dst[32 * c + (lane & 31)] = oacc[c][e] * inv;
         }
-#pragma unroll
-        for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-            for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
-        float psum = ps[0];
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * alpha + psum;
-        const bool moved = m_new != m_run;
-        m_run = m_new;
-        if (__ballot(moved)) {  // some row maximum moved: rescale (alpha = 1 for the others)
-            // the alphas of the wave's 32 rows through LDS: a lane needs rows 8j + 4hf + 0..3
-            if (hf == 0) salpha[wave][lane & 31] = alpha;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 a4 = *(const float4*)&salpha[wave][8 * j + 4 * hf];
-                const float ar[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int c = 0; c < HD / 32; ++c) oacc[c][4 * j + i] *= ar[i];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-#pragma unroll
-            for (int c = 0; c < HD / 32; ++c) {
-                const f16x8 vb8 = *(const f16x8*)(cV + (32 * c + (lane & 31)) * VS + 16 * u + 8 * hf);
-                oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
-            }
-        }
-    }
-    const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int r = 8 * (e >> 2) + 4 * hf + (e & 3);
-        const float inv = __shfl(linv, r, 64);
-        const int qi = q0 + r;
-        if (qi >= T) continue;
-        float* dst = out + b * qs + ((size_t)qi * H + h) * HD;
-#pragma unroll
-        for (int c = 0; c < HD / 32; ++c) dst[32 * c + (lane & 31)] = oacc[c][e] * inv;
     }
 }
 
@@ -1084,7 +1092,7 @@ int attention_prefill(const float* q, const float* k, const float* v, float* out
         if (!kv16) return fail(GH_ENOMEM, "attention prefill: workspace");
         _Float16* K16 = kv16;
         _Float16* Vt16 = kv16 + (size_t)B * KV * Tp * hd;
-        const dim3 gs(Tp / PF_BK, KV, B), grid(cdiv(T, PF_BQ), H, B);
+        const dim3 gs(Tp / PF_BK, KV, B), grid(cdiv(cdiv(T, PF_BQ), 2), H, B);  // q-tiles in pairs
         if (hd == 64) {
             hipLaunchKernelGGL(k_kv_f16<64>, gs, dim3(256), 0, stream(), k, v, K16, Vt16, T, KV, Tp);
             hipLaunchKernelGGL(k_attn_prefill_f16<64>, grid, dim3(256), 0, stream(), q, K16, Vt16, out, T, Tp, H, KV,
