@@ -179,7 +179,7 @@ def test_prefill_golden(gh, tag):
 
 
 @pytest.mark.parametrize("B,T,H,KV,hd,win", [(1, 200, 8, 2, 64, 0), (2, 130, 4, 4, 128, 0), (1, 300, 8, 2, 64, 77),
-                                             (1, 1, 4, 1, 128, 0)])
+                                             (1, 1, 4, 1, 128, 0), (1, 520, 4, 2, 128, 0), (2, 700, 2, 1, 64, 0)])
 def test_prefill_mfma_vs_oracle(gh, B, T, H, KV, hd, win):
     q = O.rng_normal(90, B * T * H * hd)
     k = O.rng_normal(91, B * T * KV * hd)
