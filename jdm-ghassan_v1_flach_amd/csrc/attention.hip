@@ -871,7 +871,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
         if (window > 0) kbeg = max(0, qt * PF_BQ - window + 1) / PF_BK * PF_BK;
         // per-thread piece coordinates (fixed): K row kr, dims kc; V^T dim vc, keys vr
         int kr[KPT], kc[KPT], vc[KPT], vr[KPT];
-    #pragma unroll
+#pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int e = tid + 256 * i;
             kr[i] = e / (HD / 8); kc[i] = (e % (HD / 8)) * 8;
@@ -879,7 +879,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
         }
         gh_u32x4 pk[KPT], pv[KPT];  // (ext-vector: an array of uint4 structs stays in scratch)
         if (kbeg < kend) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < KPT; ++i) {
                 pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kbeg + kr[i]) * HD + kc[i]);
                 pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kbeg + vr[i]);
@@ -888,7 +888,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
 
         const int qj = q0 + (lane & 31), hf = lane >> 5;
         f16x8 qreg[HD / 16];
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < HD / 16; ++s) {
             if (qj < T) {
                 const float* src = qb + ((size_t)qj * H + h) * HD + 16 * s + 8 * hf;
@@ -899,20 +899,20 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
                 qreg[s][3] = (_Float16)(a0.w * c); qreg[s][4] = (_Float16)(a1.x * c); qreg[s][5] = (_Float16)(a1.y * c);
                 qreg[s][6] = (_Float16)(a1.z * c); qreg[s][7] = (_Float16)(a1.w * c);
             } else {
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 8; ++e) qreg[s][e] = (_Float16)0.f;
             }
         }
         f32x16 oacc[HD / 32];
-    #pragma unroll
+#pragma unroll
         for (int c = 0; c < HD / 32; ++c)
-    #pragma unroll
+#pragma unroll
             for (int e = 0; e < 16; ++e) oacc[c][e] = 0.f;
         float m_run = -INFINITY, l_run = 0.f;
 
         int buf = 0;
         for (int k0 = kbeg; k0 < kend; k0 += PF_BK, buf ^= 1) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < KPT; ++i) {
                 *(gh_u32x4*)(sK[buf] + kr[i] * KS + kc[i]) = pk[i];
                 *(gh_u32x4*)(sVt[buf] + vc[i] * VS + vr[i]) = pv[i];
@@ -920,7 +920,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             __syncthreads();
             if (k0 + PF_BK < kend) {
                 const int kn = k0 + PF_BK;
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < KPT; ++i) {
                     pk[i] = *(const gh_u32x4*)(kbase + (size_t)(kn + kr[i]) * HD + kc[i]);
                     pv[i] = *(const gh_u32x4*)(vbase + (size_t)vc[i] * Tp + kn + vr[i]);
@@ -930,11 +930,11 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             const _Float16* cK = sK[buf];
             const _Float16* cV = sVt[buf];
             f32x16 st[2];
-    #pragma unroll
+#pragma unroll
             for (int t = 0; t < 2; ++t) {
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < 16; ++e) st[t][e] = 0.f;
-    #pragma unroll
+#pragma unroll
                 for (int s = 0; s < HD / 16; ++s) {
                     const f16x8 ka = *(const f16x8*)(cK + (32 * t + (lane & 31)) * KS + 16 * s + 8 * hf);
                     st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[s], st[t], 0, 0, 0);
@@ -943,9 +943,9 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             // masks only where the tile crosses the diagonal, the sequence end or the window
             const bool edge = (k0 + PF_BK > q0) || (k0 + PF_BK > T) || (window > 0 && k0 <= q0 + 31 - window + 1);
             if (edge) {
-    #pragma unroll
+#pragma unroll
                 for (int t = 0; t < 2; ++t)
-    #pragma unroll
+#pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const int key = k0 + 32 * t + 8 * (e >> 2) + 4 * hf + (e & 3);
                         const bool vis = key <= qj && key < T && (window <= 0 || key > qj - window);
@@ -954,11 +954,11 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             }
             // row maximum over the lane's 32 keys as a tree (no 32-long dependent chain)
             float mx[16];
-    #pragma unroll
+#pragma unroll
             for (int e = 0; e < 16; ++e) mx[e] = fmaxf(st[0][e], st[1][e]);
-    #pragma unroll
+#pragma unroll
             for (int w = 8; w >= 1; w >>= 1)
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < w; ++e) mx[e] = fmaxf(mx[e], mx[e + w]);
             float tmax = mx[0];
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
@@ -967,16 +967,16 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             const float alpha = __builtin_amdgcn_exp2f(m_run - msub);
             f16x8 pa[4];
             float ps[16];
-    #pragma unroll
+#pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const float p0 = __builtin_amdgcn_exp2f(st[0][e] - msub), p1 = __builtin_amdgcn_exp2f(st[1][e] - msub);
                 pa[e >> 3][e & 7] = (_Float16)p0;
                 pa[2 + (e >> 3)][e & 7] = (_Float16)p1;
                 ps[e] = p0 + p1;
             }
-    #pragma unroll
+#pragma unroll
             for (int w = 8; w >= 1; w >>= 1)
-    #pragma unroll
+#pragma unroll
                 for (int e = 0; e < w; ++e) ps[e] += ps[e + w];
             float psum = ps[0];
             psum += __shfl_xor(psum, 32, 64);
@@ -989,21 +989,21 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float4 a4 = *(const float4*)&salpha[wave][8 * j + 4 * hf];
                     const float ar[4] = {a4.x, a4.y, a4.z, a4.w};
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 4; ++i)
-    #pragma unroll
+#pragma unroll
                         for (int c = 0; c < HD / 32; ++c) oacc[c][4 * j + i] *= ar[i];
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
             }
-    #pragma unroll
+#pragma unroll
             for (int u = 0; u < 4; ++u) {
-    #pragma unroll
+#pragma unroll
                 for (int c = 0; c < HD / 32; ++c) {
                     const f16x8 vb8 = *(const f16x8*)(cV + (32 * c + (lane & 31)) * VS + 16 * u + 8 * hf);
                     oacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[u], vb8, oacc[c], 0, 0, 0);
@@ -1011,14 +1011,14 @@ __global__ void __launch_bounds__(256, 2) k_attn_prefill_f16(const float* __rest
             }
         }
         const float linv = l_run > 0.f ? 1.0f / l_run : 0.f;
-    #pragma unroll
+#pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int r = 8 * (e >> 2) + 4 * hf + (e & 3);
             const float inv = __shfl(linv, r, 64);
             const int qi = q0 + r;
             if (qi >= T) continue;
             float* dst = out + b * qs + ((size_t)qi * H + h) * HD;
-    #pragma unroll
+#pragma unroll
             for (int c = 0; c < HD / 32; ++c) dst[32 * c + (lane & 31)] = oacc[c][e] * inv;
         }
     }
