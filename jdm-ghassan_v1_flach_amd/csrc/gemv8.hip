@@ -31,9 +31,15 @@ struct G8Raw {  // one super-block of one row, this lane's part: header + 4 x 8 
     uint2 q[4];
 };
 
+// K slices: grid row blockIdx.y takes values [blockIdx.y K, (blockIdx.y + 1) K) of rows of
+// ldx activations and writes its partial sums to y + blockIdx.y M N.
 template <int SBW>
 __global__ void __launch_bounds__(512) k_gemv8_q4k(const float* __restrict__ x, const uint8_t* __restrict__ W,
-                                                    float* __restrict__ y, int M, int K, int N, size_t rowb) {
+                                                    float* __restrict__ y, int M, int K, int N, size_t rowb, int ldx) {
+    const int ks0 = blockIdx.y * K;  // first value of this slice
+    x += ks0;
+    W += (size_t)(ks0 / 256) * 144;
+    y += (size_t)blockIdx.y * M * N;
     __shared__ float red[2][8][8][16];  // [buf][wave][token][row]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, WB = blockDim.x >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -51,7 +57,7 @@ __global__ void __launch_bounds__(512) k_gemv8_q4k(const float* __restrict__ x, 
             for (int j = 0; j < 8; ++j) {
                 float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
                 if (live) {
-                    const float4* p = (const float4*)(x + (size_t)t * K + k0 + 32 * j);
+                    const float4* p = (const float4*)(x + (size_t)t * ldx + k0 + 32 * j);
                     v0 = p[0];
                     v1 = p[1];
                 }
@@ -136,9 +142,18 @@ __global__ void __launch_bounds__(512) k_gemv8_q4k(const float* __restrict__ x, 
     }
 }
 
+// sum of the K-slice partials, in slice order
+__global__ void __launch_bounds__(256) k_g8_sum(const float* __restrict__ part, float* __restrict__ y, int n, int S) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = part[i];
+    for (int s = 1; s < S; ++s) v += part[(size_t)s * n + i];
+    y[i] = v;
+}
+
 template <int SBW>
-static int g8_launch(const float* x, const void* w, float* y, int M, int K, int N) {
-    const int WB = K / (256 * SBW);
+static int g8_launch(const float* x, const void* w, float* y, int M, int K, int N, int S) {
+    const int Ks = K / S, WB = Ks / (256 * SBW);
     static int per_cu[17];
     if (!per_cu[WB]) {
         int nb = 0;
@@ -146,23 +161,43 @@ static int g8_launch(const float* x, const void* w, float* y, int M, int K, int 
         per_cu[WB] = e == hipSuccess && nb > 0 ? nb : 1;
     }
     const int ntiles = (N + 15) / 16;
-    const int slots = per_cu[WB] * num_cus();
-    hipLaunchKernelGGL(k_gemv8_q4k<SBW>, dim3(ntiles < slots ? ntiles : slots), dim3(64 * WB), 0, stream(), x,
-                       (const uint8_t*)w, y, M, K, N, row_bytes(3, K));
+    const int slots = per_cu[WB] * num_cus() / S;  // the K slices share the chip
+    float* out = y;
+    if (S > 1) {
+        out = (float*)workspace(WS_GEMM_PART, (size_t)S * M * N * 4);
+        if (!out) return fail(GH_ENOMEM, "gemv8: workspace");
+    }
+    hipLaunchKernelGGL(k_gemv8_q4k<SBW>, dim3(ntiles < slots ? ntiles : (slots > 0 ? slots : 1), S), dim3(64 * WB),
+                       0, stream(), x, (const uint8_t*)w, out, M, Ks, N, row_bytes(3, K), K);
     GH_LAUNCHED("k_gemv8_q4k");
+    if (S > 1) {
+        hipLaunchKernelGGL(k_g8_sum, dim3(cdiv(M * N, 256)), dim3(256), 0, stream(), out, y, M * N, S);
+        GH_LAUNCHED("k_g8_sum");
+    }
     return GH_OK;
 }
 
-// Returns 1 if handled: Q4_K, 2 <= M <= 8, K a multiple of 256 up to 4096.
+// Returns 1 if handled: Q4_K, 2 <= M <= 8, K a multiple of 256; above 4096 values the row is
+// cut into equal K slices (the smallest count whose slice fits a block), their partial sums
+// added by a second launch in slice order.
 int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
     if (kind != 3 || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
     const int nsb = K / 256;
     // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands and two tiles of
     // weight bytes stay in registers)
-    if (nsb <= 8) *rc = g8_launch<1>(x, w, y, M, K, N);
-    else if (nsb % 2 == 0 && nsb <= 16) *rc = g8_launch<2>(x, w, y, M, K, N);
-    else return 0;
-    return 1;
+    for (int S = 1; S <= 8; ++S) {
+        if (nsb % S) continue;
+        const int ns = nsb / S;
+        if (ns <= 8) {
+            *rc = g8_launch<1>(x, w, y, M, K, N, S);
+            return 1;
+        }
+        if (ns % 2 == 0 && ns <= 16) {
+            *rc = g8_launch<2>(x, w, y, M, K, N, S);
+            return 1;
+        }
+    }
+    return 0;
 }
 
 }  // namespace gh

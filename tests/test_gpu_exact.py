@@ -28,15 +28,16 @@ def _run_linear(gh, x, w, M, K, N, kind):
 
 
 @pytest.mark.parametrize("kind", [2, 3])
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096),
-                                   (1, 512, 2192), (1, 1024, 520), (1, 2048, 4100)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096), (8, 14336, 4096),
+                                   (3, 7168, 2056), (1, 512, 2192), (1, 1024, 520), (1, 2048, 4100)])
 def test_gemv_c2_vs_exact(gh, kind, M, K, N):
     """c2 shapes and the decode shapes of the int8 single-token GEMV (K <= 2048 for Q8_0, with a
-    short last tile at N = 520 / 4100)."""
+    short last tile at N = 520 / 4100); batched Q4_K rows longer than 4096 values run as K slices
+    (K 14336: 4 slices, K 7168: 2) whose partial sums are added in slice order."""
     w = O.quantize(kind, O.rng_normal(2, N * K, 0, 0.02))
     x = O.rng_normal(8, M * K)
     got = _run_linear(gh, x, w, M, K, N, kind)
-    if kind == 3 and M > 1 and K <= 4096:
+    if kind == 3 and M > 1:
         # the batched Q4_K GEMV (k_gemv8_q4k) decodes each weight to fp16, as the reference's
         # quant_materialize does: its exact product is the one over those fp16 weights
         W16 = O.f16_to_f32(O.materialize(kind, w, N * K)).astype(np.float64).reshape(N, K)
