@@ -143,7 +143,8 @@ def kernel_suite(gh):
     res = {}
     # ---------------- c2: quantized GEMV / GEMM, W 14336x4096
     for kind, kname in ((3, "q4_k"), (2, "q8_0")):
-        for (M, K, N) in ((1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096), (2048, 4096, 14336)):
+        for (M, K, N) in ((1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096), (8, 14336, 4096),
+                          (2048, 4096, 14336), (2048, 14336, 4096)):
             w = gh.quantize(kind, gh.rng_normal(2, N * K, 0, 0.02))
             x = gh.rng_normal(3, M * K)
             dw, dx = gh.Buf.from_array(w), gh.Buf.from_array(x)
@@ -153,7 +154,8 @@ def kernel_suite(gh):
             tag = f"c2_{kname}_M{M}_{N}x{K}"
             if M <= 8:
                 kern = ("k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else
-                        "k_gemv8_q4k" if (kind == 3 and 2 <= M <= 8 and K <= 4096) else "k_gemv_mfma")
+                        "k_gemv8_q4k" if (kind == 3 and 2 <= M <= 8 and K <= 4096) else
+                        "k_gemv8_q4k (4 K slices) + k_g8_sum" if (kind == 3 and 2 <= M <= 8) else "k_gemv_mfma")
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)
             else:
                 res[tag] = entry("k_dequant_fused (weights + x to bf16)+hipBLASLt bf16 GEMM (fp32 out)", ms,
