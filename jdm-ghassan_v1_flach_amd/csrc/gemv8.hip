@@ -18,6 +18,13 @@
 // Weight values: (1024 + q) is made an fp16 number by one v_and_or_b32 per
 // pair of codes, then q d sc - dmin m = (1024 + q) s + nb with s = d sc,
 // nb = -(1024 s + dmin m), rounded to fp16.
+//
+// Q8_0 (k_gemv8_q8): 256 values are 8 blocks of 34 bytes (a 272-byte group); lane (n, g)
+// reads blocks 2g and 2g + 1 of its row as 17 dwords (68 bytes, 4-byte aligned) and MFMA
+// k-step m (0..7) takes codes 8 (m % 4) .. + 7 of block 2g + m / 4 from every lane, the A
+// operands permuted to match. A code becomes an fp16 integer exactly (0x6400 | (q + 128),
+// minus 1152) and one fp16 multiply by the block scale rounds q d once: the fp16 weight the
+// reference's quant_materialize forms.
 #include <stdlib.h>
 
 #include "gemm_tile.h"
@@ -142,6 +149,126 @@ __global__ void __launch_bounds__(512) k_gemv8_q4k(const float* __restrict__ x, 
     }
 }
 
+// codes 4i .. 4i + 3 of a dword -> two packed fp16 pairs (q0, q1), (q2, q3), exact
+__device__ __forceinline__ void g8_q8_pairs(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;  // q + 128 as unsigned bytes
+    lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+}
+typedef _Float16 g8_h2 __attribute__((ext_vector_type(2)));
+
+template <int SBW>
+__global__ void __launch_bounds__(512) k_gemv8_q8(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                   float* __restrict__ y, int M, int K, int N, size_t rowb, int ldx) {
+    constexpr int GB = 272;  // bytes per 256 values
+    const int ks0 = blockIdx.y * K;
+    x += ks0;
+    W += (size_t)(ks0 / 256) * GB;
+    y += (size_t)blockIdx.y * M * N;
+    __shared__ float red[2][8][8][16];  // [buf][wave][token][row]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, WB = blockDim.x >> 6;
+    const int n16 = lane & 15, g = lane >> 4;
+    const int ntiles = (N + 15) >> 4;
+    // ---- A operands: row n16 = token n16/2, part n16%2; k-step m, value i: position
+    // 32 (2g + m/4) + 8 (m%4) + i of the group
+    f16x8 A[SBW][8];
+    {
+        const int t = n16 >> 1, part = n16 & 1;
+        const bool live = t < M;
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int k0 = (wave * SBW + s) * 256 + 32 * (2 * g + (m >> 2)) + 8 * (m & 3);
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (live) {
+                    const float4* p = (const float4*)(x + (size_t)t * ldx + k0);
+                    v0 = p[0];
+                    v1 = p[1];
+                }
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 h = (_Float16)v[e];
+                    A[s][m][e] = part ? (_Float16)(v[e] - (float)h) : h;
+                }
+            }
+        }
+    }
+    struct Raw {
+        uint32_t d[17];
+    };
+    auto load = [&](int tile, Raw (&r)[SBW]) {
+        int n = tile * 16 + n16;
+        n = n < N ? n : N - 1;
+        const uint8_t* row = W + (size_t)n * rowb;
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+            const uint32_t* src = (const uint32_t*)(row + (size_t)(wave * SBW + s) * GB + 68 * g);
+#pragma unroll
+            for (int i = 0; i < 17; ++i) r[s].d[i] = src[i];
+        }
+    };
+    Raw ra[SBW], rb[SBW];
+    int tile = blockIdx.x;
+    if (tile < ntiles) load(tile, ra);
+    int buf = 0;
+    const g8_h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    auto run = [&](int tl, Raw (&cur)[SBW], Raw (&nxt)[SBW]) {
+        if (tl + (int)gridDim.x < ntiles) load(tl + gridDim.x, nxt);
+        g8_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SBW; ++s) {
+            const uint32_t* d = cur[s].d;
+            const _Float16 s0 = __builtin_bit_cast(_Float16, (uint16_t)(d[0] & 0xFFFF));  // block 2g
+            const _Float16 s1 = __builtin_bit_cast(_Float16, (uint16_t)(d[8] >> 16));     // block 2g + 1
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const int q = m & 3;
+                uint32_t c0, c1;
+                if (m < 4) {  // block 2g: codes at byte 2 + c
+                    c0 = __builtin_amdgcn_alignbyte(d[2 * q + 1], d[2 * q], 2);
+                    c1 = __builtin_amdgcn_alignbyte(d[2 * q + 2], d[2 * q + 1], 2);
+                } else {  // block 2g + 1: codes at byte 36 + c (dword aligned)
+                    c0 = d[9 + 2 * q];
+                    c1 = d[10 + 2 * q];
+                }
+                const _Float16 sc = m < 4 ? s0 : s1;
+                const g8_h2 sc2 = {sc, sc};
+                uint32_t pr[4];
+                g8_q8_pairs(c0, pr[0], pr[1]);
+                g8_q8_pairs(c1, pr[2], pr[3]);
+                f16x8 b;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const g8_h2 cq = __builtin_bit_cast(g8_h2, pr[i]) - off;  // the codes, exact
+                    const g8_h2 wv = cq * sc2;                                // q d, rounded once
+                    b[2 * i] = wv[0];
+                    b[2 * i + 1] = wv[1];
+                }
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[s][m], b, acc, 0, 0, 0);
+            }
+        }
+        red[buf][wave][2 * g][n16] = acc[0] + acc[1];
+        red[buf][wave][2 * g + 1][n16] = acc[2] + acc[3];
+        __syncthreads();
+        for (int i = tid; i < 128; i += blockDim.x) {
+            const int t = i >> 4, nn = i & 15, n = tl * 16 + nn;
+            float v = 0.f;
+            for (int w = 0; w < WB; ++w) v += red[buf][w][t][nn];
+            if (t < M && n < N) y[(size_t)t * N + n] = v;
+        }
+        buf ^= 1;
+    };
+    while (tile < ntiles) {
+        run(tile, ra, rb);
+        tile += gridDim.x;
+        if (tile >= ntiles) break;
+        run(tile, rb, ra);
+        tile += gridDim.x;
+    }
+}
+
 // sum of the K-slice partials, in slice order
 __global__ void __launch_bounds__(256) k_g8_sum(const float* __restrict__ part, float* __restrict__ y, int n, int S) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -151,13 +278,14 @@ __global__ void __launch_bounds__(256) k_g8_sum(const float* __restrict__ part, 
     y[i] = v;
 }
 
-template <int SBW>
+template <int SBW, bool Q8>
 static int g8_launch(const float* x, const void* w, float* y, int M, int K, int N, int S) {
     const int Ks = K / S, WB = Ks / (256 * SBW);
     static int per_cu[17];
+    const auto kern = Q8 ? k_gemv8_q8<SBW> : k_gemv8_q4k<SBW>;
     if (!per_cu[WB]) {
         int nb = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv8_q4k<SBW>, 64 * WB, 0);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kern, 64 * WB, 0);
         per_cu[WB] = e == hipSuccess && nb > 0 ? nb : 1;
     }
     const int ntiles = (N + 15) / 16;
@@ -167,9 +295,9 @@ static int g8_launch(const float* x, const void* w, float* y, int M, int K, int 
         out = (float*)workspace(WS_GEMM_PART, (size_t)S * M * N * 4);
         if (!out) return fail(GH_ENOMEM, "gemv8: workspace");
     }
-    hipLaunchKernelGGL(k_gemv8_q4k<SBW>, dim3(ntiles < slots ? ntiles : (slots > 0 ? slots : 1), S), dim3(64 * WB),
-                       0, stream(), x, (const uint8_t*)w, out, M, Ks, N, row_bytes(3, K), K);
-    GH_LAUNCHED("k_gemv8_q4k");
+    hipLaunchKernelGGL(kern, dim3(ntiles < slots ? ntiles : (slots > 0 ? slots : 1), S), dim3(64 * WB), 0, stream(),
+                       x, (const uint8_t*)w, out, M, Ks, N, row_bytes(Q8 ? 2 : 3, K), K);
+    GH_LAUNCHED(Q8 ? "k_gemv8_q8" : "k_gemv8_q4k");
     if (S > 1) {
         hipLaunchKernelGGL(k_g8_sum, dim3(cdiv(M * N, 256)), dim3(256), 0, stream(), out, y, M * N, S);
         GH_LAUNCHED("k_g8_sum");
@@ -177,11 +305,12 @@ static int g8_launch(const float* x, const void* w, float* y, int M, int K, int 
     return GH_OK;
 }
 
-// Returns 1 if handled: Q4_K, 2 <= M <= 8, K a multiple of 256; above 4096 values the row is
-// cut into equal K slices (the smallest count whose slice fits a block), their partial sums
-// added by a second launch in slice order.
+// Returns 1 if handled: Q4_K or Q8_0 (16-byte aligned rows), 2 <= M <= 8, K a multiple of 256;
+// above 4096 values the row is cut into equal K slices (the smallest count whose slice fits a
+// block), their partial sums added by a second launch in slice order.
 int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N, int kind, int* rc) {
-    if (kind != 3 || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
+    if ((kind != 3 && kind != 2) || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
+    if (kind == 2 && ((uintptr_t)w & 15)) return 0;
     const int nsb = K / 256;
     // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands and two tiles of
     // weight bytes stay in registers)
@@ -189,11 +318,11 @@ int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N,
         if (nsb % S) continue;
         const int ns = nsb / S;
         if (ns <= 8) {
-            *rc = g8_launch<1>(x, w, y, M, K, N, S);
+            *rc = kind == 2 ? g8_launch<1, true>(x, w, y, M, K, N, S) : g8_launch<1, false>(x, w, y, M, K, N, S);
             return 1;
         }
         if (ns % 2 == 0 && ns <= 16) {
-            *rc = g8_launch<2>(x, w, y, M, K, N, S);
+            *rc = kind == 2 ? g8_launch<2, true>(x, w, y, M, K, N, S) : g8_launch<2, false>(x, w, y, M, K, N, S);
             return 1;
         }
     }

@@ -33,13 +33,13 @@ def _run_linear(gh, x, w, M, K, N, kind):
 def test_gemv_c2_vs_exact(gh, kind, M, K, N):
     """c2 shapes and the decode shapes of the int8 single-token GEMV (K <= 2048 for Q8_0, with a
     short last tile at N = 520 / 4100); batched Q4_K rows longer than 4096 values run as K slices
-    (K 14336: 4 slices, K 7168: 2) whose partial sums are added in slice order."""
+    (K 14336: 4 slices, K 7168: 2) whose partial sums are added in slice order; Q8_0 likewise."""
     w = O.quantize(kind, O.rng_normal(2, N * K, 0, 0.02))
     x = O.rng_normal(8, M * K)
     got = _run_linear(gh, x, w, M, K, N, kind)
-    if kind == 3 and M > 1:
-        # the batched Q4_K GEMV (k_gemv8_q4k) decodes each weight to fp16, as the reference's
-        # quant_materialize does: its exact product is the one over those fp16 weights
+    if M > 1:
+        # the batched GEMVs (k_gemv8_q4k / k_gemv8_q8) decode each weight to fp16, as the
+        # reference's quant_materialize does: their exact product is the one over those weights
         W16 = O.f16_to_f32(O.materialize(kind, w, N * K)).astype(np.float64).reshape(N, K)
         y64 = x.reshape(M, K).astype(np.float64) @ W16.T
     else:
