@@ -119,3 +119,22 @@ def test_prefill_gemm_c2_activation_range(gh):
     for i, r in enumerate(rows):
         n, _ = exact.errs(got[r], y64[i])
         assert n <= 2e-2, (r, scales[r], n)
+
+
+@pytest.mark.parametrize("kind", [2, 3])
+@pytest.mark.parametrize("M,K,N", [(2, 768, 100), (5, 1280, 33), (7, 4352, 64), (3, 10240, 48), (8, 256, 17)])
+def test_batched_gemv_shapes_vs_exact(gh, kind, M, K, N):
+    """The batched GEMVs at odd shapes: 3 and 5 super-blocks per row (one wave each), a row of
+    17 super-blocks (no slice count fits: the generic path), 40 super-blocks in 4 K slices, a
+    single super-block, and row counts that end in a partial 16-row tile."""
+    w = O.quantize(kind, O.rng_normal(12, N * K, 0, 0.02))
+    x = O.rng_normal(13, M * K)
+    got = _run_linear(gh, x, w, M, K, N, kind)
+    W16 = O.f16_to_f32(O.materialize(kind, w, N * K)).astype(np.float64).reshape(N, K)
+    y16 = x.reshape(M, K).astype(np.float64) @ W16.T
+    y64 = exact.linear64(x, w, M, K, N, kind)
+    g16 = exact.errs(got, y16)
+    g64 = exact.errs(got, y64)
+    # the batched kernels take the fp16-rounded weights; the generic path may not
+    ok = lambda e: e[0] <= EXACT_NORM and e[1] <= EXACT_ELEM
+    assert ok(g16) or ok(g64), (g16, g64)
