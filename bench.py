@@ -2,7 +2,7 @@
 """Benchmark of the MI355X backend on the BASELINE metric:
 "batch-1 decode tok/s + prefill tok/s (Q4_K hybrid); % HBM/MFMA roofline".
 
-Workload (one "step"): the tiny Granite-4.0 hybrid of BASELINE config 1
+Workload (one "step"): the tiny Granite-4.0 hybrid of benchmark configuration c1
 (vocab 4096, d 512, layers [M, M, A, M, M, A], MoE 8 experts top-2 + shared)
 with its matrices in Q4_K (the metric's weight format; config 1 names Q8_0,
 which is reported beside it), random-init by the shared synthetic recipe:
@@ -13,7 +13,7 @@ from the prefill's logits; the CPU baseline counts the same 63 steps); prefill
 tok/s is reported beside it.
 
 `roofline` is the path's dominant HBM kernel at production shape, the
-single-token Q4_K GEMV of BASELINE config 2 (14336x4096), timed alone over
+single-token Q4_K GEMV of benchmark configuration c2 (14336x4096), timed alone over
 repeated launches with HIP events on the backend stream, cold (10 copies of
 the weights in rotation, 331 MB, more than the 256 MB MALL: every launch reads
 HBM; the headline) and warm (the same copy every launch); `traffic` comes from
@@ -197,7 +197,7 @@ def kernel_suite(gh):
     del b_in, b_out, bv, conv, ssm
     # ---------------- c4: decode attention, L = 1k / 8k / 32k, ragged batch 16, prefill 4096
     Hq, KVh, hd = 32, 8, 128
-    kv_all = gh.rng_normal(4, 2 * 32768 * KVh * hd)  # K then V, N(0,1) (seed 4)
+    kv_all = gh.rng_normal(4, 2 * 32768 * KVh * hd)  # K then V, N(0,1) (benchmark configuration c4, seed 4)
     k16, v16 = to_f16(kv_all[:32768 * KVh * hd]), to_f16(kv_all[32768 * KVh * hd:])
     kb16, vb16 = to_bf16(kv_all[:32768 * KVh * hd]), to_bf16(kv_all[32768 * KVh * hd:])
     q = gh.Buf.from_array(gh.rng_normal(40, Hq * hd))
@@ -627,7 +627,7 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32 activations, Q4_K weights (fp32 accumulate; fp16 MFMA operands in prefill)",
         "data": "synthetic (random-init weights by the seeded recipe, uniform prompt ids seed 1)",
-        "config": {"workload": "BASELINE config 1 tiny Granite-hybrid (V4096 d512 [M,M,A,M,M,A], MoE 8x top-2 + "
+        "config": {"workload": "benchmark configuration c1 tiny Granite-hybrid (V4096 d512 [M,M,A,M,M,A], MoE 8x top-2 + "
                                "shared) in Q4_K: 128-token prefill + 64 greedy tokens, decode "
                                + ("eager" if args.eager_decode else "graph-replayed"),
                    "global_batch": 1, "seq_len": PROMPT + N_NEW, "parallelism": "single GPU"},

@@ -165,7 +165,7 @@ int gh_attention_decode_ring_fp16(const float* q, const uint16_t* kcache, const 
 int gh_attention_decode_ring_fp16_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                                           float* out, int H, int KV, int hd, int ring_start, int pinned_prefix,
                                           int cur_len, int cache_max, float scale, int window);
-/* Extension (no reference counterpart): ragged batched
+/* Extension (no reference counterpart; benchmark configuration c4): ragged batched
  * decode over a paged bf16 KV cache. q [S, H, hd]; pages [n_pages, page_size,
  * KV, hd] bf16; page_table [S, max_pages] (device int32); seq_lens [S]
  * (device int32); out [S, H, hd]. */

@@ -33,10 +33,10 @@ def granite_opts_weights(qkind=2):
     return w
 
 
-# BASELINE config 1 benched workload (bench.py): 128-token prompt + 64 greedy tokens.
+# benchmark configuration c1 benched workload (bench.py): 128-token prompt + 64 greedy tokens.
 C1_PROMPT, C1_NEW, C1_MAX_CTX = 128, 64, 256
 
-# Mamba-2 layer, Q4_K, 4096-token prompt then 512 decode steps.
+# benchmark configuration c3: Mamba-2 layer, Q4_K, 4096-token prompt then 512 decode steps.
 C3 = dict(d=1536, d_inner=3072, heads=48, d_head=64, d_state=128, conv_k=4, T=4096, steps=512)
 C3_STEP_CHECKS = (0, 1, 2, 7, 63, 255, 511)
 

@@ -2,10 +2,10 @@
 GPU test (the oracle restates the reference's CPU path, which dequantises
 whole tensors on every call, core/ops.cpp:304-347):
 
-  granite_c1_q4k_oracle.npz  BASELINE config 1 in Q4_K at the benched workload:
+  granite_c1_q4k_oracle.npz  benchmark configuration c1 in Q4_K at the benched workload:
                              128-token prompt (seed 1) + 64 greedy tokens; ids
                              and top-2 margins of orc_granite_generate.
-  mamba_c3_decode_oracle.npz BASELINE config 3: the Q4_K layer over a 4096-token
+  mamba_c3_decode_oracle.npz benchmark configuration c3: the Q4_K layer over a 4096-token
                              prompt from a zero state (orc_mamba2_forward_q),
                              then 512 single-token steps (orc_mamba2_step_q,
                              the restatement of inference/generator.cpp:510-616)

@@ -12,7 +12,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libgai_ref.so")
 
-# Tiny Granite-hybrid (BASELINE config c1) in the oracle's int layout.
+# Tiny Granite-hybrid (benchmark configuration c1) in the oracle's int layout.
 C1 = dict(V=4096, d=512, L=6, H=8, KV=2, hd=64, E=256, ne=8, K=2, SH=512, d_inner=1024,
           m_heads=16, m_dhead=64, m_dstate=64, conv_k=4, layer_types=[0, 0, 1, 0, 0, 1],
           eps=1e-5, scale=0.125)

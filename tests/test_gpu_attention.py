@@ -39,7 +39,7 @@ def _oracle_ring(q, kc, vc, H, KV, hd, rs, pin, cl, cm, sc, win):
 
 @pytest.mark.parametrize("L", [1024, 8192, 32768])
 def test_decode_c4_lengths(gh, L):
-    """BASELINE config 4 decode, batch 1 (fp16 ring cache, no wrap)."""
+    """benchmark configuration c4 decode, batch 1 (fp16 ring cache, no wrap)."""
     H, KV, hd = 32, 8, 128
     q = O.rng_normal(4, H * hd)
     kc = O.f32_to_f16(O.rng_normal(41, L * KV * hd))
@@ -133,7 +133,7 @@ def test_paged_small(gh):
 
 
 def test_paged_c4_ragged_batch16(gh):
-    """ragged decode, 16 sequences, lengths U[512, 8192]."""
+    """benchmark configuration c4: ragged decode, 16 sequences, lengths U[512, 8192]."""
     H, KV, hd, ps = 32, 8, 128, 64
     lens = (512 + O.rng_below(4, 16, 8192 - 512 + 1)).tolist()
     args = paged_case(16, lens, H, KV, hd, ps, 80)
@@ -144,7 +144,7 @@ def test_paged_c4_ragged_batch16(gh):
 
 @pytest.mark.parametrize("L", [1024, 8192, 32768])
 def test_decode_c4_bf16_batch1(gh, L):
-    """BASELINE config 4 as configured: batch-1 decode over a bf16 K/V cache
+    """benchmark configuration c4 as configured: batch-1 decode over a bf16 K/V cache
     drawn N(0,1) (seed 4), context 1k / 8k / 32k, through the paged bf16 entry
     point with one sequence; the oracle widens bf16 -> fp32 exactly
     (core/dtype.h:121-126) and runs the reference's ring kernel."""
@@ -192,7 +192,7 @@ def test_prefill_mfma_vs_oracle(gh, B, T, H, KV, hd, win):
 
 
 def test_prefill_c4_rows_match_decode(gh):
-    """BASELINE config 4 causal prefill, T=4096: row t equals decode with
+    """benchmark configuration c4 causal prefill, T=4096: row t equals decode with
     cur_len = t+1 over the same (fp32 -> widened) keys, checked on sampled rows."""
     T, H, KV, hd = 4096, 32, 8, 128
     q = O.rng_normal(93, T * H * hd)

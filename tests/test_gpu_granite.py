@@ -1,4 +1,4 @@
-"""End-to-end tiny Granite-hybrid: 128-token prompt, 64
+"""End-to-end tiny Granite-hybrid (benchmark configuration c1): 128-token prompt, 64
 greedy tokens, against the greedy ids and top-2 margins of the COMPILED
 REFERENCE Generator (tests/golden/granite_c1_q8.npz). Ids must be identical
 at every step up to the first step whose reference margin is <= 1e-3 (after

@@ -53,7 +53,7 @@ def test_gemv_parity(gh, kind, M, K, N):
 @pytest.mark.parametrize("kind", [2, 3])
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 14336), (8, 4096, 14336), (1, 14336, 4096)])
 def test_gemv_c2_full(gh, kind, M, K, N):
-    """BASELINE config 2 at full size."""
+    """benchmark configuration c2 at full size."""
     w = _w(kind, N, K)
     x = O.rng_normal(8, M * K)
     y = gh.Buf.zeros(M * N, np.float32)

@@ -53,7 +53,7 @@ def test_ssd_scan_small(gh, T, H, N, chunk):
 
 
 def test_ssd_scan_c3(gh):
-    """BASELINE config 3 scan at full size: T=4096, 48 heads x 64, d_state 128, chunk 256."""
+    """benchmark configuration c3 scan at full size: T=4096, 48 heads x 64, d_state 128, chunk 256."""
     T, H, P, N = 4096, 48, 64, 128
     case = scan_case(T, H, P, N, 3)
     y, st = gpu_scan(gh, case, T, H, P, N)
@@ -119,7 +119,7 @@ def layer_case(d, di, nh, ds, k, kind, seed):
 
 
 def test_mamba_forward_c3_vs_oracle(gh):
-    """BASELINE config 3 layer (d 1536, d_inner 3072, 48x64, d_state 128, Q4_K)
+    """benchmark configuration c3 layer (d 1536, d_inner 3072, 48x64, d_state 128, Q4_K)
     at T=256 against the oracle's sequential layer."""
     d, di, nh, dh, ds, k, T, kind = 1536, 3072, 48, 64, 128, 4, 256, 3
     w, conv_dim = layer_case(d, di, nh, ds, k, kind, 30)
@@ -191,7 +191,7 @@ def test_mamba_prefill_equals_steps(gh):
 
 
 def test_mamba_c3_prompt_then_512_steps(gh):
-    """BASELINE config 3 as configured: the Q4_K layer over a 4096-token prompt
+    """benchmark configuration c3 as configured: the Q4_K layer over a 4096-token prompt
     (chunked SSD scan) from a zero state, then 512 single-token state updates
     carried from the state that scan left. Against the oracle's run of the same
     workload (tests/golden/mamba_c3_decode_oracle.npz: orc_mamba2_forward_q then

@@ -73,7 +73,7 @@ def oracle_moe(case, N, d, E, ne, K, SH, kind):
 @pytest.mark.parametrize("kind", [2, 3])
 @pytest.mark.parametrize("N,skew", [(1, False), (1, True), (5, False)])
 def test_moe_c5_decode(gh, kind, N, skew):
-    """BASELINE config 5 shapes (d 1536, 64 experts top-6, E 512, SH 1024), decode path."""
+    """benchmark configuration c5 shapes (d 1536, 64 experts top-6, E 512, SH 1024), decode path."""
     d, E, ne, K, SH = 1536, 512, 64, 6, 1024
     case = make_case(N, d, E, ne, K, SH, kind, 500 + N, skew)
     out, probs, idx, w = MoE(gh, *case, N, d, E, ne, K, SH, kind).run()
@@ -88,7 +88,7 @@ def test_moe_c5_decode(gh, kind, N, skew):
 @pytest.mark.parametrize("kind", [2, 3])
 @pytest.mark.parametrize("skew", [False, True])
 def test_moe_c5_prefill(gh, kind, skew):
-    """BASELINE config 5 prefill path at 64 tokens (oracle cost), grouped MFMA GEMM."""
+    """benchmark configuration c5 prefill path at 64 tokens (oracle cost), grouped MFMA GEMM."""
     N, d, E, ne, K, SH = 64, 1536, 512, 64, 6, 1024
     case = make_case(N, d, E, ne, K, SH, kind, 600, skew)
     out, probs, idx, w = MoE(gh, *case, N, d, E, ne, K, SH, kind).run()
@@ -124,7 +124,7 @@ def test_moe_c5_prefill_2048_matches_decode_path(gh):
 
 @pytest.mark.parametrize("skew", [False, True])
 def test_moe_c5_prefill_2048_vs_oracle_rows(gh, skew):
-    """BASELINE config 5 prefill at its full 2048 tokens (grouped MFMA path),
+    """benchmark configuration c5 prefill at its full 2048 tokens (grouped MFMA path),
     plain and skewed (+2.0 on 4 experts), against the oracle on 48 sampled
     token rows: the MoE FFN is per token, so the oracle on those rows alone is
     the oracle of the full batch there. Ids bit-exact on every row."""
