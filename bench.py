@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X backend on the BASELINE metric:
+"""Benchmark of the MI355X backend on the headline metric:
 "batch-1 decode tok/s + prefill tok/s (Q4_K hybrid); % HBM/MFMA roofline".
 
 Workload (one "step"): the tiny Granite-4.0 hybrid of benchmark configuration c1
@@ -21,7 +21,7 @@ the committed rocprofv3 PMC summary of `--probe` (FETCH_SIZE + WRITE_SIZE per
 launch, scaled by what the counters read for a plain copy of known size);
 `stream_ceiling` is a read-only streaming kernel over the same cold rotation
 (what the memory system delivers to a kernel that does nothing but read);
-`kernels` gives the per-kernel figures for BASELINE configs 2-5 at
+`kernels` gives the per-kernel figures for benchmark configurations c2-c5 at
 full size. `cpu_baseline` times the CPU oracle (a restatement of the
 reference's CPU path) on the same workload on the host's cores.
 
