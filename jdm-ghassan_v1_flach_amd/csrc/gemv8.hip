@@ -278,6 +278,12 @@ __global__ void __launch_bounds__(256) k_g8_sum(const float* __restrict__ part, 
     y[i] = v;
 }
 
+int g8_sum_launch(const float* part, float* y, int n, int S) {
+    hipLaunchKernelGGL(k_g8_sum, dim3(cdiv(n, 256)), dim3(256), 0, stream(), part, y, n, S);
+    GH_LAUNCHED("k_g8_sum");
+    return GH_OK;
+}
+
 template <int SBW, bool Q8>
 static int g8_launch(const float* x, const void* w, float* y, int M, int K, int N, int S) {
     const int Ks = K / S, WB = Ks / (256 * SBW);

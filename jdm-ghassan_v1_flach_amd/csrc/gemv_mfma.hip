@@ -777,12 +777,20 @@ constexpr int GD_ATT_PT = 8;      // (max, sum) pairs per thread: GD_ATT_MAX / 1
 // as 8-block groups of 272 bytes in place of a 144-byte super-block): lane (n, g) takes blocks
 // 2g and 2g + 1 of a group as 17 dwords, the codes realigned with alignbyte; they are int8
 // already, so no nibble or offset work, and no min term.
-template <int SBW, int NB, bool FUSED = false, bool Q8 = false>
+template <int SBW, int NB, bool FUSED = false, bool Q8 = false, bool SLICED = false>
 __global__ void __launch_bounds__(1024 / SBW) k_gemv_q4k_i8(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                            float* __restrict__ y, int K, int N, size_t rowb,
                                                            int rpb, GmFuse f) {
     using C = GdCfg<SBW, Q8>;
     constexpr int PR = C::PR, NP = C::NP, PPL = C::PPL, SBB = C::SBB;
+    if (SLICED) {
+        // K slices (rows longer than one block takes): grid row blockIdx.y covers values
+        // [blockIdx.y K, (blockIdx.y + 1) K) of each row and writes its partial sums to y + blockIdx.y N
+        const int ks0 = blockIdx.y * K;
+        x += ks0;
+        W += (size_t)(ks0 / 256) * SBB;
+        y += (size_t)blockIdx.y * N;
+    }
     extern __shared__ __attribute__((aligned(16))) uint4 gd_lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n16 = lane & 15, g = lane >> 4;
@@ -1246,15 +1254,22 @@ static int gm_kind(const float* x, const void* w, float* y, int M, int K, int N)
     return gm_ss<KIND, 4>(x, w, y, M, K, N);
 }
 
-template <int SBW, int NB, bool FUSED = false, bool Q8 = false>
-static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, const GmFuse& f = GmFuse{}) {
+int g8_sum_launch(const float* part, float* y, int n, int S);  // gemv8.hip
+
+// S > 1 (plain form only): each row is cut into S equal K slices on the grid's second
+// dimension; the partial sums go to a workspace and are added in slice order.
+template <int SBW, int NB, bool FUSED = false, bool Q8 = false, bool SLICED = false>
+static int gd_launch(const float* x, const uint8_t* w, float* y, int Kfull, int N, const GmFuse& f = GmFuse{},
+                     int S = 1) {
     static int configured = 0;
     static int per_cu[17];  // resident blocks per CU by K / (256 SBW)
-    if (K > (Q8 ? GD_Q8_KMAX : 4096) || K % (256 * SBW) != 0)
-        return fail(GH_EUNSUPPORTED, "k_gemv_q4k_i8: K=%d", K);
+    const int K = Kfull / S;
+    if (S < 1 || (!SLICED && S > 1) || (FUSED && SLICED) || Kfull % S != 0 || K > (Q8 ? GD_Q8_KMAX : 4096) ||
+        K % (256 * SBW) != 0)
+        return fail(GH_EUNSUPPORTED, "k_gemv_q4k_i8: K=%d in %d slices", Kfull, S);
     const size_t lds = gd_lds_bytes(K, SBW, NB, Q8);
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB, FUSED, Q8>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemv_q4k_i8<SBW, NB, FUSED, Q8, SLICED>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)gd_lds_bytes(Q8 ? GD_Q8_KMAX : 4096, SBW, NB, Q8));
         if (e != hipSuccess) return fail(GH_EHIP, "k_gemv_q4k_i8 LDS attribute: %s", hipGetErrorString(e));
@@ -1263,19 +1278,25 @@ static int gd_launch(const float* x, const uint8_t* w, float* y, int K, int N, c
     const int wb = K / (256 * SBW);
     if (!per_cu[wb]) {
         int nb = 0;
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED, Q8>, 64 * wb, lds);
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_gemv_q4k_i8<SBW, NB, FUSED, Q8, SLICED>, 64 * wb, lds);
         per_cu[wb] = e == hipSuccess && nb > 0 ? nb : 1;
     }
     // contiguous row ranges, equal up to 8 rows (16 with weight segments): every block
     // streams the same number of bytes, so no CU runs a tile more than the others
-    const int slots = per_cu[wb] * num_cus();
+    const int slots = per_cu[wb] * num_cus() / S;
     const int align = FUSED && f.w1 ? 16 : 8;
     const int rpb = ((N + slots - 1) / slots + align - 1) / align * align;
     const int blocks = (N + rpb - 1) / rpb;
-    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED, Q8>), dim3(blocks), dim3(64 * wb), lds, stream(), x, w, y, K,
-                       N, row_bytes(Q8 ? 2 : 3, K), rpb, f);
+    float* out = y;
+    if (S > 1) {
+        out = (float*)workspace(WS_GEMM_PART, (size_t)S * N * 4);
+        if (!out) return fail(GH_ENOMEM, "k_gemv_q4k_i8: workspace");
+    }
+    hipLaunchKernelGGL((k_gemv_q4k_i8<SBW, NB, FUSED, Q8, SLICED>), dim3(blocks, S), dim3(64 * wb), lds, stream(), x, w, out,
+                       K, N, row_bytes(Q8 ? 2 : 3, Kfull), rpb, f);
     hipError_t e = hipGetLastError();
-    return e == hipSuccess ? GH_OK : fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(GH_EHIP, "launch of k_gemv_q4k_i8 failed: %s", hipGetErrorString(e));
+    return S > 1 ? g8_sum_launch(out, y, N, S) : GH_OK;
 }
 
 // variant 1: one super-block per wave; 2: two super-blocks per wave (needs K % 512 == 0)
@@ -1294,6 +1315,14 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
     if (M == 1 && kind == 3 && K % 256 == 0 && K <= 4096) {
         *rc = gemv_q4k_i8(x, (const uint8_t*)w, y, K, N, 1);
         return 1;
+    }
+    if (M == 1 && kind == 3 && K % 256 == 0 && K > 4096) {
+        // longer rows: the smallest count of equal K slices that each fit a block
+        for (int S = 2; S <= 8; ++S)
+            if ((K / 256) % S == 0 && K / S <= 4096) {
+                *rc = gd_launch<1, GD_NB, false, false, true>(x, (const uint8_t*)w, y, K, N, GmFuse{}, S);
+                return 1;
+            }
     }
     if (M == 1 && kind == 2 && K % 256 == 0 && K <= GD_Q8_KMAX && ((uintptr_t)w & 15) == 0) {
         *rc = gd_launch<1, GD_NB, false, true>(x, (const uint8_t*)w, y, K, N);
