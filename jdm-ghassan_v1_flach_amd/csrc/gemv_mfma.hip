@@ -1328,6 +1328,13 @@ int gemv_mfma_dispatch(const float* x, const void* w, float* y, int M, int K, in
         *rc = gd_launch<1, GD_NB, false, true>(x, (const uint8_t*)w, y, K, N);
         return 1;
     }
+    if (M == 1 && kind == 2 && K % 256 == 0 && K > GD_Q8_KMAX && ((uintptr_t)w & 15) == 0) {
+        for (int S = 2; S <= 8; ++S)
+            if ((K / 256) % S == 0 && K / S <= GD_Q8_KMAX) {
+                *rc = gd_launch<1, GD_NB, false, true, true>(x, (const uint8_t*)w, y, K, N, GmFuse{}, S);
+                return 1;
+            }
+    }
     if ((kind != 2 && kind != 3) || M < 1 || M > 8 || K % 256 != 0) return 0;
     int mc = M;
     while (mc >= 1 && !(kind == 3 ? gm_fits<3>(K, mc, false) : gm_fits<2>(K, mc, false))) --mc;
