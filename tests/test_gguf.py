@@ -446,3 +446,21 @@ def test_granite_config_needs_architecture_keys(lib, tmp_path):
     write(lib, p, [], [("general.architecture", 8, "ghassan")])
     with pytest.raises(RuntimeError, match="no architecture keys"):
         granite_config(lib, p)
+
+
+def test_open_gguf_refuses_before_allocating(lib, tmp_path):
+    """gh_granite_open_gguf checks the file and its configuration before any device work: a
+    missing file, a file without architecture keys and a dense (non-hybrid) model fail with
+    the reader's message and leave the output handle null."""
+    cases = [(str(tmp_path / "missing.gguf"), "cannot open")]
+    p1 = str(tmp_path / "noarch.gguf")
+    write(lib, p1, [], [("general.architecture", 8, "llama")])
+    cases.append((p1, "no architecture keys"))
+    p2 = str(tmp_path / "dense.gguf")
+    write(lib, p2, [], [m for m in HYBRID_META if m[0] != "ghassan.hybrid"] + [("ghassan.hybrid", 7, 0)])
+    cases.append((p2, "not a Granite hybrid"))
+    for path, msg in cases:
+        h = C.c_void_p(1)
+        rc = lib.gh_granite_open_gguf(path.encode(), 2, 64, C.byref(h))
+        assert rc != 0 and not h.value, path
+        assert msg in lib.gh_last_error().decode(), (path, lib.gh_last_error())
