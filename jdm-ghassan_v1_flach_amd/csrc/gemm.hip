@@ -591,26 +591,28 @@ __global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int
 }
 
 // ---------------------------------------------------------------- skinny
-// Small M (prefill of a short prompt), Q4_K, K = 256, 512 or 1024: a block takes 32
-// rows of x (fp32, converted to fp16 while staged into LDS) and 64 weight rows over
-// the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the
-// first multiply (one memory wait per block instead of one per K step, and no split-K
-// partials to add), wave w owns weight rows 16(w%4)..+15 over K range w/4 of NWK
-// (v_mfma_f32_16x16x32_f16, activations as A in two 16-row halves). Each output is
-// written (or added, with `accumulate`) by exactly one lane.
-template <int KK, int NWK>
-__global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
-                                                           float* __restrict__ Y, int M, int N, size_t rowb,
-                                                           int accumulate) {
+// Small M (prefill of a short prompt), Q4_K, K = 256, 512 or 1024: a block takes MT (16 or
+// 32) rows of x (fp32, converted to fp16 while staged into LDS) and 16*WR weight rows over
+// the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the first
+// multiply (one memory wait per block instead of one per K step, and no split-K partials in
+// HBM), wave w owns weight rows 16(w%WR)..+15 over K range w/WR of NWK
+// (v_mfma_f32_16x16x32_f16, activations as A in MT/16 16-row halves). The tile is chosen per
+// shape so that a launch spreads over the CUs (a short prompt has few 32x64 tiles). Each
+// output is written (or added, with `accumulate`) by exactly one lane.
+template <int KK, int NWK, int WR, int MT>
+__global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
+                                                               float* __restrict__ Y, int M, int N, size_t rowb,
+                                                               int accumulate) {
     // NWK wave groups split K: group kg takes k-steps kg*NS .. kg*NS + NS - 1; the groups'
     // sums meet in LDS and group 0 adds them in group order
-    constexpr int SA = KK + 8, NS = KK / 32 / NWK;
-    __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
-    __shared__ float sR[NWK > 1 ? (NWK - 1) * 4 * 64 * 8 : 1];
-    const int m0 = blockIdx.x * 32, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 3, kg = wave >> 2;
+    constexpr int SA = KK + 8, NS = KK / 32 / NWK, NT = 64 * WR * NWK, NW = WR * NWK, NH2 = MT / 16;
+    static_assert(NS >= 1 && (8 % NS == 0 || NS % 8 == 0), "K steps of a group stay within whole super-blocks");
+    __shared__ __attribute__((aligned(16))) _Float16 sA[MT * SA];
+    __shared__ float sR[NWK > 1 ? (NWK - 1) * WR * 64 * 4 * NH2 : 1];
+    const int m0 = blockIdx.x * MT, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave % WR, kg = wave / WR;
     const int col = lane & 15, kq = lane >> 4;
-    const int nrow = blockIdx.y * 64 + 16 * wr + col;
+    const int nrow = blockIdx.y * 16 * WR + 16 * wr + col;
     const bool nok = nrow < N;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * rowb;
     const int s0 = kg * NS;
@@ -622,28 +624,25 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
     for (int b = 0; b < NH; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)((s0 >> 3) + b) * 144);
 #pragma unroll
     for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
-    // 32 rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as
-    // k_to_f16_rows does (the row maxima first, one wave per group of rows)
+    // MT rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as
+    // k_to_f16_rows does (the row maxima first, one wave per row)
     constexpr int RQ = KK / 8;
-    __shared__ int sShift[32];
-    {
-        constexpr int NW = 4 * NWK, RPW = 32 / NW;  // rows per wave
-        for (int rr = 0; rr < RPW; ++rr) {
-            const int r = wave * RPW + rr;
-            float amax = 0.0f;
-            if (m0 + r < M) {
-                const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK);
-                for (int i = lane; i < KK / 4; i += 64) {
-                    const float4 v = src[i];
-                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                }
+    __shared__ int sShift[MT];
+    for (int r = wave; r < MT; r += NW) {
+        float amax = 0.0f;
+        if (m0 + r < M) {
+            const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK);
+#pragma unroll
+            for (int i = lane; i < KK / 4; i += 64) {
+                const float4 v = src[i];
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
             }
-            for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-            if (lane == 0) sShift[r] = f16_row_shift(amax);
         }
+        for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        if (lane == 0) sShift[r] = f16_row_shift(amax);
     }
     __syncthreads();
-    for (int e = tid; e < 32 * RQ; e += 256 * NWK) {
+    for (int e = tid; e < MT * RQ; e += NT) {
         const int r = e / RQ, c = e - r * RQ;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
         if (m0 + r < M) {
@@ -661,22 +660,24 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
     }
     __syncthreads();
     typedef float f32x4k __attribute__((ext_vector_type(4)));
-    f32x4k acc[2] = {f32x4k{0.f, 0.f, 0.f, 0.f}, f32x4k{0.f, 0.f, 0.f, 0.f}};
+    f32x4k acc[NH2];
+#pragma unroll
+    for (int h = 0; h < NH2; ++h) acc[h] = f32x4k{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int sg = s0 + s;
         const sk_f16x8 bv = sk_q4k_bfrag(hdr[NS >= 8 ? s >> 3 : 0], qb[s], sg & 7, nok);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NH2; ++h) {
             const sk_f16x8 av = *(const sk_f16x8*)(sA + (16 * h + col) * SA + 32 * sg + 8 * kq);
             acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
         }
     }
     if constexpr (NWK > 1) {
         if (kg > 0) {
-            float* r = sR + (((kg - 1) * 4 + wr) * 64 + lane) * 8;
+            float* r = sR + (((kg - 1) * WR + wr) * 64 + lane) * 4 * NH2;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < NH2; ++h)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) r[4 * h + j] = acc[h][j];
         }
@@ -684,16 +685,16 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
         if (kg > 0) return;
 #pragma unroll
         for (int g = 1; g < NWK; ++g) {
-            const float* r = sR + (((g - 1) * 4 + wr) * 64 + lane) * 8;
+            const float* r = sR + (((g - 1) * WR + wr) * 64 + lane) * 4 * NH2;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < NH2; ++h)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[h][j] += r[4 * h + j];
         }
     }
     if (!nok) return;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = m0 + 16 * h + 4 * kq + j;
@@ -705,18 +706,38 @@ __global__ void __launch_bounds__(256 * NWK) k_gemm_skinny(const float* __restri
         }
 }
 
-// Returns 1 if the skinny path took the product (Q4_K, K 256 / 512 / 1024, M <= 256).
+template <int KK, int NWK, int WR, int MT>
+static void skinny_launch(const float* x, const uint8_t* w, float* y, int M, int N, size_t rowb, int accumulate) {
+    hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT>), dim3(cdiv(M, MT), cdiv(N, 16 * WR)), dim3(64 * WR * NWK), 0,
+                       stream(), x, w, y, M, N, rowb, accumulate);
+}
+
+// Returns 1 if the skinny path took the product (Q4_K, K 256 / 512 / 1024, M <= 256). The
+// 32x64 tile when it already gives a CU-filling grid; otherwise 16-row tiles over 64, 32 or
+// 16 weight rows, the first of these that reaches 256 blocks (or the smallest), with the
+// waves freed from weight rows splitting K instead.
 static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate,
                        int* rc) {
     if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
-    const dim3 grid(cdiv(M, 32), cdiv(N, 64));
     const uint8_t* wb = (const uint8_t*)w;
-    if (K == 256)
-        hipLaunchKernelGGL((k_gemm_skinny<256, 2>), grid, dim3(512), 0, stream(), x, wb, y, M, N, rowb, accumulate);
-    else if (K == 512)
-        hipLaunchKernelGGL((k_gemm_skinny<512, 2>), grid, dim3(512), 0, stream(), x, wb, y, M, N, rowb, accumulate);
-    else
-        hipLaunchKernelGGL((k_gemm_skinny<1024, 4>), grid, dim3(1024), 0, stream(), x, wb, y, M, N, rowb, accumulate);
+    const int64_t b32 = (int64_t)cdiv(M, 32) * cdiv(N, 64), m16 = cdiv(M, 16);
+    int cfg = 0;  // 0: 32x64, 1: 16x64, 2: 16x32, 3: 16x16
+    if (b32 < 256) {
+        cfg = 3;
+        for (int c = 1; c <= 3; ++c)
+            if (m16 * cdiv(N, 64 >> (c - 1)) >= 256) { cfg = c; break; }
+    }
+#define GH_SKINNY(KK, NWK0)                                                                        \
+    switch (cfg) {                                                                                 \
+        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate); break;           \
+        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate); break;           \
+        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate); break;       \
+        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate); break;      \
+    }
+    if (K == 256) { GH_SKINNY(256, 2) }
+    else if (K == 512) { GH_SKINNY(512, 2) }
+    else { GH_SKINNY(1024, 4) }
+#undef GH_SKINNY
     GH_LAUNCHED("k_gemm_skinny");
     *rc = GH_OK;
     return 1;

@@ -64,7 +64,8 @@ def test_gemv_c2_full(gh, kind, M, K, N):
 
 
 @pytest.mark.parametrize("kind", [0, 1, 2, 3])
-@pytest.mark.parametrize("M,K,N", [(9, 256, 40), (128, 512, 256), (300, 1024, 200), (33, 1024, 130), (256, 512, 2192), (64, 256, 70)])
+@pytest.mark.parametrize("M,K,N", [(9, 256, 40), (128, 512, 256), (300, 1024, 200), (33, 1024, 130), (256, 512, 2192), (64, 256, 70),
+                                   (250, 1024, 1100), (200, 256, 1100), (128, 512, 2320)])
 def test_gemm_parity(gh, kind, M, K, N):
     w = _w(kind, N, K)
     x = O.rng_normal(9, M * K)
