@@ -693,15 +693,24 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
         }
     }
     if (!nok) return;
+    // with `accumulate`, every old value of the lane is loaded before the first store (the
+    // compiler cannot tell the rows apart, and would otherwise wait for each load in turn)
+    float old[NH2][4];
+#pragma unroll
+    for (int h = 0; h < NH2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + 16 * h + 4 * kq + j;
+            old[h][j] = accumulate && m < M ? Y[(size_t)m * N + nrow] : 0.f;
+        }
 #pragma unroll
     for (int h = 0; h < NH2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int m = m0 + 16 * h + 4 * kq + j;
             if (m < M) {
-                float* yp = Y + (size_t)m * N + nrow;
                 const float v = ldexpf(acc[h][j], -sShift[m - m0]);
-                *yp = accumulate ? *yp + v : v;
+                Y[(size_t)m * N + nrow] = accumulate ? old[h][j] + v : v;
             }
         }
 }

@@ -1058,28 +1058,33 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 // as in the 128-row kernel.
 typedef sk_f16x8 f16x8s;
 typedef float f32x4s __attribute__((ext_vector_type(4)));
-template <bool DUAL, int KK>
+template <bool DUAL, int KK, int WR>
 __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm P1, int ntiles0) {
     // blocks [0, ntiles0) take problem P0, the rest problem P1 (the shared expert beside the
     // routed ones in one launch)
     const bool second = (int)blockIdx.x >= ntiles0;
     const GroupGemm& P = second ? P1 : P0;
-    // two wave groups split K (steps kg*NS ..); group 1's sums meet group 0's in LDS
+    // WR waves own weight rows, 8 / WR wave groups split K (steps kg*NS ..); the groups' sums
+    // meet group 0's in LDS, added in group order. DUAL takes WR = 4 (gate rows in waves 0-1,
+    // up rows in 2-3); a plain product takes fewer weight-row waves when its grid is small.
+    static_assert(!DUAL || WR == 4, "gate/up tiles pair waves 0-1 with 2-3");
+    constexpr int NWK = 8 / WR;
     constexpr int SA = KK + 8;  // LDS row stride (fp16)
-    constexpr int NS = KK / 32 / 2;
+    constexpr int NS = KK / 32 / NWK;
+    static_assert(NS >= 1 && 8 % NS == 0, "a group's K steps stay within one super-block");
     __shared__ __attribute__((aligned(16))) _Float16 sA[32 * SA];
     __shared__ float sU[DUAL ? 32 * 33 : 1];
-    __shared__ float sR[4 * 64 * 8];
+    __shared__ float sR[(NWK - 1) * WR * 64 * 8];
     const int tile = second ? (int)blockIdx.x - ntiles0 : (int)blockIdx.x;
     const bool table = P.tiles != nullptr;
     if (table && tile >= P.tiles[0]) return;
     const int g = table ? P.tiles[1 + 2 * tile] : 0, m0 = table ? P.tiles[2 + 2 * tile] : 32 * tile;
     const int mend = table ? P.offsets[g + 1] : P.rows;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 3, kg = wave >> 2;
+    const int wr = wave % WR, kg = wave / WR;
     constexpr int K = KK;
     // weight row of this lane: DUAL waves 0-1 gate, 2-3 up rows of outputs n0 .. n0+31
-    const int NT = DUAL ? 32 : 64;
+    const int NT = DUAL ? 32 : 16 * WR;
     const int n0 = blockIdx.y * NT;
     if (n0 >= P.N) return;  // the other problem's output range is wider
     const int col = lane & 15, kq = lane >> 4;
@@ -1144,8 +1149,8 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
             acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[h], 0, 0, 0);
         }
     }
-    if (kg == 1) {
-        float* r = sR + (wr * 64 + lane) * 8;
+    if (kg > 0) {
+        float* r = sR + (((kg - 1) * WR + wr) * 64 + lane) * 8;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -1153,11 +1158,14 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
     }
     __syncthreads();
     if (kg == 0) {
-        const float* r = sR + (wr * 64 + lane) * 8;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int gk = 1; gk < NWK; ++gk) {
+            const float* r = sR + (((gk - 1) * WR + wr) * 64 + lane) * 8;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[h][j] += r[4 * h + j];
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[h][j] += r[4 * h + j];
+        }
     }
     // acc[h][j] of waves 0-3: row 16 h + 4 (lane / 16) + j, weight row column lane % 16
     if (DUAL) {
@@ -1181,6 +1189,35 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
                     }
                 }
         }
+    } else if (kg == 0 && comb) {
+        // the ordered combine of tokens m, output nrow: every load of the lane first (the routed
+        // outputs and the accumulated rows), then the stores, so the loads are not serialised
+        // behind stores the compiler cannot tell apart from them
+        float cyv[2][4][CKM], ov[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = m0 + 16 * h + 4 * kq + j;
+                const bool ok = m < mend && nok;
+#pragma unroll
+                for (int k = 0; k < CKM; ++k)
+                    cyv[h][j][k] = ok && k < P.cK ? P.cy[(size_t)cp[h][j][k] * P.N + nrow] : 0.f;
+                ov[h][j] = ok && P.caccum ? P.cout[(size_t)m * P.N + nrow] : 0.f;
+            }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = m0 + 16 * h + 4 * kq + j;
+                if (m < mend && nok) {
+                    float v = acc[h][j];
+#pragma unroll
+                    for (int k = 0; k < CKM; ++k)
+                        if (k < P.cK) v += cwv[h][j][k] * cyv[h][j][k];
+                    P.cout[(size_t)m * P.N + nrow] = P.caccum ? ov[h][j] + v : v;
+                }
+            }
     } else if (kg == 0) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -1188,14 +1225,7 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
             for (int j = 0; j < 4; ++j) {
                 const int m = m0 + 16 * h + 4 * kq + j;
                 if (m < mend && nok) {
-                    if (comb) {  // the ordered combine of token m, output nrow
-                        float v = acc[h][j];
-#pragma unroll
-                        for (int k = 0; k < CKM; ++k)
-                            if (k < P.cK) v += cwv[h][j][k] * P.cy[(size_t)cp[h][j][k] * P.N + nrow];
-                        float* o = P.cout + (size_t)m * P.N + nrow;
-                        *o = P.caccum ? *o + v : v;
-                    } else if (P.cout) {  // more than CKM experts per token
+                    if (P.cout) {  // more than CKM experts per token
                         float v = acc[h][j];
                         for (int k = 0; k < P.cK; ++k) {
                             const int sl = m * P.cK + k;
@@ -1211,15 +1241,38 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
     }
 }
 
-// the skinny kernel for K = 256 or 512 (the caller checks K); grid (tiles, outputs / 32 or 64)
-// P1 (optional, ntiles1 blocks) runs in the same launch after P0's ntiles0; both take the same K
+// the skinny kernel for K = 256 or 512 (the caller checks K); grid (tiles, outputs / 32 or
+// 16 WR). P1 (optional, ntiles1 blocks) runs in the same launch after P0's ntiles0; both take
+// the same K. A plain product takes 64, 32 or 16 weight rows per block: the first that gives
+// 256 blocks, or 16.
+template <int KK, int WR, bool DUAL>
+static void skinny_go(dim3 grid, const GroupGemm& P0, const GroupGemm& Q1, int ntiles0) {
+    hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, KK, WR>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
+}
 template <bool DUAL>
 static void launch_skinny(const GroupGemm& P0, int ntiles0, const GroupGemm* P1 = nullptr, int ntiles1 = 0) {
     const int nw = std::max(P0.N, P1 ? P1->N : 0);
-    const dim3 grid(ntiles0 + ntiles1, DUAL ? cdiv(nw, 32) : cdiv(nw, 64));
     const GroupGemm Q1 = P1 ? *P1 : GroupGemm{};
-    if (P0.K == 256) hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 256>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
-    else hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, 512>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
+    const int nt = ntiles0 + ntiles1;
+    if constexpr (DUAL) {
+        const dim3 grid(nt, cdiv(nw, 32));
+        if (P0.K == 256) skinny_go<256, 4, true>(grid, P0, Q1, ntiles0);
+        else skinny_go<512, 4, true>(grid, P0, Q1, ntiles0);
+    } else {
+        int wr = 1;
+        for (int c = 4; c >= 2; c >>= 1)
+            if ((int64_t)nt * cdiv(nw, 16 * c) >= 256) { wr = c; break; }
+        const dim3 grid(nt, cdiv(nw, 16 * wr));
+        if (P0.K == 256) {
+            if (wr == 4) skinny_go<256, 4, false>(grid, P0, Q1, ntiles0);
+            else if (wr == 2) skinny_go<256, 2, false>(grid, P0, Q1, ntiles0);
+            else skinny_go<256, 1, false>(grid, P0, Q1, ntiles0);
+        } else {
+            if (wr == 4) skinny_go<512, 4, false>(grid, P0, Q1, ntiles0);
+            else if (wr == 2) skinny_go<512, 2, false>(grid, P0, Q1, ntiles0);
+            else skinny_go<512, 1, false>(grid, P0, Q1, ntiles0);
+        }
+    }
 }
 
 // tile table of one group covering rows [0, N)
