@@ -346,22 +346,42 @@ __global__ void __launch_bounds__(256) k_ssd_state_cb(const float* __restrict__ 
     float* out = dS + ((size_t)c * H + h) * P * N;
     const float dec = expf(cend);
     // a single chunk (state != null): the inter-chunk pass of this head runs here, with
-    // k_ssd_state_pass's arithmetic: S_in = state (fp16 for the outputs), state = state dec + dS
+    // k_ssd_state_pass's arithmetic: S_in = state (fp16 for the outputs), state = state dec + dS.
+    // Every state value of the lane is loaded before the first store (the compiler cannot tell
+    // the stores from the later loads, and would otherwise wait for each load in turn).
+    if (state) {
+        float sv[TPW][16];
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        const int tile = wave * TPW + i;
-        const int pt = tile % (P / 32), nt = tile / (P / 32);
+        for (int i = 0; i < TPW; ++i) {
+            const int tile = wave * TPW + i;
+            const int pt = tile % (P / 32), nt = tile / (P / 32);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            const int n = nt * 32 + (lane & 31);
-            if (state) {
-                const size_t si = ((size_t)h * P + p) * N + n;
-                const float s0 = state[si];
-                Sin16[si] = (_Float16)s0;
-                state[si] = s0 * dec + acc[i][e];
-            } else {
-                out[(size_t)p * N + n] = acc[i][e];
+            for (int e = 0; e < 16; ++e) {
+                const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                sv[i][e] = state[((size_t)h * P + p) * N + nt * 32 + (lane & 31)];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+            const int tile = wave * TPW + i;
+            const int pt = tile % (P / 32), nt = tile / (P / 32);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const size_t si = ((size_t)h * P + p) * N + nt * 32 + (lane & 31);
+                Sin16[si] = (_Float16)sv[i][e];
+                state[si] = sv[i][e] * dec + acc[i][e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TPW; ++i) {
+            const int tile = wave * TPW + i;
+            const int pt = tile % (P / 32), nt = tile / (P / 32);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int p = pt * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                out[(size_t)p * N + nt * 32 + (lane & 31)] = acc[i][e];
             }
         }
     }
