@@ -153,7 +153,7 @@ def kernel_suite(gh):
                                10 if M > 8 else 200)
             tag = f"c2_{kname}_M{M}_{N}x{K}"
             if M <= 8:
-                g8 = "k_gemv8_q4k" if kind == 3 else "k_gemv8_q8"
+                g8 = "k_gemv8<Q4_K>" if kind == 3 else "k_gemv8<Q8_0>"
                 kern = ("k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else
                         "k_gemv_q4k_i8 (4 K slices) + k_g8_sum" if (kind == 3 and M == 1) else
                         "k_gemv_q4k_i8<Q8> (2 / 7 K slices) + k_g8_sum" if M == 1 else

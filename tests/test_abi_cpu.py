@@ -82,7 +82,7 @@ def test_m0_only_set_for_lds_transfers(tmp_path):
     import re
     import subprocess
     src = os.path.join(os.path.dirname(gh.LIB_PATH), "csrc")
-    for f in ("gemv_mfma", "attention", "gemm", "decode_persistent"):
+    for f in ("gemv_mfma", "gemv8", "attention", "gemm", "decode_persistent"):
         out = tmp_path / (f + ".s")
         subprocess.run(["/opt/rocm/bin/hipcc", "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-Xclang",
                         "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",

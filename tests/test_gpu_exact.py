@@ -38,7 +38,7 @@ def test_gemv_c2_vs_exact(gh, kind, M, K, N):
     x = O.rng_normal(8, M * K)
     got = _run_linear(gh, x, w, M, K, N, kind)
     if M > 1:
-        # the batched GEMVs (k_gemv8_q4k / k_gemv8_q8) decode each weight to fp16, as the
+        # the batched GEMV (k_gemv8, both kinds) decode each weight to fp16, as the
         # reference's quant_materialize does: their exact product is the one over those weights
         W16 = O.f16_to_f32(O.materialize(kind, w, N * K)).astype(np.float64).reshape(N, K)
         y64 = x.reshape(M, K).astype(np.float64) @ W16.T
