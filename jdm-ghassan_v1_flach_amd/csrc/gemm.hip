@@ -591,6 +591,28 @@ __global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int
 }
 
 // ---------------------------------------------------------------- skinny
+// Row prologues of the skinny GEMM (the row is normalised while it is staged, so the norm
+// takes no launch of its own):
+//  SK_RMSNORM:  x * inv * w with inv = 1 / sqrt(mean(x^2) + eps) in double, the sum of squares
+//               in double (elementwise.hip k_rmsnorm, core/math_cpu.cpp rmsnorm);
+//  SK_GATENORM: rows already gated (v = y * silu(z), applied by the SSD scan's stores), then
+//               v * inv * w with inv = 1 / sqrtf(mean(v^2) + eps) in float (mamba.hip
+//               k_gated_norm, the Mamba-2 gated RMSNorm before out_proj).
+enum { SK_PLAIN = 0, SK_RMSNORM = 1, SK_GATENORM = 2 };
+struct SkPro {
+    const float* nw;  // norm weight (K values)
+    float eps;
+};
+template <int PRO>
+__device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
+    if constexpr (PRO == SK_RMSNORM) {
+        const double invd = 1.0 / sqrt(ss / (double)n + (double)eps);
+        return isfinite(invd) ? (float)invd : 0.0f;
+    } else {
+        return 1.0f / sqrtf((float)(ss / (double)n) + eps);
+    }
+}
+
 // Small M (prefill of a short prompt), Q4_K, K = 256, 512 or 1024: a block takes MT (16 or
 // 32) rows of x (fp32, converted to fp16 while staged into LDS) and 16*WR weight rows over
 // the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the first
@@ -599,10 +621,10 @@ __global__ void k_add_to(float* __restrict__ y, const float* __restrict__ t, int
 // (v_mfma_f32_16x16x32_f16, activations as A in MT/16 16-row halves). The tile is chosen per
 // shape so that a launch spreads over the CUs (a short prompt has few 32x64 tiles). Each
 // output is written (or added, with `accumulate`) by exactly one lane.
-template <int KK, int NWK, int WR, int MT>
+template <int KK, int NWK, int WR, int MT, int PRO = SK_PLAIN>
 __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
                                                                float* __restrict__ Y, int M, int N, size_t rowb,
-                                                               int accumulate) {
+                                                               int accumulate, SkPro pro) {
     // NWK wave groups split K: group kg takes k-steps kg*NS .. kg*NS + NS - 1; the groups'
     // sums meet in LDS and group 0 adds them in group order
     constexpr int SA = KK + 8, NS = KK / 32 / NWK, NT = 64 * WR * NWK, NW = WR * NWK, NH2 = MT / 16;
@@ -625,40 +647,82 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
 #pragma unroll
     for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
     // MT rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as
-    // k_to_f16_rows does (the row maxima first, one wave per row)
+    // k_to_f16_rows does (the row maxima first, one wave per row). With a row prologue the
+    // staged values are the normalised rows.
     constexpr int RQ = KK / 8;
     __shared__ int sShift[MT];
-    for (int r = wave; r < MT; r += NW) {
-        float amax = 0.0f;
-        if (m0 + r < M) {
-            const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK);
+    if constexpr (PRO != SK_PLAIN) {
+        // one wave per row: the row's values stay in registers (4 per lane per float4), its norm,
+        // maximum and fp16 copy are formed from them
+        constexpr int U = KK / 256;  // float4 per lane
+        for (int r = wave; r < MT; r += NW) {
+            float4 v[U];
+            double ss = 0.0;
 #pragma unroll
-            for (int i = lane; i < KK / 4; i += 64) {
-                const float4 v = src[i];
-                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            for (int u = 0; u < U; ++u) {
+                v[u] = m0 + r < M ? ((const float4*)(X + (size_t)(m0 + r) * KK))[lane + 64 * u]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+                ss += (double)v[u].x * v[u].x + (double)v[u].y * v[u].y + (double)v[u].z * v[u].z +
+                      (double)v[u].w * v[u].w;
+            }
+            ss = wave_sum(ss);
+            const float inv = sk_inv<PRO>(ss, KK, pro.eps);
+            float amax = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float4 w = ((const float4*)pro.nw)[lane + 64 * u];
+                v[u].x = v[u].x * inv * w.x;
+                v[u].y = v[u].y * inv * w.y;
+                v[u].z = v[u].z * inv * w.z;
+                v[u].w = v[u].w * inv * w.w;
+                amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+            }
+            for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            const int sh = f16_row_shift(amax);
+            if (lane == 0) sShift[r] = sh;
+            typedef _Float16 sk_f16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                sk_f16x4 h;
+                h[0] = (_Float16)ldexpf(v[u].x, sh); h[1] = (_Float16)ldexpf(v[u].y, sh);
+                h[2] = (_Float16)ldexpf(v[u].z, sh); h[3] = (_Float16)ldexpf(v[u].w, sh);
+                *(sk_f16x4*)(sA + r * SA + 4 * (lane + 64 * u)) = h;
             }
         }
-        for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-        if (lane == 0) sShift[r] = f16_row_shift(amax);
-    }
-    __syncthreads();
-    for (int e = tid; e < MT * RQ; e += NT) {
-        const int r = e / RQ, c = e - r * RQ;
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-        if (m0 + r < M) {
-            const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK + 8 * c);
-            a = src[0];
-            b = src[1];
+        __syncthreads();
+    } else {
+        for (int r = wave; r < MT; r += NW) {
+            float amax = 0.0f;
+            if (m0 + r < M) {
+                const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK);
+#pragma unroll
+                for (int i = lane; i < KK / 4; i += 64) {
+                    const float4 v = src[i];
+                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                }
+            }
+            for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            if (lane == 0) sShift[r] = f16_row_shift(amax);
         }
-        const int sh = sShift[r];
-        sk_f16x8 h;
-        h[0] = (_Float16)ldexpf(a.x, sh); h[1] = (_Float16)ldexpf(a.y, sh);
-        h[2] = (_Float16)ldexpf(a.z, sh); h[3] = (_Float16)ldexpf(a.w, sh);
-        h[4] = (_Float16)ldexpf(b.x, sh); h[5] = (_Float16)ldexpf(b.y, sh);
-        h[6] = (_Float16)ldexpf(b.z, sh); h[7] = (_Float16)ldexpf(b.w, sh);
-        *(sk_f16x8*)(sA + r * SA + 8 * c) = h;
+        __syncthreads();
+        for (int e = tid; e < MT * RQ; e += NT) {
+            const int r = e / RQ, c = e - r * RQ;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (m0 + r < M) {
+                const float4* src = (const float4*)(X + (size_t)(m0 + r) * KK + 8 * c);
+                a = src[0];
+                b = src[1];
+            }
+            const int sh = sShift[r];
+            sk_f16x8 h;
+            h[0] = (_Float16)ldexpf(a.x, sh); h[1] = (_Float16)ldexpf(a.y, sh);
+            h[2] = (_Float16)ldexpf(a.z, sh); h[3] = (_Float16)ldexpf(a.w, sh);
+            h[4] = (_Float16)ldexpf(b.x, sh); h[5] = (_Float16)ldexpf(b.y, sh);
+            h[6] = (_Float16)ldexpf(b.z, sh); h[7] = (_Float16)ldexpf(b.w, sh);
+            *(sk_f16x8*)(sA + r * SA + 8 * c) = h;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     typedef float f32x4k __attribute__((ext_vector_type(4)));
     f32x4k acc[NH2];
 #pragma unroll
@@ -716,17 +780,32 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
 }
 
 template <int KK, int NWK, int WR, int MT>
-static void skinny_launch(const float* x, const uint8_t* w, float* y, int M, int N, size_t rowb, int accumulate) {
-    hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT>), dim3(cdiv(M, MT), cdiv(N, 16 * WR)), dim3(64 * WR * NWK), 0,
-                       stream(), x, w, y, M, N, rowb, accumulate);
+static void skinny_launch(const float* x, const uint8_t* w, float* y, int M, int N, size_t rowb, int accumulate,
+                          int mode, const SkPro& pro) {
+    const dim3 grid(cdiv(M, MT), cdiv(N, 16 * WR)), blk(64 * WR * NWK);
+    if (mode == SK_RMSNORM)
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_RMSNORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+                           accumulate, pro);
+    else if (mode == SK_GATENORM)
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_GATENORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+                           accumulate, pro);
+    else
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_PLAIN>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+                           accumulate, pro);
+}
+
+// Whether the skinny path takes a product of linear_any / linear_acc: Q4_K, K 256 / 512 / 1024,
+// 8 < M <= 256 rows (smaller M go to the GEMVs), 16-byte aligned x and W.
+bool skinny_takes(const void* x, const void* w, int M, int K, int kind) {
+    return kind == 3 && M > 8 && M <= 256 && (K == 256 || K == 512 || K == 1024) && !(((uintptr_t)x | (uintptr_t)w) & 15);
 }
 
 // Returns 1 if the skinny path took the product (Q4_K, K 256 / 512 / 1024, M <= 256). The
 // 32x64 tile when it already gives a CU-filling grid; otherwise 16-row tiles over 64, 32 or
 // 16 weight rows, the first of these that reaches 256 blocks (or the smallest), with the
-// waves freed from weight rows splitting K instead.
+// waves freed from weight rows splitting K instead. `mode` / `pro`: the row prologue.
 static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate,
-                       int* rc) {
+                       int* rc, int mode = SK_PLAIN, const SkPro& pro = SkPro{}) {
     if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
     const uint8_t* wb = (const uint8_t*)w;
     const int64_t b32 = (int64_t)cdiv(M, 32) * cdiv(N, 64), m16 = cdiv(M, 16);
@@ -736,12 +815,12 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
         for (int c = 1; c <= 3; ++c)
             if (m16 * cdiv(N, 64 >> (c - 1)) >= 256) { cfg = c; break; }
     }
-#define GH_SKINNY(KK, NWK0)                                                                        \
-    switch (cfg) {                                                                                 \
-        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate); break;           \
-        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate); break;           \
-        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate); break;       \
-        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate); break;      \
+#define GH_SKINNY(KK, NWK0)                                                                                     \
+    switch (cfg) {                                                                                              \
+        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;             \
+        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;             \
+        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;         \
+        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;        \
     }
     if (K == 256) { GH_SKINNY(256, 2) }
     else if (K == 512) { GH_SKINNY(512, 2) }
@@ -750,6 +829,19 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
     GH_LAUNCHED("k_gemm_skinny");
     *rc = GH_OK;
     return 1;
+}
+
+// Normalised-input product on the skinny path: y (+)= norm(x) W^T with the norm as the GEMM's
+// row prologue (mode SK_RMSNORM or SK_GATENORM, x rows of K values). Returns GH_EUNSUPPORTED,
+// launching nothing, where the skinny path does not take the shape (skinny_takes false) or the
+// norm weights are not 16-byte aligned.
+int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, const void* w, float* y, int M, int K,
+                       int N, int kind, int accumulate) {
+    if (!skinny_takes(x, w, M, K, kind) || ((uintptr_t)nw & 15)) return GH_EUNSUPPORTED;
+    SkPro pro{nw, eps};
+    int rc = GH_OK;
+    if (!gemm_skinny(x, w, y, M, K, N, row_bytes(kind, K), accumulate, &rc, mode, pro)) return GH_EUNSUPPORTED;
+    return rc;
 }
 
 // y = x W^T, or y += x W^T with `accumulate` (the split-K sum adds in place; the other paths

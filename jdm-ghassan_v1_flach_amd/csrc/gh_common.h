@@ -241,5 +241,6 @@ enum WsSlot {
     WS_PEN_HIST = 39,   // device copy of the penalty history
     WS_GEMM_W16 = 40,   // large-M prefill: the weights decoded to bf16 for the library GEMM
     WS_BLASLT = 41,     // hipBLASLt workspace
+    WS_MAMBA_XN = 42,   // prefill: the RMS-normalised Mamba input where no GEMM prologue takes the norm
 };
 }  // namespace gh

@@ -39,7 +39,10 @@ int attn_decode_devctl(const float* q, const uint16_t* kc, const uint16_t* vc, f
 int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
                        const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
                        float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
-                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate);
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate,
+                       const float* pre_nw, float pre_eps);
+int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, const void* w, float* y, int M, int K,
+                       int N, int kind, int accumulate);  // gemm.hip
 int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
 
 // decode control block (device ints)
@@ -835,25 +838,39 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
     const bool acc = g->res_mult == 1.0f;
     for (int l = 0; l < g->L; ++l) {
         const std::string pre = "layers." + std::to_string(l) + ".";
-        GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, P, d, g->eps));
+        // the layer's input norm: on the row prologue of the projections that read it where the
+        // skinny GEMM takes them, else one k_rmsnorm launch into xb (made at most once)
+        bool xb_made = false;
+        auto make_xb = [&]() -> int {
+            if (!xb_made) GHC(gh_rmsnorm_forward(g->x, g->F(pre + "attn_norm"), g->xb, nullptr, P, d, g->eps));
+            xb_made = true;
+            return GH_OK;
+        };
+        auto proj_normed = [&](const void* w, float* y, int N) -> int {
+            const int rc = linear_norm_skinny(g->x, 1, g->F(pre + "attn_norm"), g->eps, w, y, P, d, N, g->qkind, 0);
+            if (rc != GH_EUNSUPPORTED) return rc;
+            GHC(make_xb());
+            return linear_any(g->xb, w, y, P, d, N, g->qkind);
+        };
         if (g->lt[l] == 0) {
             if (mamba_mode == 0) {
+                GHC(make_xb());
                 // token by token, the reference's order (inference/generator.cpp:743-760)
                 for (int t = 0; t < P; ++t) GHC(mamba_step(g, l, g->xb + (size_t)t * d, g->pr + (size_t)t * d));
             } else {
                 const std::string mp = pre + "mamba.";
                 // the residual add is folded into out_proj (x += ...)
-                GHC(mamba_forward_impl(g->xb, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
+                GHC(mamba_forward_impl(g->x, g->W(mp + "in_proj"), g->F(mp + "conv1d.weight"),
                                        g->F(mp + "conv1d.bias"), g->F(mp + "dt_bias"), g->F(mp + "A_log"),
                                        g->F(mp + "D"), g->F(mp + "norm.weight"), g->W(mp + "out_proj"), g->ssm[l],
                                        g->conv[l], acc ? g->x : g->pr, P, d, g->di, g->conv_dim, g->mh, g->mdh,
-                                       g->mds, g->ck, g->eps, g->qkind, acc));
+                                       g->mds, g->ck, g->eps, g->qkind, acc, g->F(pre + "attn_norm"), g->eps));
                 if (!acc) GHC(add_branch(g, g->pr, (int64_t)P * d));
             }
         } else {
-            GHC(linear_any(g->xb, g->W(pre + "wq"), g->q, P, d, g->qd, g->qkind));
-            GHC(linear_any(g->xb, g->W(pre + "wk"), g->k, P, d, g->kvd, g->qkind));
-            GHC(linear_any(g->xb, g->W(pre + "wv"), g->v, P, d, g->kvd, g->qkind));
+            GHC(proj_normed(g->W(pre + "wq"), g->q, g->qd));
+            GHC(proj_normed(g->W(pre + "wk"), g->k, g->kvd));
+            GHC(proj_normed(g->W(pre + "wv"), g->v, g->kvd));
             GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
             GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
             GHC(attention_prefill(g->q, g->k, g->v, g->att, 1, P, g->H, g->KV, g->hd, g->scale, 0));

@@ -25,6 +25,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 int linear_any(const float* x, const void* w, float* y, int M, int K, int N, int kind);
 int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
+// gemm.hip: y (+)= norm(x) W^T with the norm on the skinny GEMM's row prologue; mode 1 RMSNorm
+// (k_rmsnorm), 2 the RMS norm of already gated rows (k_gated_norm's second half);
+// GH_EUNSUPPORTED (nothing launched) off that path, which skinny_takes tells beforehand
+int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, const void* w, float* y, int M, int K,
+                       int N, int kind, int accumulate);
+bool skinny_takes(const void* x, const void* w, int M, int K, int kind);
 
 __device__ __forceinline__ float softplus_ref(float v) {
     // core/mamba_cpu.cpp:139-140 (identity above 20)
@@ -436,12 +442,13 @@ __global__ void __launch_bounds__(256) k_ssd_state_pass(float* __restrict__ stat
 // step) and are weighted in registers. Wave w owns the 32-row block w (32 t rows x 32 p, one
 // 32x32 MFMA tile, fp32 accumulation). The decay factor is split per 16-position step (one
 // exponential per row and step rather than per element).
-template <int N>
+template <int N, bool GATE = false>
 __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, int ldx,
                                                  const _Float16* __restrict__ C16, const _Float16* __restrict__ G,
                                                  const float* __restrict__ W, const int* __restrict__ F,
                                                  const _Float16* __restrict__ Sin16, const float* __restrict__ D,
-                                                 float* __restrict__ y, int ldy, int T, int H, int L) {
+                                                 float* __restrict__ y, int ldy, int T, int H, int L,
+                                                 const float* __restrict__ gate, int ldg) {
     constexpr int P = 64, PH = 32, PN = P * N, SX = 256 + 8, SS = N + 8, SD = PH + 4;
     __shared__ __attribute__((aligned(16))) _Float16 sXt[PH * SX];
     __shared__ __attribute__((aligned(16))) _Float16 sS[PH * SS];
@@ -480,6 +487,15 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
     const int t = 32 * rb + col;        // this lane's A row (chunk-local)
     const bool trow = t < len;
     const int nk = 2 * (rb + 1);        // 16-wide tau steps of the causal range
+    // the gate values of this lane's outputs (see the stores), requested first
+    float zv[GATE ? 16 : 1];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int tl = 32 * rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            zv[e] = tl < len ? gate[(size_t)(t0 + tl) * ldg + h * P + pc0 + col] : 0.f;
+        }
+    }
 
     // ---- this wave's C fragments and the first 8 G fragments of its causal range, requested first
     f16x8 craw[N / 16], graw[8];
@@ -607,7 +623,19 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
             mma(a, tau0);
         }
     }
-    // + D x, store. acc element e: t row 32 rb + 8(e/4) + 4(lane/32) + e%4, p col pc0 + lane%32
+    // + D x, store. acc element e: t row 32 rb + 8(e/4) + 4(lane/32) + e%4, p col pc0 + lane%32.
+    // With `gate`, the stored value is the gated one, y * silu(z) (the first step of the Mamba-2
+    // gated norm, mamba.hip k_gated_norm's arithmetic), z = gate[t][h P + p].
+    if constexpr (GATE) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int tl = 32 * rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (tl < len)
+                y[(size_t)(t0 + tl) * ldy + h * P + pc0 + col] =
+                    (acc[e] + sDx[tl * SD + col]) * (zv[e] / (1.0f + expf(-zv[e])));
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int tl = 32 * rb + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
@@ -618,7 +646,7 @@ __global__ void __launch_bounds__(512) k_ssd_out(const float* __restrict__ xs, i
 // Runs the chunked scan over rows [0, T) of one sequence.
 static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, int ldbc, const float* dt_raw, int dt_ld,
                    const float* dt_bias, const float* A, const float* a_log, const float* D, float* state, float* y,
-                   int ldy, int T, int H, int P, int N, int L) {
+                   int ldy, int T, int H, int P, int N, int L, const float* gate = nullptr, int ldg = 0) {
     GH_REQUIRE(P == 64, "ssd scan: head_dim %d (the kernels are built for 64)", P);
     GH_REQUIRE(N == 64 || N == 128, "ssd scan: d_state %d (64 or 128)", N);
     GH_REQUIRE(L >= 64 && L <= 256 && L % 64 == 0, "ssd scan: chunk %d (64..256, multiple of 64)", L);
@@ -649,16 +677,24 @@ static int ssd_run(const float* xs, int ldx, const float* Bm, const float* Cm, i
         if (!one)
             hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
                                (int)PN);
-        hipLaunchKernelGGL(k_ssd_out<128>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, W, F,
-                           Sin16, D, y, ldy, T, H, L);
+        if (gate)
+            hipLaunchKernelGGL((k_ssd_out<128, true>), dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs,
+                               ldx, C16, G, W, F, Sin16, D, y, ldy, T, H, L, gate, ldg);
+        else
+            hipLaunchKernelGGL((k_ssd_out<128, false>), dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs,
+                               ldx, C16, G, W, F, Sin16, D, y, ldy, T, H, L, nullptr, 0);
     } else {
         hipLaunchKernelGGL(k_ssd_state_cb<64>, dim3(nb1), dim3(256), 0, stream(), xs, ldx, Bm, Cm, ldbc, dt_raw, dt_ld,
                            dt_bias, A, a_log, W, F, G, C16, dS, decay, T, H, L, one ? state : nullptr, Sin16);
         if (!one)
             hipLaunchKernelGGL(k_ssd_state_pass, dim3(nbp), dim3(256), 0, stream(), state, dS, decay, Sin16, nch, H,
                                (int)PN);
-        hipLaunchKernelGGL(k_ssd_out<64>, dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs, ldx, C16, G, W, F,
-                           Sin16, D, y, ldy, T, H, L);
+        if (gate)
+            hipLaunchKernelGGL((k_ssd_out<64, true>), dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs,
+                               ldx, C16, G, W, F, Sin16, D, y, ldy, T, H, L, gate, ldg);
+        else
+            hipLaunchKernelGGL((k_ssd_out<64, false>), dim3((unsigned)(2 * cdiv(nch * H, 8) * 8)), dim3(512), 0, stream(), xs,
+                               ldx, C16, G, W, F, Sin16, D, y, ldy, T, H, L, nullptr, 0);
     }
     GH_LAUNCHED("k_ssd_*");
     return GH_OK;
@@ -750,10 +786,13 @@ __global__ void __launch_bounds__(256) k_step_scan(const float* __restrict__ xbc
 // One sequence of T tokens: in_proj, conv1d (+ optionally the conv window
 // left for decode), chunked scan, gated norm, out_proj. kind 0-3 packed,
 // 4 fp16 weights.
+// pre_nw: x is first RMS-normalised with these weights (eps pre_eps), on the in_proj GEMM's row
+// prologue where the skinny path takes it, else by one k_rmsnorm launch; null: x is used as is.
 int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, const float* conv_b,
                        const float* dt_bias, const float* a_log, const float* D, const float* norm_w, const void* w_out,
                        float* state, float* conv_state, float* out, int T, int d, int d_inner, int conv_dim,
-                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate) {
+                       int n_heads, int d_head, int d_state, int k, float eps, int kind, bool accumulate,
+                       const float* pre_nw, float pre_eps) {
     GH_REQUIRE(conv_dim - d_inner == 2 * d_state, "mamba: inconsistent conv_dim / d_state (n_groups must be 1)");
     GH_REQUIRE(n_heads * d_head == d_inner, "mamba: n_heads * d_head != d_inner");
     const int proj = d_inner + conv_dim + n_heads;
@@ -762,14 +801,30 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
     float* yb = (float*)workspace(WS_MAMBA_Y, (size_t)T * d_inner * 4 * 2);
     if (!pr || !xbc || !yb) return fail(GH_ENOMEM, "mamba: workspace");
     float* normed = yb + (size_t)T * d_inner;
-    int rc = linear_any(x, w_in, pr, T, d, proj, kind);
+    int rc = GH_EUNSUPPORTED;
+    if (pre_nw) {
+        rc = linear_norm_skinny(x, 1, pre_nw, pre_eps, w_in, pr, T, d, proj, kind, 0);
+        if (rc == GH_EUNSUPPORTED) {  // the norm as its own launch, into the (later) gated-norm rows
+            float* xn = (float*)workspace(WS_MAMBA_XN, (size_t)T * d * 4);
+            if (!xn) return fail(GH_ENOMEM, "mamba: workspace");
+            rc = gh_rmsnorm_forward(x, pre_nw, xn, nullptr, T, d, pre_eps);
+            if (!rc) rc = linear_any(xn, w_in, pr, T, d, proj, kind);
+        }
+    } else {
+        rc = linear_any(x, w_in, pr, T, d, proj, kind);
+    }
     if (rc) return rc;
     hipLaunchKernelGGL(k_conv1d, dim3(cdiv(conv_dim, 256), T), dim3(256), 0, stream(), pr, proj, d_inner, conv_w,
                        conv_b, xbc, 1, T, conv_dim, k, conv_state);
     GH_LAUNCHED("k_conv1d");
+    // where the skinny GEMM takes out_proj, the scan's stores apply the gate (y * silu(z)) and the
+    // GEMM's row prologue the RMS norm; otherwise k_gated_norm does both as its own launch
+    const bool gate_fused = skinny_takes(yb, w_out, T, d_inner, kind) && ((uintptr_t)norm_w & 15) == 0;
     rc = ssd_run(xbc, conv_dim, xbc + d_inner, xbc + d_inner + d_state, conv_dim, pr + d_inner + conv_dim, proj,
-                 dt_bias, nullptr, a_log, D, state, yb, d_inner, T, n_heads, d_head, d_state, 256);
+                 dt_bias, nullptr, a_log, D, state, yb, d_inner, T, n_heads, d_head, d_state, 256,
+                 gate_fused ? pr : nullptr, proj);
     if (rc) return rc;
+    if (gate_fused) return linear_norm_skinny(yb, 2, norm_w, eps, w_out, out, T, d_inner, d, kind, accumulate ? 1 : 0);
     hipLaunchKernelGGL(k_gated_norm, dim3(T), dim3(256), 0, stream(), yb, d_inner, pr, proj, norm_w, normed, d_inner,
                        eps);
     GH_LAUNCHED("k_gated_norm");
@@ -863,7 +918,8 @@ int gh_mamba2_forward_half(const float* x, const void* w_in, const float* conv_w
     for (int b = 0; b < B; ++b) {
         int rc = mamba_forward_impl(x + (size_t)b * T * d, w_in, conv_w, conv_b, dt_bias, a_log, D, norm_w, w_out,
                                     state + (size_t)b * n_heads * d_head * d_state, nullptr, out + (size_t)b * T * d,
-                                    T, d, d_inner, conv_dim, n_heads, d_head, d_state, k, eps, kind, false);
+                                    T, d, d_inner, conv_dim, n_heads, d_head, d_state, k, eps, kind, false,
+                                    nullptr, 0.0f);
         if (rc) return rc;
     }
     return GH_OK;
