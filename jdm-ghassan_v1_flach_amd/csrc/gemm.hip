@@ -603,6 +603,17 @@ struct SkPro {
     const float* nw;  // norm weight (K values)
     float eps;
 };
+// Up to three products of the same rows in one launch (the attention q / k / v projections):
+// output rows [off[s], off[s + 1]) of the grid belong to segment s (weights w[s], outputs y[s]
+// of n[s] columns; y16[s], if set, takes an fp16 copy of them, the KV cache's copy). Each
+// segment is a whole number of the launch's weight-row tiles. n = 0 segments: one product.
+struct SkSeg {
+    const uint8_t* w[3];
+    float* y[3];
+    uint16_t* y16[3];
+    int off[4];
+    int nseg;
+};
 template <int PRO>
 __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
     if constexpr (PRO == SK_RMSNORM) {
@@ -624,7 +635,7 @@ __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
 template <int KK, int NWK, int WR, int MT, int PRO = SK_PLAIN>
 __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
                                                                float* __restrict__ Y, int M, int N, size_t rowb,
-                                                               int accumulate, SkPro pro) {
+                                                               int accumulate, SkPro pro, SkSeg seg) {
     // NWK wave groups split K: group kg takes k-steps kg*NS .. kg*NS + NS - 1; the groups'
     // sums meet in LDS and group 0 adds them in group order
     constexpr int SA = KK + 8, NS = KK / 32 / NWK, NT = 64 * WR * NWK, NW = WR * NWK, NH2 = MT / 16;
@@ -634,7 +645,17 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
     const int m0 = blockIdx.x * MT, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wr = wave % WR, kg = wave / WR;
     const int col = lane & 15, kq = lane >> 4;
-    const int nrow = blockIdx.y * 16 * WR + 16 * wr + col;
+    int nrow = blockIdx.y * 16 * WR + 16 * wr + col;
+    uint16_t* Y16 = nullptr;
+    if (seg.nseg > 0) {  // the block's segment (block-uniform: segments are whole tiles)
+        const int n0 = blockIdx.y * 16 * WR;
+        const int sg = n0 >= seg.off[2] && seg.nseg > 2 ? 2 : n0 >= seg.off[1] && seg.nseg > 1 ? 1 : 0;
+        W = seg.w[sg];
+        Y = seg.y[sg];
+        Y16 = seg.y16[sg];
+        N = seg.off[sg + 1] - seg.off[sg];
+        nrow -= seg.off[sg];
+    }
     const bool nok = nrow < N;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * rowb;
     const int s0 = kg * NS;
@@ -774,24 +795,26 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
             const int m = m0 + 16 * h + 4 * kq + j;
             if (m < M) {
                 const float v = ldexpf(acc[h][j], -sShift[m - m0]);
-                Y[(size_t)m * N + nrow] = accumulate ? old[h][j] + v : v;
+                const float o = accumulate ? old[h][j] + v : v;
+                Y[(size_t)m * N + nrow] = o;
+                if (Y16) Y16[(size_t)m * N + nrow] = f32_to_f16(o);
             }
         }
 }
 
 template <int KK, int NWK, int WR, int MT>
 static void skinny_launch(const float* x, const uint8_t* w, float* y, int M, int N, size_t rowb, int accumulate,
-                          int mode, const SkPro& pro) {
+                          int mode, const SkPro& pro, const SkSeg& seg) {
     const dim3 grid(cdiv(M, MT), cdiv(N, 16 * WR)), blk(64 * WR * NWK);
     if (mode == SK_RMSNORM)
         hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_RMSNORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
-                           accumulate, pro);
+                           accumulate, pro, seg);
     else if (mode == SK_GATENORM)
         hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_GATENORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
-                           accumulate, pro);
+                           accumulate, pro, seg);
     else
         hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_PLAIN>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
-                           accumulate, pro);
+                           accumulate, pro, seg);
 }
 
 // Whether the skinny path takes a product of linear_any / linear_acc: Q4_K, K 256 / 512 / 1024,
@@ -805,7 +828,7 @@ bool skinny_takes(const void* x, const void* w, int M, int K, int kind) {
 // 16 weight rows, the first of these that reaches 256 blocks (or the smallest), with the
 // waves freed from weight rows splitting K instead. `mode` / `pro`: the row prologue.
 static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate,
-                       int* rc, int mode = SK_PLAIN, const SkPro& pro = SkPro{}) {
+                       int* rc, int mode = SK_PLAIN, const SkPro& pro = SkPro{}, const SkSeg* seg = nullptr) {
     if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
     const uint8_t* wb = (const uint8_t*)w;
     const int64_t b32 = (int64_t)cdiv(M, 32) * cdiv(N, 64), m16 = cdiv(M, 16);
@@ -815,12 +838,19 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
         for (int c = 1; c <= 3; ++c)
             if (m16 * cdiv(N, 64 >> (c - 1)) >= 256) { cfg = c; break; }
     }
+    SkSeg sg{};
+    if (seg) {  // segments must be whole tiles of the chosen weight-row count
+        const int rows = cfg <= 1 ? 64 : cfg == 2 ? 32 : 16;
+        for (int i = 0; i < seg->nseg; ++i)
+            if ((seg->off[i + 1] - seg->off[i]) % rows) return 0;
+        sg = *seg;
+    }
 #define GH_SKINNY(KK, NWK0)                                                                                     \
     switch (cfg) {                                                                                              \
-        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;             \
-        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;             \
-        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;         \
-        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro); break;        \
+        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;             \
+        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;             \
+        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;         \
+        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;        \
     }
     if (K == 256) { GH_SKINNY(256, 2) }
     else if (K == 512) { GH_SKINNY(512, 2) }
@@ -841,6 +871,29 @@ int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, con
     SkPro pro{nw, eps};
     int rc = GH_OK;
     if (!gemm_skinny(x, w, y, M, K, N, row_bytes(kind, K), accumulate, &rc, mode, pro)) return GH_EUNSUPPORTED;
+    return rc;
+}
+
+// q / k / v (up to three weight matrices of the same K over the same rows) in one skinny launch,
+// with the row prologue `mode` (SK_PLAIN / SK_RMSNORM) and optional fp16 copies of the outputs.
+// GH_EUNSUPPORTED, launching nothing, where the skinny path does not take it.
+int linear_multi_skinny(const float* x, int mode, const float* nw, float eps, int nseg, const void* const* w,
+                        float* const* y, uint16_t* const* y16, const int* n, int M, int K, int kind) {
+    if (nseg < 1 || nseg > 3 || (mode != SK_PLAIN && ((uintptr_t)nw & 15))) return GH_EUNSUPPORTED;
+    SkSeg sg{};
+    sg.nseg = nseg;
+    sg.off[0] = 0;
+    for (int i = 0; i < nseg; ++i) {
+        if (!skinny_takes(x, w[i], M, K, kind) || n[i] <= 0) return GH_EUNSUPPORTED;
+        sg.w[i] = (const uint8_t*)w[i];
+        sg.y[i] = y[i];
+        sg.y16[i] = y16 ? y16[i] : nullptr;
+        sg.off[i + 1] = sg.off[i] + n[i];
+    }
+    SkPro pro{nw, eps};
+    int rc = GH_OK;
+    if (!gemm_skinny(x, w[0], y[0], M, K, sg.off[nseg], row_bytes(kind, K), 0, &rc, mode, pro, &sg))
+        return GH_EUNSUPPORTED;
     return rc;
 }
 

@@ -43,6 +43,8 @@ int mamba_forward_impl(const float* x, const void* w_in, const float* conv_w, co
                        const float* pre_nw, float pre_eps);
 int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, const void* w, float* y, int M, int K,
                        int N, int kind, int accumulate);  // gemm.hip
+int linear_multi_skinny(const float* x, int mode, const float* nw, float eps, int nseg, const void* const* w,
+                        float* const* y, uint16_t* const* y16, const int* n, int M, int K, int kind);  // gemm.hip
 int linear_acc(const float* x, const void* w, float* y, int M, int K, int N, int kind);  // y += x W^T
 
 // decode control block (device ints)
@@ -868,11 +870,23 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
                 if (!acc) GHC(add_branch(g, g->pr, (int64_t)P * d));
             }
         } else {
-            GHC(proj_normed(g->W(pre + "wq"), g->q, g->qd));
-            GHC(proj_normed(g->W(pre + "wk"), g->k, g->kvd));
-            GHC(proj_normed(g->W(pre + "wv"), g->v, g->kvd));
-            GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
-            GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
+            // q, k, v in one launch with the norm as its row prologue and the fp16 KV-cache copies
+            // of k and v in its epilogue (the cache starts at position 0); else one by one
+            const void* wqkv[3] = {g->W(pre + "wq"), g->W(pre + "wk"), g->W(pre + "wv")};
+            float* yqkv[3] = {g->q, g->k, g->v};
+            uint16_t* y16[3] = {nullptr, g->kc[l], g->vc[l]};
+            const int nqkv[3] = {g->qd, g->kvd, g->kvd};
+            const int rc = linear_multi_skinny(g->x, 1, g->F(pre + "attn_norm"), g->eps, 3, wqkv, yqkv, y16, nqkv, P, d,
+                                               g->qkind);
+            if (rc != GH_EUNSUPPORTED) {
+                GHC(rc);
+            } else {
+                GHC(proj_normed(wqkv[0], g->q, g->qd));
+                GHC(proj_normed(wqkv[1], g->k, g->kvd));
+                GHC(proj_normed(wqkv[2], g->v, g->kvd));
+                GHC(launch_f32_to_f16(g->k, g->kc[l], (int64_t)P * g->kvd));
+                GHC(launch_f32_to_f16(g->v, g->vc[l], (int64_t)P * g->kvd));
+            }
             GHC(attention_prefill(g->q, g->k, g->v, g->att, 1, P, g->H, g->KV, g->hd, g->scale, 0));
             if (acc) {
                 GHC(linear_acc(g->att, g->W(pre + "wo"), g->x, P, g->qd, d, g->qkind));  // x += attn W_o^T
