@@ -911,8 +911,14 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
     const int32_t zero = 0;
     GH_HIP(hipMemcpyAsync(g->ctl + CTL_STEP, &zero, 4, hipMemcpyHostToDevice, stream()));
     g->host_len = P;
-    GHC(gh_rmsnorm_forward(g->x + (size_t)(P - 1) * d, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
-    GHC(lm_head(g, g->xb));
+    // final norm of the last row + lm head: one launch (k_head_argmax without the pick) where it
+    // fits and the logits are unscaled, else the norm and the head GEMV
+    if (g->logits_scaling != 1.0f ||
+        !launch_head_argmax(g->x + (size_t)(P - 1) * d, g->F("final_norm"), g->eps,
+                            (const uint16_t*)g->W(g->head_name()), g->logits, d, g->V, g->ctl, nullptr, 0, false)) {
+        GHC(gh_rmsnorm_forward(g->x + (size_t)(P - 1) * d, g->F("final_norm"), g->xb, nullptr, 1, d, g->eps));
+        GHC(lm_head(g, g->xb));
+    }
     if (logits_host) {
         GH_HIP(hipMemcpyAsync(logits_host, g->logits, (size_t)g->V * 4, hipMemcpyDeviceToHost, stream()));
     }
