@@ -614,6 +614,30 @@ struct SkSeg {
     int off[4];
     int nseg;
 };
+// Q8_0 B operand of the skinny GEMM: codes 8 kq .. 8 kq + 7 of a 34-byte block as fp16 q d,
+// rounded once (the reference's quant_materialize weight). w[0]: the dword holding the scale
+// at byte offset so; w[1..3]: the dwords holding the codes from byte offset co. A code becomes
+// the exact fp16 integer 1024 + (q + 128) (0x6400 | byte), minus 1152, times the scale.
+__device__ __forceinline__ sk_f16x8 sk_q8_bfrag(const uint32_t* w, int so, int co, bool ok) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t c0 = __builtin_amdgcn_alignbyte(w[2], w[1], co), c1 = __builtin_amdgcn_alignbyte(w[3], w[2], co);
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)((w[0] >> (8 * so)) & 0xFFFF));
+    const h2 d2 = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t u[2] = {c0 ^ 0x80808080u, c1 ^ 0x80808080u};
+    sk_f16x8 bv;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u[i], 0x04010400u)) - off;
+        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u[i], 0x04030402u)) - off;
+        const h2 a = lo * d2, b = hi * d2;
+        bv[4 * i] = ok ? a[0] : (_Float16)0.f;
+        bv[4 * i + 1] = ok ? a[1] : (_Float16)0.f;
+        bv[4 * i + 2] = ok ? b[0] : (_Float16)0.f;
+        bv[4 * i + 3] = ok ? b[1] : (_Float16)0.f;
+    }
+    return bv;
+}
+
 template <int PRO>
 __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
     if constexpr (PRO == SK_RMSNORM) {
@@ -624,7 +648,7 @@ __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
     }
 }
 
-// Small M (prefill of a short prompt), Q4_K, K = 256, 512 or 1024: a block takes MT (16 or
+// Small M (prefill of a short prompt), Q4_K or Q8_0, K = 256, 512 or 1024: a block takes MT (16 or
 // 32) rows of x (fp32, converted to fp16 while staged into LDS) and 16*WR weight rows over
 // the WHOLE K: each lane requests every Q4_K byte of its MFMA B operands before the first
 // multiply (one memory wait per block instead of one per K step, and no split-K partials in
@@ -632,7 +656,7 @@ __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
 // (v_mfma_f32_16x16x32_f16, activations as A in MT/16 16-row halves). The tile is chosen per
 // shape so that a launch spreads over the CUs (a short prompt has few 32x64 tiles). Each
 // output is written (or added, with `accumulate`) by exactly one lane.
-template <int KK, int NWK, int WR, int MT, int PRO = SK_PLAIN>
+template <int KK, int NWK, int WR, int MT, int PRO = SK_PLAIN, int KIND = 3>
 __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __restrict__ X, const uint8_t* __restrict__ W,
                                                                float* __restrict__ Y, int M, int N, size_t rowb,
                                                                int accumulate, SkPro pro, SkSeg seg) {
@@ -659,14 +683,29 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
     const bool nok = nrow < N;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * rowb;
     const int s0 = kg * NS;
-    // every weight byte of the lane, requested first (headers of the super-blocks it touches)
-    constexpr int NH = NS >= 8 ? NS / 8 : 1;
+    // every weight byte of the lane, requested first: Q4_K, the headers of the super-blocks it
+    // touches and 8 code bytes per k-step; Q8_0, per k-step (one 34-byte block) the dword holding
+    // the block's scale and the three dwords holding codes 8 kq .. 8 kq + 7 (2-byte aligned)
+    constexpr int NH = KIND == 3 ? (NS >= 8 ? NS / 8 : 1) : 1;
     uint4 hdr[NH];
-    uint2 qb[NS];
+    uint2 qb[KIND == 3 ? NS : 1];
+    uint32_t q8w[KIND == 2 ? NS : 1][4];
+    if constexpr (KIND == 3) {
 #pragma unroll
-    for (int b = 0; b < NH; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)((s0 >> 3) + b) * 144);
+        for (int b = 0; b < NH; ++b) hdr[b] = *(const uint4*)(wrow + (size_t)((s0 >> 3) + b) * 144);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
+        for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int ob = 34 * (s0 + s), oc = ob + 2 + 8 * kq;
+            const uint32_t* cw = (const uint32_t*)(wrow + (oc & ~3));
+            q8w[s][0] = *(const uint32_t*)(wrow + (ob & ~3));
+            q8w[s][1] = cw[0];
+            q8w[s][2] = cw[1];
+            q8w[s][3] = cw[2];
+        }
+    }
     // MT rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as
     // k_to_f16_rows does (the row maxima first, one wave per row). With a row prologue the
     // staged values are the normalised rows.
@@ -751,7 +790,13 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
         const int sg = s0 + s;
-        const sk_f16x8 bv = sk_q4k_bfrag(hdr[NS >= 8 ? s >> 3 : 0], qb[s], sg & 7, nok);
+        sk_f16x8 bv;
+        if constexpr (KIND == 3) {
+            bv = sk_q4k_bfrag(hdr[NS >= 8 ? s >> 3 : 0], qb[s], sg & 7, nok);
+        } else {
+            const int ob = 34 * sg, oc = ob + 2 + 8 * kq;
+            bv = sk_q8_bfrag(q8w[s], ob & 3, oc & 3, nok);
+        }
 #pragma unroll
         for (int h = 0; h < NH2; ++h) {
             const sk_f16x8 av = *(const sk_f16x8*)(sA + (16 * h + col) * SA + 32 * sg + 8 * kq);
@@ -802,34 +847,35 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
         }
 }
 
-template <int KK, int NWK, int WR, int MT>
+template <int KK, int NWK, int WR, int MT, int KIND>
 static void skinny_launch(const float* x, const uint8_t* w, float* y, int M, int N, size_t rowb, int accumulate,
                           int mode, const SkPro& pro, const SkSeg& seg) {
     const dim3 grid(cdiv(M, MT), cdiv(N, 16 * WR)), blk(64 * WR * NWK);
     if (mode == SK_RMSNORM)
-        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_RMSNORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_RMSNORM, KIND>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
                            accumulate, pro, seg);
     else if (mode == SK_GATENORM)
-        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_GATENORM>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_GATENORM, KIND>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
                            accumulate, pro, seg);
     else
-        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_PLAIN>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
+        hipLaunchKernelGGL((k_gemm_skinny<KK, NWK, WR, MT, SK_PLAIN, KIND>), grid, blk, 0, stream(), x, w, y, M, N, rowb,
                            accumulate, pro, seg);
 }
 
 // Whether the skinny path takes a product of linear_any / linear_acc: Q4_K, K 256 / 512 / 1024,
 // 8 < M <= 256 rows (smaller M go to the GEMVs), 16-byte aligned x and W.
 bool skinny_takes(const void* x, const void* w, int M, int K, int kind) {
-    return kind == 3 && M > 8 && M <= 256 && (K == 256 || K == 512 || K == 1024) && !(((uintptr_t)x | (uintptr_t)w) & 15);
+    return (kind == 3 || kind == 2) && M > 8 && M <= 256 && (K == 256 || K == 512 || K == 1024) && !(((uintptr_t)x | (uintptr_t)w) & 15);
 }
 
-// Returns 1 if the skinny path took the product (Q4_K, K 256 / 512 / 1024, M <= 256). The
+// Returns 1 if the skinny path took the product (Q4_K / Q8_0, K 256 / 512 / 1024, M <= 256). The
 // 32x64 tile when it already gives a CU-filling grid; otherwise 16-row tiles over 64, 32 or
 // 16 weight rows, the first of these that reaches 256 blocks (or the smallest), with the
 // waves freed from weight rows splitting K instead. `mode` / `pro`: the row prologue.
 static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, int N, size_t rowb, int accumulate,
-                       int* rc, int mode = SK_PLAIN, const SkPro& pro = SkPro{}, const SkSeg* seg = nullptr) {
-    if (M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
+                       int* rc, int mode = SK_PLAIN, const SkPro& pro = SkPro{}, const SkSeg* seg = nullptr,
+                       int kind = 3) {
+    if ((kind != 3 && kind != 2) || M > 256 || (K != 256 && K != 512 && K != 1024) || (((uintptr_t)x | (uintptr_t)w) & 15)) return 0;
     const uint8_t* wb = (const uint8_t*)w;
     const int64_t b32 = (int64_t)cdiv(M, 32) * cdiv(N, 64), m16 = cdiv(M, 16);
     int cfg = 0;  // 0: 32x64, 1: 16x64, 2: 16x32, 3: 16x16
@@ -845,17 +891,21 @@ static int gemm_skinny(const float* x, const void* w, float* y, int M, int K, in
             if ((seg->off[i + 1] - seg->off[i]) % rows) return 0;
         sg = *seg;
     }
-#define GH_SKINNY(KK, NWK0)                                                                                     \
-    switch (cfg) {                                                                                              \
-        case 0: skinny_launch<KK, NWK0, 4, 32>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;             \
-        case 1: skinny_launch<KK, NWK0, 4, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;             \
-        case 2: skinny_launch<KK, 2 * NWK0, 2, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;         \
-        default: skinny_launch<KK, 4 * NWK0, 1, 16>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;        \
+#define GH_SKINNY_K(KK, NWK0, KD)                                                                                \
+    switch (cfg) {                                                                                               \
+        case 0: skinny_launch<KK, NWK0, 4, 32, KD>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;      \
+        case 1: skinny_launch<KK, NWK0, 4, 16, KD>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;      \
+        case 2: skinny_launch<KK, 2 * NWK0, 2, 16, KD>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break;  \
+        default: skinny_launch<KK, 4 * NWK0, 1, 16, KD>(x, wb, y, M, N, rowb, accumulate, mode, pro, sg); break; \
     }
+#define GH_SKINNY(KK, NWK0)                         \
+    if (kind == 3) { GH_SKINNY_K(KK, NWK0, 3) }     \
+    else { GH_SKINNY_K(KK, NWK0, 2) }
     if (K == 256) { GH_SKINNY(256, 2) }
     else if (K == 512) { GH_SKINNY(512, 2) }
     else { GH_SKINNY(1024, 4) }
 #undef GH_SKINNY
+#undef GH_SKINNY_K
     GH_LAUNCHED("k_gemm_skinny");
     *rc = GH_OK;
     return 1;
@@ -870,7 +920,8 @@ int linear_norm_skinny(const float* x, int mode, const float* nw, float eps, con
     if (!skinny_takes(x, w, M, K, kind) || ((uintptr_t)nw & 15)) return GH_EUNSUPPORTED;
     SkPro pro{nw, eps};
     int rc = GH_OK;
-    if (!gemm_skinny(x, w, y, M, K, N, row_bytes(kind, K), accumulate, &rc, mode, pro)) return GH_EUNSUPPORTED;
+    if (!gemm_skinny(x, w, y, M, K, N, row_bytes(kind, K), accumulate, &rc, mode, pro, nullptr, kind))
+        return GH_EUNSUPPORTED;
     return rc;
 }
 
@@ -892,7 +943,7 @@ int linear_multi_skinny(const float* x, int mode, const float* nw, float eps, in
     }
     SkPro pro{nw, eps};
     int rc = GH_OK;
-    if (!gemm_skinny(x, w[0], y[0], M, K, sg.off[nseg], row_bytes(kind, K), 0, &rc, mode, pro, &sg))
+    if (!gemm_skinny(x, w[0], y[0], M, K, sg.off[nseg], row_bytes(kind, K), 0, &rc, mode, pro, &sg, kind))
         return GH_EUNSUPPORTED;
     return rc;
 }
@@ -984,7 +1035,11 @@ int gemm_dispatch(const float* x, const void* w, float* y, int M, int K, int N, 
     const dim3 g(blocks), b(256);
     if ((kind == 2 || kind == 3 || kind == 4) && K % 4 == 0) {
         switch (kind) {
-            case 2: return gemm2_launch<2>(x, w, y, M, K, N, rowb, accumulate);
+            case 2: {
+                int rc = GH_OK;
+                if (gemm_skinny(x, w, y, M, K, N, rowb, accumulate, &rc, SK_PLAIN, SkPro{}, nullptr, 2)) return rc;
+                return gemm2_launch<2>(x, w, y, M, K, N, rowb, accumulate);
+            }
             case 3: {
                 int rc = GH_OK;
                 if (gemm_skinny(x, w, y, M, K, N, rowb, accumulate, &rc)) return rc;

@@ -83,14 +83,14 @@ def test_moe_c5_decode_vs_exact(gh, kind):
     assert exact.errs(r_out, y)[1] > 4 * g_elem
 
 
+@pytest.mark.parametrize("kind", [2, 3])
 @pytest.mark.parametrize("M", [64, 2048])
 @pytest.mark.parametrize("K", [512, 4096])
-def test_prefill_gemm_activation_range(gh, M, K):
+def test_prefill_gemm_activation_range(gh, M, K, kind):
     """M > 8 (skinny GEMM at K=512 with M=64, the 256x256-tile / split-K GEMMs otherwise):
     rows of activations scaled by 1e-6 .. 1e5 (beyond fp16's range at both ends), each row
     within the fp16-operand tolerance 2e-2 of the exact product, normwise per row."""
     N = 384
-    kind = 3
     w = O.quantize(kind, O.rng_normal(41, N * K, 0, 0.02))
     x = O.rng_normal(42, M * K).reshape(M, K)
     scales = 10.0 ** np.linspace(-6, 5, M)
