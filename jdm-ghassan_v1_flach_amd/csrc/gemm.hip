@@ -614,30 +614,6 @@ struct SkSeg {
     int off[4];
     int nseg;
 };
-// Q8_0 B operand of the skinny GEMM: codes 8 kq .. 8 kq + 7 of a 34-byte block as fp16 q d,
-// rounded once (the reference's quant_materialize weight). w[0]: the dword holding the scale
-// at byte offset so; w[1..3]: the dwords holding the codes from byte offset co. A code becomes
-// the exact fp16 integer 1024 + (q + 128) (0x6400 | byte), minus 1152, times the scale.
-__device__ __forceinline__ sk_f16x8 sk_q8_bfrag(const uint32_t* w, int so, int co, bool ok) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const uint32_t c0 = __builtin_amdgcn_alignbyte(w[2], w[1], co), c1 = __builtin_amdgcn_alignbyte(w[3], w[2], co);
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)((w[0] >> (8 * so)) & 0xFFFF));
-    const h2 d2 = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const uint32_t u[2] = {c0 ^ 0x80808080u, c1 ^ 0x80808080u};
-    sk_f16x8 bv;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u[i], 0x04010400u)) - off;
-        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u[i], 0x04030402u)) - off;
-        const h2 a = lo * d2, b = hi * d2;
-        bv[4 * i] = ok ? a[0] : (_Float16)0.f;
-        bv[4 * i + 1] = ok ? a[1] : (_Float16)0.f;
-        bv[4 * i + 2] = ok ? b[0] : (_Float16)0.f;
-        bv[4 * i + 3] = ok ? b[1] : (_Float16)0.f;
-    }
-    return bv;
-}
-
 template <int PRO>
 __device__ __forceinline__ float sk_inv(double ss, int n, float eps) {
     if constexpr (PRO == SK_RMSNORM) {

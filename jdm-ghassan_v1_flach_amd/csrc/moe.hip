@@ -1047,7 +1047,7 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 // Skinny grouped GEMM (Q4_K, K = 256 or 512): tiles of 32 grouped rows x 64 weight
 // rows (DUAL: 32 gate + the matching 32 up rows, i.e. 32 outputs), the WHOLE K in
 // one pass: the block's 32 activation rows (fp16) go to LDS once, and each lane
-// requests every Q4_K byte its MFMA B operands need (8 values per k-step of 32,
+// requests every weight byte its MFMA B operands need (8 values per k-step of 32,
 // plus the super-block headers) before the first multiply, so a block waits for
 // memory once instead of once per K step (the 128-row tiles of k_moe_group_gemm2
 // spent ~2 us per K step on a group of ~32 rows). Wave w owns weight rows
@@ -1055,11 +1055,12 @@ __global__ void __launch_bounds__(256, 2) k_moe_group_gemm2(GroupGemm P) {
 // (two 16-row halves) and the lane's dequantised weights as B (lane: weight row
 // l % 16, values 8 (l / 16) .. +7 of the k-step, one sub-block of one super-block).
 // Weights are rounded to fp16 after dequantisation (d sc q - dmin m in fp32),
-// as in the 128-row kernel.
+// as in the 128-row kernel. KIND 2 (Q8_0): per k-step one 34-byte block, the lane's
+// 8 codes and the block scale read as dwords (gemm_tile.h sk_q8_bfrag), q d rounded once.
 typedef sk_f16x8 f16x8s;
 typedef float f32x4s __attribute__((ext_vector_type(4)));
-template <bool DUAL, int KK, int WR>
-__global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm P1, int ntiles0) {
+template <bool DUAL, int KK, int WR, int KIND = 3>
+__global__ void __launch_bounds__(512) k_moe_skinny(GroupGemm P0, GroupGemm P1, int ntiles0) {
     // blocks [0, ntiles0) take problem P0, the rest problem P1 (the shared expert beside the
     // routed ones in one launch)
     const bool second = (int)blockIdx.x >= ntiles0;
@@ -1093,11 +1094,26 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
     const uint8_t* W = (DUAL && wr >= 2 ? P.W1 : P.W0) + (size_t)g * P.gstride;
     const uint8_t* wrow = W + (size_t)(nok ? nrow : 0) * P.rowb;
     const int s0 = kg * NS;
-    // every weight byte of the lane, requested first
-    uint4 hdr = *(const uint4*)(wrow + (size_t)(s0 >> 3) * 144);
-    uint2 qb[NS];
+    // every weight byte of the lane, requested first (Q4_K: the super-block header and 8 code
+    // bytes per k-step; Q8_0: per k-step the dwords holding the block scale and codes 8 kq ..)
+    uint4 hdr;
+    uint2 qb[KIND == 3 ? NS : 1];
+    uint32_t q8w[KIND == 2 ? NS : 1][4];
+    if constexpr (KIND == 3) {
+        hdr = *(const uint4*)(wrow + (size_t)(s0 >> 3) * 144);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
+        for (int s = 0; s < NS; ++s) qb[s] = *(const uint2*)(wrow + sk_q4k_qofs(s0 + s, kq));
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int ob = 34 * (s0 + s), oc = ob + 2 + 8 * kq;
+            const uint32_t* cw = (const uint32_t*)(wrow + (oc & ~3));
+            q8w[s][0] = *(const uint32_t*)(wrow + (ob & ~3));
+            q8w[s][1] = cw[0];
+            q8w[s][2] = cw[1];
+            q8w[s][3] = cw[2];
+        }
+    }
     // combine epilogue: the rows' slot positions and weights (up to top-2 here), requested now
     constexpr int CKM = 2;
     int cp[2][4][CKM];
@@ -1142,7 +1158,13 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
     for (int h = 0; h < 2; ++h) acc[h] = f32x4s{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        const f16x8s bv = sk_q4k_bfrag(hdr, qb[s], (s0 + s) & 7, nok);
+        f16x8s bv;
+        if constexpr (KIND == 3) {
+            bv = sk_q4k_bfrag(hdr, qb[s], (s0 + s) & 7, nok);
+        } else {
+            const int ob = 34 * (s0 + s), oc = ob + 2 + 8 * kq;
+            bv = sk_q8_bfrag(q8w[s], ob & 3, oc & 3, nok);
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const f16x8s av = *(const f16x8s*)(sA + (16 * h + (lane & 15)) * SA + 32 * (s0 + s) + 8 * kq);
@@ -1245,32 +1267,32 @@ __global__ void __launch_bounds__(512) k_moe_skinny_q4k(GroupGemm P0, GroupGemm 
 // 16 WR). P1 (optional, ntiles1 blocks) runs in the same launch after P0's ntiles0; both take
 // the same K. A plain product takes 64, 32 or 16 weight rows per block: the first that gives
 // 256 blocks, or 16.
-template <int KK, int WR, bool DUAL>
+template <int KK, int WR, bool DUAL, int KIND>
 static void skinny_go(dim3 grid, const GroupGemm& P0, const GroupGemm& Q1, int ntiles0) {
-    hipLaunchKernelGGL((k_moe_skinny_q4k<DUAL, KK, WR>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
+    hipLaunchKernelGGL((k_moe_skinny<DUAL, KK, WR, KIND>), grid, dim3(512), 0, stream(), P0, Q1, ntiles0);
 }
-template <bool DUAL>
+template <bool DUAL, int KIND>
 static void launch_skinny(const GroupGemm& P0, int ntiles0, const GroupGemm* P1 = nullptr, int ntiles1 = 0) {
     const int nw = std::max(P0.N, P1 ? P1->N : 0);
     const GroupGemm Q1 = P1 ? *P1 : GroupGemm{};
     const int nt = ntiles0 + ntiles1;
     if constexpr (DUAL) {
         const dim3 grid(nt, cdiv(nw, 32));
-        if (P0.K == 256) skinny_go<256, 4, true>(grid, P0, Q1, ntiles0);
-        else skinny_go<512, 4, true>(grid, P0, Q1, ntiles0);
+        if (P0.K == 256) skinny_go<256, 4, true, KIND>(grid, P0, Q1, ntiles0);
+        else skinny_go<512, 4, true, KIND>(grid, P0, Q1, ntiles0);
     } else {
         int wr = 1;
         for (int c = 4; c >= 2; c >>= 1)
             if ((int64_t)nt * cdiv(nw, 16 * c) >= 256) { wr = c; break; }
         const dim3 grid(nt, cdiv(nw, 16 * wr));
         if (P0.K == 256) {
-            if (wr == 4) skinny_go<256, 4, false>(grid, P0, Q1, ntiles0);
-            else if (wr == 2) skinny_go<256, 2, false>(grid, P0, Q1, ntiles0);
-            else skinny_go<256, 1, false>(grid, P0, Q1, ntiles0);
+            if (wr == 4) skinny_go<256, 4, false, KIND>(grid, P0, Q1, ntiles0);
+            else if (wr == 2) skinny_go<256, 2, false, KIND>(grid, P0, Q1, ntiles0);
+            else skinny_go<256, 1, false, KIND>(grid, P0, Q1, ntiles0);
         } else {
-            if (wr == 4) skinny_go<512, 4, false>(grid, P0, Q1, ntiles0);
-            else if (wr == 2) skinny_go<512, 2, false>(grid, P0, Q1, ntiles0);
-            else skinny_go<512, 1, false>(grid, P0, Q1, ntiles0);
+            if (wr == 4) skinny_go<512, 4, false, KIND>(grid, P0, Q1, ntiles0);
+            else if (wr == 2) skinny_go<512, 2, false, KIND>(grid, P0, Q1, ntiles0);
+            else skinny_go<512, 1, false, KIND>(grid, P0, Q1, ntiles0);
         }
     }
 }
@@ -1366,7 +1388,7 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
     // prefill: permutation, grouped gate/up GEMM, grouped down GEMM, combine. Small groups
     // (a few dozen rows per expert) take the skinny 32-row tiles with the whole K in one pass.
     auto kfits = [](int k) { return k == 256 || k == 512; };
-    const bool skinny = KIND == 3 && (size_t)S <= (size_t)64 * ne && kfits(d) && kfits(E) && (!has_sh || kfits(SH));
+    const bool skinny = (KIND == 3 || KIND == 2) && (size_t)S <= (size_t)64 * ne && kfits(d) && kfits(E) && (!has_sh || kfits(SH));
     const int bm = skinny ? 32 : BM;
     int32_t* perm = (int32_t*)workspace(WS_MOE_XG, ((size_t)2 * S + ne + 1 + 1 + 2 * ((size_t)S / bm + ne + 1)) * 4);
     if (!perm) return fail(GH_ENOMEM, "moe: workspace");
@@ -1403,10 +1425,10 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
             R.A = x; R.lda = d; R.topk = 1; R.rows = N;
             R.W0 = (const uint8_t*)sh_g; R.W1 = (const uint8_t*)sh_u; R.rowb = rowb_d; R.K = d; R.N = SH;
             R.out16 = sh_act16;
-            launch_skinny<true>(P, max_tiles, has_sh ? &R : nullptr, has_sh ? cdiv(N, 32) : 0);
-            GH_LAUNCHED("k_moe_skinny_q4k(gate/up)");
-            launch_skinny<false>(Q, max_tiles);
-            GH_LAUNCHED("k_moe_skinny_q4k(down)");
+            launch_skinny<true, KIND>(P, max_tiles, has_sh ? &R : nullptr, has_sh ? cdiv(N, 32) : 0);
+            GH_LAUNCHED("k_moe_skinny(gate/up)");
+            launch_skinny<false, KIND>(Q, max_tiles);
+            GH_LAUNCHED("k_moe_skinny(down)");
             if (has_sh) {
                 float* cdst = out;
                 int cacc = 0;
@@ -1415,8 +1437,8 @@ static int moe_kind(const float* x, const float* w_route, const int32_t* idx, co
                 U.A16 = sh_act16; U.lda = SH; U.topk = 1; U.rows = N;
                 U.W0 = (const uint8_t*)sh_d; U.rowb = rowb_SH; U.K = SH; U.N = d;
                 U.cy = yr; U.cpos = pos; U.cw = w_route; U.cK = K; U.caccum = cacc; U.cout = cdst;
-                launch_skinny<false>(U, cdiv(N, 32));
-                GH_LAUNCHED("k_moe_skinny_q4k(shared down + combine)");
+                launch_skinny<false, KIND>(U, cdiv(N, 32));
+                GH_LAUNCHED("k_moe_skinny(shared down + combine)");
                 return GH_OK;
             }
         } else {

@@ -97,14 +97,15 @@ def test_moe_c5_prefill(gh, kind, skew):
     assert close(out, r_out, 2e-2)
 
 
+@pytest.mark.parametrize("kind", [2, 3])
 @pytest.mark.parametrize("N,d,E,ne,K,SH", [(128, 512, 256, 8, 2, 512), (45, 512, 512, 8, 2, 256),
                                            (7, 256, 256, 4, 1, 512)])
-def test_moe_prefill_small_groups(gh, N, d, E, ne, K, SH):
-    """The skinny grouped path (Q4_K, a few dozen rows per expert, K of 256 or 512; c1's
-    MoE shape first): ids bit-exact, output against the oracle."""
-    case = make_case(N, d, E, ne, K, SH, 3, 610, False)
-    out, probs, idx, w = MoE(gh, *case, N, d, E, ne, K, SH, 3).run()
-    r_out, r_idx, r_w = oracle_moe(case, N, d, E, ne, K, SH, 3)
+def test_moe_prefill_small_groups(gh, N, d, E, ne, K, SH, kind):
+    """The skinny grouped path (Q4_K / Q8_0, a few dozen rows per expert, K of 256 or 512;
+    c1's MoE shape first): ids bit-exact, output against the oracle."""
+    case = make_case(N, d, E, ne, K, SH, kind, 610, False)
+    out, probs, idx, w = MoE(gh, *case, N, d, E, ne, K, SH, kind).run()
+    r_out, r_idx, r_w = oracle_moe(case, N, d, E, ne, K, SH, kind)
     assert np.array_equal(idx, r_idx)
     assert close(out, r_out, 2e-2)
 
