@@ -234,6 +234,15 @@ __global__ void __launch_bounds__(256) k_head_argmax(const float* __restrict__ x
     }
 }
 
+// After a prefill of P tokens: cache length P, ring start 0, decode step 0.
+__global__ void k_ctl_prefilled(int32_t* ctl, int P) {
+    if (threadIdx.x == 0) {
+        ctl[CTL_LEN] = P;
+        ctl[CTL_START] = 0;
+        ctl[CTL_STEP] = 0;
+    }
+}
+
 // Returns 1 if launched (fp16 table, d a multiple of 8 up to 2048, 16-byte aligned rows).
 static int launch_head_argmax(const float* x, const float* nw, float eps, const uint16_t* tab, float* logits, int d,
                               int V, int32_t* ctl, int32_t* ids, int cap, bool argmax) {
@@ -301,6 +310,8 @@ struct gh_granite {
     // An aborted persistent launch leaves the recurrent state, the KV cache and the generated
     // ids partly advanced: the model refuses every call that reads that state until a reset.
     bool state_invalid = false;
+    int32_t* ids_pin = nullptr;  // pinned host staging of a prompt's ids (an asynchronous H2D copy)
+    int ids_pin_cap = 0;
     bool pd_force_abort = false;  // test hook: the next persistent launch starts aborted
 
     const void* W(const std::string& n) const {
@@ -331,6 +342,7 @@ static void free_all(gh_granite* g) {
     }
     if (g->pd_dev) (void)hipFree(g->pd_dev);
     if (g->pd_buf) (void)hipFree(g->pd_buf);
+    if (g->ids_pin) (void)hipHostFree(g->ids_pin);
     void* ptrs[] = {g->wbuf, g->state_buf, g->x, g->ids, g->ctl, g->gen_ids};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -833,7 +845,17 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
     GH_REQUIRE(P <= 1024 && P < g->max_ctx, "granite_prefill: %d tokens (batched prefill takes <= 1024 and < ctx)", P);
     const int d = g->d;
     GHC(ensure_acts(g, P));
-    GH_HIP(hipMemcpyAsync(g->ids, ids_host, (size_t)P * 4, hipMemcpyHostToDevice, stream()));
+    // the ids through pinned host memory: a DMA the host does not wait for (the staging buffer is
+    // reused only after this call's closing synchronisation)
+    if (g->ids_pin_cap < P) {
+        if (g->ids_pin) GH_HIP(hipHostFree(g->ids_pin));
+        g->ids_pin = nullptr;
+        g->ids_pin_cap = 0;
+        GH_HIP(hipHostMalloc((void**)&g->ids_pin, (size_t)1024 * 4, hipHostMallocDefault));
+        g->ids_pin_cap = 1024;
+    }
+    memcpy(g->ids_pin, ids_host, (size_t)P * 4);
+    GH_HIP(hipMemcpyAsync(g->ids, g->ids_pin, (size_t)P * 4, hipMemcpyHostToDevice, stream()));
     GHC(gh_embedding_forward_half(g->ids, (const uint16_t*)g->W("tok_embeddings"), g->x, P, d, g->V));
     if (g->emb_mult != 1.0f) GHC(gh_scale_inplace(g->x, g->emb_mult, (int64_t)P * d));
     // with a residual multiplier every branch lands in pr first and is scaled there
@@ -905,11 +927,9 @@ int gh_granite_prefill(gh_granite* g, const int32_t* ids_host, int P, float* log
                             g->ne, g->K, g->SH, g->qkind, g->F(pre + "ffn_norm"), g->eps, g->xb));
         if (!added) GHC(add_branch(g, g->pr, (int64_t)P * d));
     }
-    // cache length P, ring start 0 (KVCache::set_length)
-    const int32_t lenstart[2] = {P, 0};
-    GH_HIP(hipMemcpyAsync(g->ctl + CTL_LEN, lenstart, 8, hipMemcpyHostToDevice, stream()));
-    const int32_t zero = 0;
-    GH_HIP(hipMemcpyAsync(g->ctl + CTL_STEP, &zero, 4, hipMemcpyHostToDevice, stream()));
+    // cache length P, ring start 0 (KVCache::set_length), decode step 0: one small launch
+    hipLaunchKernelGGL(k_ctl_prefilled, dim3(1), dim3(64), 0, stream(), g->ctl, P);
+    GH_LAUNCHED("k_ctl_prefilled");
     g->host_len = P;
     // final norm of the last row + lm head: one launch (k_head_argmax without the pick) where it
     // fits and the logits are unscaled, else the norm and the head GEMV
