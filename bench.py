@@ -157,6 +157,7 @@ def kernel_suite(gh):
                 kern = ("k_gemv_q4k_i8" if (kind == 3 and M == 1 and K <= 4096) else
                         "k_gemv_q4k_i8 (4 K slices) + k_g8_sum" if (kind == 3 and M == 1) else
                         "k_gemv_q4k_i8<Q8> (2 / 7 K slices) + k_g8_sum" if M == 1 else
+                        g8 + " (2 K slices) + k_g8_sum" if (2 <= M <= 8 and K == 4096 and kind == 3) else
                         g8 if (2 <= M <= 8 and K <= 4096) else
                         g8 + " (4 K slices) + k_g8_sum" if 2 <= M <= 8 else "k_gemv_mfma")
                 res[tag] = entry(kern, ms, bytes_=w.nbytes + x.nbytes + M * N * 4, flops=2.0 * M * N * K)

@@ -313,9 +313,11 @@ int gemv8_dispatch(const float* x, const void* w, float* y, int M, int K, int N,
     if ((kind != 3 && kind != 2) || M < 2 || M > 8 || K % 256 != 0 || (((uintptr_t)x) & 15)) return 0;
     if (kind == 2 && ((uintptr_t)w & 15)) return 0;
     const int nsb = K / 256;
-    // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands and two tiles of
-    // weight bytes stay in registers)
-    for (int S = 1; S <= 8; ++S) {
+    // waves of SBW super-blocks, at most 8 waves (two per SIMD: the A operands stay in registers)
+    // Q4_K rows of 16 super-blocks or more start at two slices: each block then converts half of
+    // the activations (the launch's fixed part), worth the extra sum launch (c2 M=8 17.0 -> 16.2 us;
+    // for Q8_0 it is not: 18.2 -> 19.0)
+    for (int S = (kind == 3 && nsb >= 16) ? 2 : 1; S <= 8; ++S) {
         if (nsb % S) continue;
         const int ns = nsb / S;
         if (ns <= 8) {
