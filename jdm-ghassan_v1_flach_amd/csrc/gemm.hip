@@ -679,7 +679,9 @@ __global__ void __launch_bounds__(64 * WR * NWK) k_gemm_skinny(const float* __re
             q8w[s][0] = *(const uint32_t*)(wrow + (ob & ~3));
             q8w[s][1] = cw[0];
             q8w[s][2] = cw[1];
-            q8w[s][3] = cw[2];
+            // the third dword only when the codes start mid-dword: otherwise it lies past the
+            // block (for a row's last block, past the row and possibly past the allocation)
+            q8w[s][3] = (oc & 3) ? cw[2] : 0u;
         }
     }
     // MT rows x KK fp32 -> fp16 LDS (8 values per piece), each row scaled by 2^s_r as

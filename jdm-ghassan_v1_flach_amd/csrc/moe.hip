@@ -1111,7 +1111,9 @@ __global__ void __launch_bounds__(512) k_moe_skinny(GroupGemm P0, GroupGemm P1, 
             q8w[s][0] = *(const uint32_t*)(wrow + (ob & ~3));
             q8w[s][1] = cw[0];
             q8w[s][2] = cw[1];
-            q8w[s][3] = cw[2];
+            // the third dword only when the codes start mid-dword: otherwise it lies past the
+            // block (for a row's last block, past the row and possibly past the allocation)
+            q8w[s][3] = (oc & 3) ? cw[2] : 0u;
         }
     }
     // combine epilogue: the rows' slot positions and weights (up to top-2 here), requested now
